@@ -1,0 +1,208 @@
+/*
+ * sisa_hip.h -- C ABI of the MI355X (gfx950) SISA hot-path library libsisa_hip.so.
+ *
+ * Every entry point takes one argument struct and a hipStream_t (passed as void*), launches its kernels on that
+ * stream, never allocates device memory and never synchronises the host. The caller owns every buffer (inputs,
+ * outputs and workspaces). Return value: SISA_OK or an error code; sisa_last_error() gives the message of the last
+ * failing call on the calling thread.
+ *
+ * Conventions
+ *   - (B,H,L,.) views: pointer + element strides (sb, sh, sl) of the batch, head and sequence axes; the last axis is
+ *     contiguous. (B,H,L) views: pointer + (sb, sh, sl).
+ *   - d_head = 64, d_state = 32 (the shapes the reference's kernels are written for, src/sisa/config.py:15-16).
+ *   - Attention element types: SISA_BF16, SISA_F16, SISA_F32. g, F, lambda, lse, factors: fp32.
+ *   - lse is stored in log2 units (max(s)*log2(e) + log2(sum)), as the reference's kernels do
+ *     (src/sisa/kernels/attention.py:296).
+ *   - Deterministic: no atomics; results are bitwise reproducible for a given shape.
+ *
+ * Each declaration names the reference interface it replaces (path:line in tlstngud/sisa).
+ */
+#ifndef SISA_HIP_H
+#define SISA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SISA_ABI_VERSION 1
+
+enum sisa_dtype { SISA_F32 = 0, SISA_BF16 = 1, SISA_F16 = 2, SISA_F64 = 3 };
+
+enum sisa_status {
+    SISA_OK = 0,
+    SISA_ERR_INVALID = 1,      /* bad argument (shape, stride, null pointer, dtype) */
+    SISA_ERR_UNSUPPORTED = 2,  /* valid but not implemented for this configuration */
+    SISA_ERR_LAUNCH = 3        /* a HIP launch failed */
+};
+
+/* A (B,H,L,.) tensor view with a contiguous last axis, or a (B,H,L) view. Strides are in elements. */
+typedef struct {
+    void* ptr;
+    int64_t sb, sh, sl;
+} sisa_view;
+
+/* ------------------------------------------------------------------------------------------------ attention */
+
+/* rowf/colf decay factors over 64-row blocks and the per-block maximum increase of g (monotonicity check).
+ * Replaces `_factors` (src/sisa/kernels/attention.py:129-153), launched at attention.py:709. */
+typedef struct {
+    int32_t B, H, L;
+    sisa_view g;         /* (B,H,L) fp32 */
+    float* rowf;         /* (B,H,L) contiguous */
+    float* colf;         /* (B,H,L) contiguous */
+    float* mono;         /* (B*H*ceil(L/64)) */
+} sisa_factors_args;
+
+/* Forward attention: o, lse and (optionally) the self-normalised fp32 o'' used by the exact-delta backward.
+ * Replaces `_fwd` (src/sisa/kernels/attention.py:177-296) and the host core `attn_forward` (attention.py:686-727).
+ * rowf/colf must come from sisa_factors or sisa_prep_fwd (64-row blocks). */
+typedef struct {
+    int32_t B, H, L;
+    int32_t dtype;             /* of q, k, v, c, b, o */
+    sisa_view q, k, v;         /* (B,H,L,64) */
+    sisa_view c, b;            /* (B,H,L,32) rotated C~, B~ */
+    sisa_view g;               /* (B,H,L) fp32 cumulative log-decay */
+    sisa_view f;               /* (B,H,L) fp32 cumulative log-sigmoid forget gate; ptr NULL = no forget term */
+    const float* lam;          /* (H,) fp32 */
+    int64_t s_lam;
+    const float* rowf;         /* (B,H,L) contiguous */
+    const float* colf;         /* (B,H,L) contiguous */
+    sisa_view o;               /* (B,H,L,64) output, dtype */
+    float* lse;                /* (B,H,L) contiguous output, log2 units */
+    float* o32;                /* (B,H,L,64) contiguous fp32 output or NULL (bf16/fp16 only) */
+} sisa_attn_fwd_args;
+
+/* Workspace (bytes) of sisa_attn_bwd: six (B,H,L) fp32 row buffers. */
+int64_t sisa_attn_bwd_workspace_bytes(int32_t B, int32_t H, int32_t L);
+
+/* Exact-delta backward: dq, dk, dv, dc, db, dg, dF and dlambda.
+ * Replaces `_bwd_dq` (src/sisa/kernels/attention.py:300-491), `_bwd_dkv` (attention.py:495-663), the fp64 dlambda
+ * reduction (attention.py:781-783) and the host core `attn_backward` (attention.py:730-784). */
+typedef struct {
+    int32_t B, H, L;
+    int32_t dtype;             /* of q, k, v, c, b, o, do, dq, dk, dv */
+    int32_t dcb_dtype;         /* of dc, db: dtype or SISA_F32 */
+    sisa_view q, k, v, c, b, g, f;
+    const float* lam;
+    int64_t s_lam;
+    const float* rowf;
+    const float* colf;
+    sisa_view o;               /* forward output (dtype) */
+    const float* o32;          /* (B,H,L,64) contiguous fp32 o'' or NULL (then delta = o.do) */
+    const float* lse;          /* (B,H,L) contiguous */
+    sisa_view dout;            /* (B,H,L,64) upstream gradient (dtype) */
+    sisa_view dq, dk, dv;      /* outputs (dtype), any strides with contiguous last axis */
+    sisa_view dc, db;          /* outputs (dcb_dtype) */
+    float* dg;                 /* (B,H,L) contiguous output */
+    float* df;                 /* (B,H,L) contiguous output, NULL when f.ptr is NULL */
+    float* dlam;               /* (H,) output */
+    void* workspace;           /* sisa_attn_bwd_workspace_bytes(B,H,L) bytes */
+} sisa_attn_bwd_args;
+
+int sisa_factors(const sisa_factors_args* a, void* stream);
+int sisa_attn_fwd(const sisa_attn_fwd_args* a, void* stream);
+int sisa_attn_bwd(const sisa_attn_bwd_args* a, void* stream);
+
+/* ------------------------------------------------------------------------------------------------ fused prep */
+
+/* proj column layout (src/sisa/kernels/fused_prep.py:71-96): [Q H*64 | K H*64 | V H*64 | B H*32 | C H*32 |
+ * theta H*16 | alpha H | zero pad to NPAD = ceil(273H/16)*16]. */
+
+/* Forward prep: g = cumsum(-softplus(alpha)), F = cumsum(logsigmoid(z)), Phi = cumsum(theta), C~ = R(Phi)C,
+ * B~ = R(Phi)B, rowf/colf, and the per-64-row block totals TOT (B*H, ceil(L/64), 18).
+ * Replaces `_prep_sums` + `_prep_fwd` (src/sisa/kernels/fused_prep.py:247-352), host `_launch_prep_forward`
+ * (fused_prep.py:527-564). q and k are not copied (they are read as strided views of proj). */
+typedef struct {
+    int32_t B, L, H;
+    int32_t dtype;             /* of proj, cr, br: SISA_BF16 or SISA_F16 */
+    const void* proj;          /* (B,L,NPAD) */
+    int64_t s_pb, s_pl;
+    const float* z;            /* (B,L,H) fp32, contiguous last axis, or NULL (no forget gate) */
+    int64_t s_zb, s_zl;
+    void* cr;                  /* (B,L,H,32) contiguous, dtype */
+    void* br;                  /* (B,L,H,32) contiguous, dtype */
+    float* g;                  /* (B,H,L) contiguous */
+    float* f;                  /* (B,H,L) contiguous, ignored when z is NULL */
+    float* rowf;               /* (B,H,L) contiguous */
+    float* colf;               /* (B,H,L) contiguous */
+    float* tot;                /* (B*H, ceil(L/64), 18) contiguous block totals */
+} sisa_prep_fwd_args;
+
+/* Workspace (bytes) of sisa_prep_bwd: fp64 block totals (B*H, ceil(L/64), 18). */
+int64_t sisa_prep_bwd_workspace_bytes(int32_t B, int32_t L, int32_t H);
+
+/* Backward prep: reverse scans (fp64) for d alpha, dz, d theta; inverse rotation of dC~/dB~; zero pad columns.
+ * Replaces `_prep_bsums` + `_prep_bwd` (src/sisa/kernels/fused_prep.py:385-494). The Q/K/V columns of dproj are
+ * written by sisa_attn_bwd (views); this call writes the B, C, theta, alpha and pad columns. */
+typedef struct {
+    int32_t B, L, H;
+    int32_t dtype;             /* of proj and dproj */
+    const void* proj;
+    int64_t s_pb, s_pl;
+    const float* z;            /* or NULL */
+    int64_t s_zb, s_zl;
+    const float* tot;          /* from sisa_prep_fwd */
+    const float* dg;           /* (B,H,L) contiguous */
+    const float* df;           /* (B,H,L) contiguous or NULL */
+    const float* dcr;          /* (B,L,H,32) contiguous fp32 */
+    const float* dbr;          /* (B,L,H,32) contiguous fp32 */
+    void* dproj;               /* (B,L,NPAD) dtype */
+    int64_t s_db, s_dl;
+    float* dz;                 /* (B,L,H) fp32 or NULL */
+    int64_t s_dzb, s_dzl;
+    void* workspace;           /* sisa_prep_bwd_workspace_bytes(B,L,H) bytes */
+} sisa_prep_bwd_args;
+
+int sisa_prep_fwd(const sisa_prep_fwd_args* a, void* stream);
+int sisa_prep_bwd(const sisa_prep_bwd_args* a, void* stream);
+
+/* ------------------------------------------------------------------------------------------------ linear CE */
+
+/* Chunked linear + cross-entropy, one token chunk. logits = x W^T are never stored: the first call computes the
+ * per-row log-sum-exp and loss row; the second recomputes each logits tile and accumulates dx = G W (token-owned)
+ * and writes G = (softmax - onehot) * scale for the dW GEMM.
+ * Replaces the chunk loop of `_LinearCrossEntropyFn.forward` (src/sisa/kernels/linear_ce.py:167-191) and
+ * `_lmce_row_kernel` (linear_ce.py:60-96). */
+typedef struct {
+    int32_t N;                 /* rows in this chunk */
+    int32_t D;                 /* hidden size (multiple of 32) */
+    int32_t V;                 /* real vocabulary rows */
+    int32_t Vp;                /* padded rows of w (multiple of 128, rows >= V are zero) */
+    int32_t dtype;             /* of x and w: SISA_BF16 or SISA_F16 */
+    const void* x;             /* (N, D) contiguous */
+    const void* w;             /* (Vp, D) contiguous */
+    const int64_t* labels;     /* (N,) */
+    int64_t ignore_index;
+    float* lse;                /* (N,) output, natural log */
+    float* loss_rows;          /* (N,) output: lse - logit[label], 0 if ignored */
+} sisa_lmce_fwd_args;
+
+typedef struct {
+    int32_t N, D, V, Vp;
+    int32_t dtype;
+    const void* x;
+    const void* w;
+    const int64_t* labels;
+    int64_t ignore_index;
+    const float* lse;          /* from sisa_lmce_fwd */
+    const float* scale;        /* (1,) device scalar: 1/N_valid */
+    float gscale;              /* host multiplier (grad_scale promise or 1) */
+    float* dx;                 /* (N, D) fp32 output or NULL */
+    void* gbuf;                /* (N, Vp) dtype output G (for dW) or NULL */
+} sisa_lmce_bwd_args;
+
+int sisa_lmce_fwd(const sisa_lmce_fwd_args* a, void* stream);
+int sisa_lmce_bwd(const sisa_lmce_bwd_args* a, void* stream);
+
+/* ------------------------------------------------------------------------------------------------ misc */
+
+int sisa_abi_version(void);
+const char* sisa_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SISA_HIP_H */

@@ -1,0 +1,462 @@
+"""Plain-PyTorch restatement of the SISA hot path (reference: tlstngud/sisa 0.1.0) -- test infrastructure only.
+
+Pinning (each check lives in tests/test_oracle.py and is chosen so that a dropped term, a wrong sign or index or a
+transposed operand fails it):
+
+  dense_attention / truth64
+      * pure-Python scalar evaluation of the README formula (tests/golden/attn_tiny.json, written by
+        tests/golden/make_golden.py with the math module only, no torch)
+      * torch.autograd.gradcheck of dense_attention in fp64 (finite differences)
+      * special cases: lam = 0 and F = 0 is causal softmax attention (torch SDPA math path, fp64); L = 1 gives o = v;
+        c = 0 makes the output independent of lam; a constant shift of g or F changes nothing
+  analytic_grads64 (delta-free)   == fp64 autograd of dense_attention (two independent derivations)
+  attention_blocked               == dense_attention (block sizes 1, 7, 64)
+  fa_emulation                    fp32 inputs: == the unrounded emulation; fp64 mode == autograd
+  glue / prep64                   rotate_pairs == complex multiplication by exp(i Phi); g, F, Phi == scalar loops;
+                                  layout == NTOT 273H and NPAD {2192, 3280, 4368}
+  factors                         rowf_i * mid * colf_j == exp(g_i - g_j) (closed form, fp64)
+  lmce64                          == F.cross_entropy(fp64 logits); ignored rows get exactly zero gradient;
+                                  == pure-Python scalar loops on a tiny case (golden fixture)
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+D_HEAD, D_STATE = 64, 32
+U32 = 2.0 ** -24
+
+
+# ============================================================================================ layout / glue
+def layout(H: int) -> dict:
+    """Column layout of the fused projection (src/sisa/kernels/fused_prep.py:71-96)."""
+    o = {"Q": 0, "K": 64 * H, "V": 128 * H, "B": 192 * H, "C": 224 * H, "TH": 256 * H, "A": 272 * H}
+    o["NTOT"] = 273 * H
+    o["NPAD"] = -(-o["NTOT"] // 16) * 16
+    return o
+
+
+def rotate_pairs(z: torch.Tensor, phi: torch.Tensor) -> torch.Tensor:
+    """Interleaved-pair rotation (src/sisa/functional.py:38-48)."""
+    ze, zo = z[..., 0::2], z[..., 1::2]
+    cp, sp = torch.cos(phi), torch.sin(phi)
+    return torch.stack([ze * cp - zo * sp, ze * sp + zo * cp], dim=-1).flatten(-2)
+
+
+def glue(proj: torch.Tensor, z: torch.Tensor | None, H: int, dtype=torch.float64) -> dict:
+    """g, F, Phi and the rotated c, b from the fused projection (src/sisa/modeling.py:180-197,
+    tests/test_fused_prep.py:146-159). Computed in ``dtype`` from the stored values of ``proj`` and ``z``."""
+    B, L, _ = proj.shape
+    off = layout(H)
+    P = proj.to(dtype)
+
+    def cols(nm, w):
+        return P[..., off[nm]:off[nm] + H * w].view(B, L, H, w).transpose(1, 2)
+    alpha = P[..., off["A"]:off["A"] + H].transpose(1, 2)
+    theta = cols("TH", 16)
+    g = torch.cumsum(-F.softplus(alpha), 2)
+    Phi = torch.cumsum(theta, 2)
+    c = rotate_pairs(cols("C", 32), Phi)
+    b = rotate_pairs(cols("B", 32), Phi)
+    Fg = None if z is None else torch.cumsum(F.logsigmoid(z.to(dtype)).transpose(1, 2), 2)
+    return dict(q=cols("Q", 64), k=cols("K", 64), v=cols("V", 64), c=c, b=b, g=g, F=Fg, Phi=Phi)
+
+
+def factors(g: torch.Tensor, T: int = 64) -> tuple[torch.Tensor, torch.Tensor]:
+    """rowf_t = exp(min(g_t - g_{block start}, 0)), colf_t = exp(min(g_{block end} - g_t, 0)) over T-row blocks
+    (src/sisa/kernels/attention.py:129-153; block end clamped to L-1)."""
+    L = g.shape[-1]
+    idx = torch.arange(L)
+    start = (idx // T) * T
+    end = torch.clamp(start + T - 1, max=L - 1)
+    rowf = torch.exp(torch.clamp(g - g[..., start], max=0))
+    colf = torch.exp(torch.clamp(g[..., end] - g, max=0))
+    return rowf, colf
+
+
+# ============================================================================================ attention
+def scores(q, k, c, b, g, Fg, lam, r0, r1):
+    """Logits of query rows r0:r1 against keys 0:r1, masked to -inf (tests/test_attention_kernel.py:158-172)."""
+    sc = 1.0 / math.sqrt(q.shape[-1])
+    s = torch.matmul(q[:, :, r0:r1], k[:, :, :r1].transpose(-1, -2)) * sc
+    i = torch.arange(r0, r1, device=q.device)[:, None]
+    j = torch.arange(0, r1, device=q.device)[None, :]
+    mask = i >= j
+    dg = g[:, :, r0:r1, None] - g[:, :, None, :r1]
+    E = torch.exp(torch.where(mask, dg, torch.full((), -math.inf, dtype=dg.dtype, device=dg.device)))
+    cb = torch.matmul(c[:, :, r0:r1], b[:, :, :r1].transpose(-1, -2))
+    s = s + lam.view(1, -1, 1, 1) * E * cb
+    if Fg is not None:
+        s = s + (Fg[:, :, r0:r1, None] - Fg[:, :, None, :r1])
+    return s.masked_fill(~mask, -math.inf), E, cb, mask
+
+
+def dense_attention(q, k, v, c, b, g, lam, Fg=None):
+    """o = softmax(s) v, unblocked (README.md:33-72; src/sisa/functional.py:69-103). Any d_head, any d_state."""
+    L = q.shape[2]
+    s, _, _, _ = scores(q, k, c, b, g, Fg, lam, 0, L)
+    return torch.matmul(torch.softmax(s, -1), v)
+
+
+IN_NAMES = ["q", "k", "v", "c", "b", "g", "lam", "F"]
+GRAD_NAMES = ["dq", "dk", "dv", "dc", "db", "dg", "dlam", "dF"]
+
+
+def _rows_per_block(B, H, L, budget=4.0e8):
+    return int(max(8, min(1024, budget // max(1, B * H * max(L, 1) * 8 * 24))))
+
+
+def truth64(ins: dict, rb: int | None = None) -> dict:
+    """fp64 dense evaluation with autograd on the given (possibly low-precision) inputs lifted exactly to fp64, in row
+    blocks (tests/test_attention_kernel.py:194-212). Works on any device. Returns o and every input gradient."""
+    X = {n: (ins[n].detach().double().requires_grad_(True) if ins[n] is not None else None) for n in IN_NAMES}
+    q, k, v, c, b, g, lam, Fg = [X[n] for n in IN_NAMES]
+    B, H, L, D = q.shape
+    dO = ins["do"].double()
+    rb = rb or _rows_per_block(B, H, L)
+    o = torch.empty(B, H, L, D, dtype=torch.float64, device=q.device)
+    for r0 in range(0, L, rb):
+        r1 = min(L, r0 + rb)
+        s, _, _, _ = scores(q, k, c, b, g, Fg, lam, r0, r1)
+        ob = torch.matmul(torch.softmax(s, -1), v[:, :, :r1])
+        ob.backward(dO[:, :, r0:r1])
+        o[:, :, r0:r1] = ob.detach()
+    out = {"o": o}
+    for n, gn in zip(IN_NAMES, GRAD_NAMES):
+        if X[n] is not None:
+            out[gn] = X[n].grad if X[n].grad is not None else torch.zeros_like(X[n])
+    return out
+
+
+def analytic_grads64(q, k, v, c, b, g, lam, Fg, do):
+    """Delta-free analytic fp64 gradients of one (b, h) (tests/test_attention_diag.py:68-100): 2-D fp64 inputs,
+    scalar lam. dS_tj = P_tj (dP_tj - T_t) for j < t; dS_tt = P_tt * sum_{j<t} P_tj (dP_tt - dP_tj)."""
+    L, D = q.shape
+    sc = 1.0 / math.sqrt(D)
+    i = torch.arange(L, device=q.device)
+    mask = i[:, None] >= i[None, :]
+    strict = i[:, None] > i[None, :]
+    ninf = torch.full((), -math.inf, dtype=torch.float64, device=q.device)
+    zero = torch.zeros((), dtype=torch.float64, device=q.device)
+    E = torch.exp(torch.where(mask, g[:, None] - g[None, :], ninf))
+    CB = c @ b.T
+    U = E * CB
+    s = (q @ k.T) * sc + lam * U
+    if Fg is not None:
+        s = s + (Fg[:, None] - Fg[None, :])
+    P = torch.softmax(torch.where(mask, s, ninf), -1)
+    dP = do @ v.T
+    T = (P * dP).sum(1)
+    dS = torch.where(strict, P * (dP - T[:, None]), zero)
+    Ptt, dPtt = torch.diagonal(P), torch.diagonal(dP)
+    dSd = Ptt * torch.where(strict, P * (dPtt[:, None] - dP), zero).sum(1)
+    dSf = dS + torch.diag(dSd)
+    dSE = dSf * E
+    dSU = dS * U
+    out = dict(o=P @ v, dq=(dSf @ k) * sc, dk=(dSf.T @ q) * sc, dv=P.T @ do, dc=lam * (dSE @ b),
+               db=lam * (dSE.T @ c), dg=lam * (dSU.sum(1) - dSU.sum(0)), dlam=(dSf * U).sum())
+    out["dF"] = (dS.sum(1) - dS.sum(0)) if Fg is not None else None
+    return out
+
+
+def fa_emulation(ins: dict, mode: str = "fa", rb: int | None = None) -> dict:
+    """Dense emulations on the same inputs (tests/test_attention_kernel.py:235-360, without the error magnitudes).
+
+    mode 'fa': the unavoidable rounding points of a standard FlashAttention-2 pipeline in the input dtype DT (P~ and
+    dS rounded to DT for the MMAs, o stored in DT, delta = o_DT . do, outputs in DT); 'ideal': no intermediate rounding;
+    'exact64': fp64 without rounding (checks the hand-written backward against autograd)."""
+    cdt = torch.float64 if mode == "exact64" else torch.float32
+    dt = ins["q"].dtype
+    low = mode == "fa" and dt != torch.float32
+    R = (lambda x: x.to(dt).to(cdt)) if low else (lambda x: x)
+
+    def RO(x, odt):
+        return x if mode == "exact64" else x.to(odt).to(cdt)
+    q, k, v, c, b = [ins[n].to(cdt) for n in "qkvcb"]
+    g, lam = ins["g"].to(cdt), ins["lam"].to(cdt)
+    Fg = ins["F"].to(cdt) if ins["F"] is not None else None
+    dO = ins["do"].to(cdt)
+    B, H, L, D = q.shape
+    S = c.shape[-1]
+    sc = 1.0 / math.sqrt(D)
+    rb = rb or _rows_per_block(B, H, L)
+    dev = q.device
+    o = torch.empty(B, H, L, D, dtype=cdt, device=dev)
+    lse = torch.empty(B, H, L, dtype=cdt, device=dev)
+    for r0 in range(0, L, rb):
+        r1 = min(L, r0 + rb)
+        s, E, cb, mask = scores(q, k, c, b, g, Fg, lam, r0, r1)
+        m = s.amax(-1, keepdim=True)
+        Ph = torch.exp(s - m)
+        lsum = Ph.sum(-1, keepdim=True)
+        o[:, :, r0:r1] = torch.matmul(R(Ph), v[:, :, :r1]) / lsum
+        lse[:, :, r0:r1] = (m + torch.log(lsum)).squeeze(-1)
+    o_out = RO(o, dt)
+    Delta = ((o_out if mode == "fa" else o) * dO).sum(-1)
+
+    def z(*s_):
+        return torch.zeros(*s_, dtype=cdt, device=dev)
+    dq, dk, dv = z(B, H, L, D), z(B, H, L, D), z(B, H, L, D)
+    dc, db = z(B, H, L, S), z(B, H, L, S)
+    dg, dF, dlam = z(B, H, L), z(B, H, L), z(H)
+    lamv = lam.view(1, H, 1, 1)
+    for r0 in range(0, L, rb):
+        r1 = min(L, r0 + rb)
+        s, E, cb, mask = scores(q, k, c, b, g, Fg, lam, r0, r1)
+        P = torch.exp(s - lse[:, :, r0:r1, None])
+        dP = torch.matmul(dO[:, :, r0:r1], v[:, :, :r1].transpose(-1, -2))
+        dS = P * (dP - Delta[:, :, r0:r1, None])
+        dv[:, :, :r1] += torch.matmul(R(P).transpose(-1, -2), dO[:, :, r0:r1])
+        dq[:, :, r0:r1] = torch.matmul(R(dS), k[:, :, :r1]) * sc
+        dk[:, :, :r1] += torch.matmul(R(dS).transpose(-1, -2), q[:, :, r0:r1]) * sc
+        W = dS * lamv * E
+        dc[:, :, r0:r1] = torch.matmul(R(W), b[:, :, :r1])
+        db[:, :, :r1] += torch.matmul(R(W).transpose(-1, -2), c[:, :, r0:r1])
+        Tm = dS * E * cb
+        dg[:, :, r0:r1] += lam.view(1, H, 1) * Tm.sum(-1)
+        dg[:, :, :r1] -= lam.view(1, H, 1) * Tm.sum(-2)
+        dlam += Tm.sum(dim=(0, 2, 3))
+        dF[:, :, r0:r1] += dS.sum(-1)
+        dF[:, :, :r1] -= dS.sum(-2)
+    out = dict(o=o_out, dq=RO(dq, dt), dk=RO(dk, dt), dv=RO(dv, dt), dc=RO(dc, ins["c"].dtype),
+               db=RO(db, ins["b"].dtype), dg=RO(dg, torch.float32), dlam=RO(dlam, torch.float32))
+    if Fg is not None:
+        out["dF"] = RO(dF, torch.float32)
+    return out
+
+
+def attention_blocked(q, k, v, c, b, g, lam, Fg=None, block_q: int = 256):
+    """The reference's pure-PyTorch path (src/sisa/functional.py:106-155): inputs cast to fp32 (fp64 stays fp64),
+    query blocks of ``block_q`` rows against the keys up to the block end, each block checkpointed with gradients.
+    This is the timed CPU baseline of bench.py."""
+    from torch.utils.checkpoint import checkpoint
+    out_dtype = q.dtype
+    wd = torch.promote_types(q.dtype, torch.float32)
+    q, k, v, c, b, g, lam = (t.to(wd) for t in (q, k, v, c, b, g, lam))
+    Fg = None if Fg is None else Fg.to(wd)
+    L = q.shape[2]
+
+    def rows(qb, kb, vb, cb_, bb, gq, gk, fq, fk, start):
+        m, n = qb.shape[-2], kb.shape[-2]
+        pos_q = torch.arange(start, start + m)
+        causal = torch.arange(n)[None, :] <= pos_q[:, None]
+        s = torch.matmul(qb, kb.transpose(-1, -2)) / math.sqrt(qb.shape[-1])
+        delta = (gq[..., :, None] - gk[..., None, :]).masked_fill(~causal, 0.0)
+        s = s + lam.view(1, -1, 1, 1) * torch.exp(delta) * torch.matmul(cb_, bb.transpose(-1, -2))
+        if fq is not None:
+            s = s + (fq[..., :, None] - fk[..., None, :])
+        return torch.matmul(torch.softmax(s.masked_fill(~causal, float("-inf")), -1), vb)
+    need = torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, k, v, c, b, g, lam, Fg))
+    outs = []
+    for st in range(0, L, block_q):
+        en = min(st + block_q, L)
+        args = (q[:, :, st:en], k[:, :, :en], v[:, :, :en], c[:, :, st:en], b[:, :, :en], g[:, :, st:en],
+                g[:, :, :en], None if Fg is None else Fg[:, :, st:en], None if Fg is None else Fg[:, :, :en], st)
+        outs.append(checkpoint(rows, *args, use_reentrant=False) if need and L > block_q else rows(*args))
+    return torch.cat(outs, dim=2).to(out_dtype)
+
+
+# ============================================================================================ gates
+def rel(a: torch.Tensor, b: torch.Tensor) -> float:
+    """Norm-wise relative error ||a - b|| / ||b|| (fp64; 0-norm references use 1)."""
+    a, b = a.double(), b.double()
+    n = b.norm().item()
+    return (a - b).norm().item() / (n if n > 0 else 1.0)
+
+
+def ulp(x: torch.Tensor, dt: torch.dtype) -> torch.Tensor:
+    mant = {torch.bfloat16: 7, torch.float16: 10, torch.float32: 23, torch.float64: 52}[dt]
+    emin = {torch.bfloat16: -126, torch.float16: -14, torch.float32: -126, torch.float64: -1022}[dt]
+    e = torch.floor(torch.log2(x.abs().double().clamp_min(2.0 ** emin)))
+    return torch.pow(2.0, e - mant)
+
+
+# ============================================================================================ linear CE
+def lmce64(h: torch.Tensor, w: torch.Tensor, labels: torch.Tensor, g: float = 1.0, quant: bool = False,
+           ignore_index: int = -100, chunk: int = 1024):
+    """Chunked fp64 linear cross-entropy: (loss, dL/dh, dL/dW) for a backward seed g (tests/test_linear_ce.py:54-85).
+    ``quant`` rounds h and W to bf16 first (isolates the op's own rounding)."""
+    D = h.shape[-1]
+    x = h.reshape(-1, D)
+    W = w
+    if quant:
+        x, W = x.to(torch.bfloat16), W.to(torch.bfloat16)
+    x, W = x.double(), W.double()
+    y = labels.reshape(-1)
+    valid = y != ignore_index
+    n = valid.sum().double()
+    loss = torch.zeros((), dtype=torch.float64, device=h.device)
+    dx = torch.zeros_like(x)
+    dW = torch.zeros_like(W)
+    for s in range(0, x.shape[0], chunk):
+        e = min(x.shape[0], s + chunk)
+        lg = x[s:e] @ W.t()
+        lse = torch.logsumexp(lg, 1)
+        vc = valid[s:e]
+        ys = torch.where(vc, y[s:e], torch.zeros_like(y[s:e]))
+        tgt = lg.gather(1, ys[:, None])[:, 0]
+        loss += torch.where(vc, lse - tgt, torch.zeros_like(lse)).sum()
+        G = torch.exp(lg - lse[:, None])
+        G[torch.arange(e - s, device=h.device), ys] -= 1.0
+        G *= (vc.double() * (g / n))[:, None]
+        dx[s:e] = G @ W
+        dW += G.t() @ x[s:e]
+    return loss / n, dx.view(h.shape), dW
+
+
+# ============================================================================================ inputs
+G_KINDS = {"zero": None, "slow": (-7.0, 0.5), "model": (-2.5, 1.0), "med": (1.0, 1.0), "fast": (3.0, 1.0),
+           "extreme": "extreme"}
+F_KINDS = {"none": None, "fox": (4.0, 1.5), "model": (1.0, 1.5), "strong": (-3.0, 1.5), "veryneg": (-10.0, 1.0),
+           "extreme": "extreme", "walk": "walk"}
+TINY = 1e-7
+# 12 heads = lam {0, tiny, 0.31, 3} x F {none, fox, strong}; g cycles model/med/slow (tests/test_attention_kernel.py:96-108)
+MIX12 = [((0.0, TINY, 0.31, 3.0)[h % 4], ("model", "med", "slow")[(h + h // 4) % 3], ("none", "fox", "strong")[h // 4])
+         for h in range(12)]
+MIX4 = [(0.31, "model", "fox"), (3.0, "slow", "strong"), (0.0, "med", "none"), (TINY, "fast", "model")]
+
+
+def heads_for(H):
+    return MIX12 if H == 12 else (MIX4[:H] if H <= 4 else MIX12[:H])
+
+
+def _incs(kind, table, B, L, gen, idx, is_g, grid):
+    spec = table[kind]
+    if spec is None:
+        return torch.zeros(B, L)
+    u = torch.randn(B, L, generator=gen)[:, idx]
+    if spec == "extreme":
+        r = torch.rand(B, L, generator=gen)[:, idx]
+        inc = -(20000.0 / L) * (0.5 + r)
+    elif spec == "walk":
+        inc = 0.5 * u
+    else:
+        a, s = spec
+        inc = -F.softplus(a + s * u) if is_g else F.logsigmoid(a + s * u)
+    if grid:
+        inc = torch.round(inc * 256.0) / 256.0
+    return inc
+
+
+def make_attention_inputs(spec: dict, device="cpu") -> dict:
+    """Seeded adversarial inputs of the reference's attention judge (tests/test_attention_kernel.py:94-154), drawn
+    on the CPU generator and moved to ``device``."""
+    B, H, L = spec["B"], spec["H"], spec["L"]
+    dt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[spec["dtype"]]
+    gen = torch.Generator().manual_seed(int(spec.get("seed", 0)))
+    pat = spec.get("pattern", "random")
+    P = max(1, min({"random": L, "repeat7": 7, "const": 1}[pat], L))
+    idx = torch.arange(L) % P
+
+    def seq(d, scale):
+        return (torch.randn(B, H, P, d, generator=gen) * scale)[:, :, idx].contiguous()
+    qs, cbs = spec.get("qk_scale", 1.0), spec.get("cb_scale", 0.6)
+    q, k, v = seq(64, qs).to(dt), seq(64, qs).to(dt), seq(64, 1.0).to(dt)
+    c, b = seq(32, cbs).to(dt), seq(32, cbs).to(dt)
+    heads = spec.get("heads") or heads_for(H)
+    assert len(heads) == H
+    g = torch.zeros(B, H, L)
+    Fg = torch.zeros(B, H, L)
+    for h, (lm, gk, fk) in enumerate(heads):
+        g[:, h] = torch.cumsum(_incs(gk, G_KINDS, B, L, gen, idx, True, spec.get("grid")), -1)
+        Fg[:, h] = torch.cumsum(_incs(fk, F_KINDS, B, L, gen, idx, False, spec.get("grid")), -1)
+    g = (g + float(spec.get("shift_g", 0.0))).contiguous()
+    Fg = (Fg + float(spec.get("shift_F", 0.0))).contiguous()
+    lam = torch.tensor([h[0] for h in heads], dtype=torch.float32)
+    do = torch.randn(B, H, L, 64, generator=gen).to(dt)
+    out = dict(q=q, k=k, v=v, c=c, b=b, g=g, lam=lam, F=None if spec.get("fgate_none") else Fg, do=do)
+    return {n: (t.to(device) if t is not None else None) for n, t in out.items()}
+
+
+def make_proj(B, L, H, seed=0, dt=torch.bfloat16, alpha_mu=-3.0, alpha_sd=2.0, th_mu=0.02, th_sd=0.2, device="cpu"):
+    """Seeded fused projection + forget logits (tests/test_fused_prep.py:79-88)."""
+    gen = torch.Generator().manual_seed(seed)
+    off = layout(H)
+    P = torch.zeros(B, L, off["NPAD"])
+    P[..., :off["TH"]] = torch.randn(B, L, off["TH"], generator=gen)
+    P[..., off["B"]:off["TH"]] *= 0.6
+    P[..., off["TH"]:off["A"]] = th_mu + th_sd * torch.randn(B, L, H * 16, generator=gen)
+    P[..., off["A"]:off["NTOT"]] = alpha_mu + alpha_sd * torch.randn(B, L, H, generator=gen)
+    z = (4.0 + 1.5 * torch.randn(B, L, H, generator=gen)).contiguous()
+    return P.to(dt).contiguous().to(device), z.to(device), off
+
+
+def config_inputs(cfg: int, device="cpu", dtype=None) -> dict:
+    """Synthetic inputs of BASELINE.json's configs, drawn from ``torch.Generator().manual_seed(cfg)`` on the CPU.
+
+    cfg 0: B=1 T=256 H=4 fp32 unfused (q,k,v,B,C ~ N(0,1), theta ~ N(0,0.01^2) [B,T,H,16], a ~ N(-5,0.5^2),
+           z ~ N(4,0.5^2), lambda_raw = -1, upstream gradient ~ N(0,1)).
+    cfg 1: B=4 T=2048 H=8; cfg 'ns': B=4 T=4096 H=8 -- the same distributions as proj columns (bf16) and z (fp32).
+    cfg 2: B=1 T=16384 H=16, a ~ N(-7,1), z ~ N(4,1).
+    Returns dict(proj, z, lam_raw, dy, H) for the fused configs and the unfused tensors for cfg 0."""
+    shapes = {0: (1, 256, 4), 1: (4, 2048, 8), "ns": (4, 4096, 8), 2: (1, 16384, 16)}
+    B, L, H = shapes[cfg]
+    seed = {0: 0, 1: 1, "ns": 5, 2: 2}[cfg]
+    a_mu, a_sd, z_sd = (-7.0, 1.0, 1.0) if cfg == 2 else (-5.0, 0.5, 0.5)
+    gen = torch.Generator().manual_seed(seed)
+    lam_raw = torch.full((H,), -1.0)
+    if cfg == 0:
+        dt = dtype or torch.float32
+        q, k, v = (torch.randn(B, H, L, 64, generator=gen) for _ in range(3))
+        bm, cm = (torch.randn(B, H, L, 32, generator=gen) for _ in range(2))
+        theta = 0.01 * torch.randn(B, L, H, 16, generator=gen)
+        a = a_mu + a_sd * torch.randn(B, L, H, generator=gen)
+        z = 4.0 + z_sd * torch.randn(B, L, H, generator=gen)
+        dy = torch.randn(B, H, L, 64, generator=gen)
+        out = dict(q=q, k=k, v=v, b=bm, c=cm, theta=theta, a=a, z=z, lam_raw=lam_raw, dy=dy)
+        return {n: t.to(device=device, dtype=dt if t.is_floating_point() else t.dtype) for n, t in out.items()}
+    dt = dtype or torch.bfloat16
+    off = layout(H)
+    P = torch.zeros(B, L, off["NPAD"])
+    P[..., :off["TH"]] = torch.randn(B, L, off["TH"], generator=gen)
+    P[..., off["TH"]:off["A"]] = 0.01 * torch.randn(B, L, H * 16, generator=gen)
+    P[..., off["A"]:off["NTOT"]] = a_mu + a_sd * torch.randn(B, L, H, generator=gen)
+    z = 4.0 + z_sd * torch.randn(B, L, H, generator=gen)
+    dy = torch.randn(B, L, H * 64, generator=gen)
+    return dict(proj=P.to(dt).to(device), z=z.to(device), lam_raw=lam_raw.to(device), dy=dy.to(dt).to(device), H=H)
+
+
+def unfused_glue(inp: dict):
+    """Config-0 glue (src/sisa/modeling.py:185-197): Phi = cumsum theta, g = cumsum(-softplus a),
+    F = cumsum(logsigmoid z), c~/b~ = rotate_pairs(c/b, Phi), lam = softplus(lambda_raw)."""
+    phi = torch.cumsum(inp["theta"], 1).transpose(1, 2)
+    g = torch.cumsum(-F.softplus(inp["a"]), 1).transpose(1, 2)
+    Fg = torch.cumsum(F.logsigmoid(inp["z"]), 1).transpose(1, 2)
+    c = rotate_pairs(inp["c"], phi)
+    b = rotate_pairs(inp["b"], phi)
+    lam = F.softplus(inp["lam_raw"])
+    return c, b, g, Fg, lam
+
+
+# ============================================================================================ fused layer
+def fused64(proj, z, lam, H, fwdvals, dy):
+    """fp64 gradients of the fused layer function y(proj, z, lam) (tests/test_fused_prep.py:162-201). The forward
+    values q/k/c/b/g/F the candidate computed (``fwdvals``) are passed straight through (value = candidate's,
+    gradient = exact formula), so only kernel and backward-prep error is measured. Returns (y, dproj, dlam, dz)."""
+    B, L, _ = proj.shape
+    off = layout(H)
+    P = proj.detach().double().requires_grad_(True)
+    Z = None if z is None else z.detach().double().requires_grad_(True)
+    LAM = lam.detach().double().requires_grad_(True)
+
+    def cols(nm, w):
+        return P[..., off[nm]:off[nm] + H * w].view(B, L, H, w).transpose(1, 2)
+
+    def st(x, val):
+        return x + (val.double() - x).detach()
+    q = st(cols("Q", 64), fwdvals["q"])
+    k = st(cols("K", 64), fwdvals["k"])
+    v = cols("V", 64)
+    g = st(torch.cumsum(-F.softplus(P[..., off["A"]:off["A"] + H].transpose(1, 2)), 2), fwdvals["g"])
+    Phi = torch.cumsum(cols("TH", 16), 2)
+    cs = st(rotate_pairs(cols("C", 32), Phi), fwdvals["c"])
+    bs = st(rotate_pairs(cols("B", 32), Phi), fwdvals["b"])
+    Fg = None
+    if Z is not None:
+        Fg = st(torch.cumsum(F.logsigmoid(Z).transpose(1, 2), 2), fwdvals["F"])
+    o = dense_attention(q, k, v, cs, bs, g, LAM, Fg)
+    y = o.transpose(1, 2).reshape(B, L, H * 64)
+    gr = torch.autograd.grad(y, [P, LAM] + ([Z] if Z is not None else []), dy.double())
+    return y.detach(), gr[0], gr[1], (gr[2] if Z is not None else None)

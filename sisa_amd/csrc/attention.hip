@@ -1,0 +1,838 @@
+// SISA attention for gfx950: decay factors, forward, exact-delta backward (query-owned and key-owned kernels) and
+// the deterministic fp64 dlambda reduction.
+//
+//   s_ij = q_i.k_j / 8 + lam * exp(g_i - g_j) * (c_i.b_j) + (F_i - F_j)        (j <= i)
+//   o_i  = sum_j softmax_j(s_ij) v_j
+//
+// Reference: src/sisa/kernels/attention.py (Triton). The arithmetic follows the reference's numerics notes
+// (attention.py:9-78): chunk-factored decay exp(g_i-g_j) = rowf_i * mid * colf_j over 64-row blocks for key blocks
+// strictly before the query block, pairwise exp2(min((g_i-g_j)*log2e, 0)) inside the query's own block, differences
+// before log2e, the self-normalised fp32 o'' for the exact delta, and the delta-free diagonal dS_tt. The kernel
+// structure (tiles, wave ownership, MFMA layouts, LDS staging) is this library's own.
+//
+// Work decomposition (256 threads = 4 waves per workgroup):
+//   forward, dq kernel: a workgroup owns 128 consecutive queries, each wave 32 of them (two 16-query column groups);
+//     key tiles of 64 positions are staged in LDS. Scores are computed transposed (S^T = K Q^T) so that one lane owns
+//     one query's softmax state and the 16x16 C blocks of S^T are directly the B fragments of O^T += V^T P^T.
+//   dkv kernel: a workgroup owns 128 consecutive keys, each wave 32; query tiles of 64 positions are staged.
+//     Scores are computed as S = Q K^T so that one lane owns one key's column sums.
+//   Ownership is exclusive (no atomics): dq/dc by query tiles, dk/dv/db/dg/dF by key tiles.
+#include "common.h"
+#include "host.h"
+
+namespace {
+
+constexpr int DH = 64;   // d_head
+constexpr int DS = 32;   // d_state
+constexpr int BLK = 64;  // decay-factor block (rowf/colf anchors)
+
+struct Ptrs {
+    int64_t sb, sh, sl;
+};
+
+// ------------------------------------------------------------------------------------------------ factors
+// rowf_t = exp2(min((g_t - g_{block start})*log2e, 0)), colf_t = exp2(min((g_{block end} - g_t)*log2e, 0)), and the
+// maximum increase g_t - g_{t-1} per block. Reference: attention.py:129-153.
+__global__ __launch_bounds__(64) void factors_kernel(sisa_factors_args a) {
+    const int p = blockIdx.x;
+    const int bh = blockIdx.y;
+    const int H = a.H, L = a.L;
+    const int b = bh / H, h = bh % H;
+    const float* G = (const float*)a.g.ptr + (int64_t)b * a.g.sb + (int64_t)h * a.g.sh;
+    const int64_t sgl = a.g.sl;
+    const int t0 = p * BLK;
+    const int t = t0 + threadIdx.x;
+    const bool msk = t < L;
+    const int tc = t < L ? t : L - 1;
+    const float g = G[(int64_t)tc * sgl];
+    const float gs = G[(int64_t)t0 * sgl];
+    const int last = (t0 + BLK - 1 < L - 1) ? t0 + BLK - 1 : L - 1;
+    const float ge = G[(int64_t)last * sgl];
+    const float rowf = exp2_le0((g - gs) * LOG2E);
+    const float colf = exp2_le0((ge - g) * LOG2E);
+    if (msk) {
+        a.rowf[(int64_t)bh * L + t] = rowf;
+        a.colf[(int64_t)bh * L + t] = colf;
+    }
+    const int tp = tc - 1 > 0 ? tc - 1 : 0;
+    const float prv = G[(int64_t)tp * sgl];
+    float inc = (msk && t > 0) ? g - prv : -__builtin_inff();
+    // wave max (64 lanes)
+    for (int o = 32; o > 0; o >>= 1) inc = nmax(inc, __shfl_xor(inc, o));
+    if (threadIdx.x == 0) a.mono[(int64_t)bh * gridDim.x + p] = inc;
+}
+
+// ------------------------------------------------------------------------------------------------ forward
+template <class T>
+struct FwdLds {
+    T ks[64 * (DH + LDS_PAD)];   // K tile, row-major
+    T bs[64 * (DS + LDS_PAD)];   // B~ tile, row-major
+    T vt[DH * (64 + LDS_PAD)];   // V tile, transposed
+    float fk[64], cf[64], gk[64];
+};
+
+template <class T>
+__global__ __launch_bounds__(256) void attn_fwd_kernel(sisa_attn_fwd_args a, float scale) {
+    __shared__ FwdLds<T> sm;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, grp = lane >> 4, lc = lane & 15;
+    const int NQT = gridDim.x;
+    const int tile = NQT - 1 - (int)blockIdx.x;   // heavy (late) query tiles first
+    const int bh = blockIdx.y;
+    const int H = a.H, L = a.L;
+    const int b = bh / H, h = bh % H;
+    const bool has_f = a.f.ptr != nullptr;
+    const T* Q = (const T*)a.q.ptr + (int64_t)b * a.q.sb + (int64_t)h * a.q.sh;
+    const T* K = (const T*)a.k.ptr + (int64_t)b * a.k.sb + (int64_t)h * a.k.sh;
+    const T* V = (const T*)a.v.ptr + (int64_t)b * a.v.sb + (int64_t)h * a.v.sh;
+    const T* C = (const T*)a.c.ptr + (int64_t)b * a.c.sb + (int64_t)h * a.c.sh;
+    const T* Bm = (const T*)a.b.ptr + (int64_t)b * a.b.sb + (int64_t)h * a.b.sh;
+    const float* G = (const float*)a.g.ptr + (int64_t)b * a.g.sb + (int64_t)h * a.g.sh;
+    const float* FF = has_f ? (const float*)a.f.ptr + (int64_t)b * a.f.sb + (int64_t)h * a.f.sh : nullptr;
+    const float* ROWF = a.rowf + (int64_t)bh * L;
+    const float* COLF = a.colf + (int64_t)bh * L;
+    const float lam = a.lam[(int64_t)h * a.s_lam];
+    const int64_t sql = a.q.sl, skl = a.k.sl, svl = a.v.sl, scl = a.c.sl, sbl = a.b.sl, sgl = a.g.sl;
+    const int64_t sfl = has_f ? a.f.sl : 0;
+
+    const int q0 = tile * 128 + 32 * w;
+    const bool live = q0 < L;
+
+    frag8<T> qf[2][2], cfr[2];
+    float fq[2], rs[2], gq[2];
+#pragma unroll
+    for (int cq = 0; cq < 2; ++cq) {
+        const int qq = q0 + 16 * cq + lc;
+        const bool ok = qq < L;
+        const int qc = ok ? qq : L - 1;
+        qf[cq][0] = ok ? load8<T>(Q + (int64_t)qq * sql + 8 * grp) : zero8<T>();
+        qf[cq][1] = ok ? load8<T>(Q + (int64_t)qq * sql + 32 + 8 * grp) : zero8<T>();
+        cfr[cq] = ok ? load8<T>(C + (int64_t)qq * scl + 8 * grp) : zero8<T>();
+        fq[cq] = (has_f && ok) ? FF[(int64_t)qq * sfl] : 0.f;
+        rs[cq] = lam * (ok ? ROWF[qq] : 0.f);
+        gq[cq] = G[(int64_t)qc * sgl];
+    }
+    const float ga = live ? G[(int64_t)(q0 / BLK * BLK) * sgl] : 0.f;   // anchor of the wave's 64-block
+
+    float m[2] = {-__builtin_inff(), -__builtin_inff()};
+    float l[2] = {0.f, 0.f}, lb[2] = {0.f, 0.f};
+    f32x4 acc[2][4];
+#pragma unroll
+    for (int cq = 0; cq < 2; ++cq)
+#pragma unroll
+        for (int db = 0; db < 4; ++db) acc[cq][db] = zero4();
+
+    const int kend = (tile * 128 + 128 < L) ? tile * 128 + 128 : L;
+    for (int n0 = 0; n0 < kend; n0 += 64) {
+        __syncthreads();
+        const int nvalid = (L - n0 < 64) ? L - n0 : 64;
+        stage_tile<T, DH, true, false>(K + (int64_t)n0 * skl, skl, nvalid, sm.ks, nullptr, tid);
+        stage_tile<T, DS, true, false>(Bm + (int64_t)n0 * sbl, sbl, nvalid, sm.bs, nullptr, tid);
+        stage_tile<T, DH, false, true>(V + (int64_t)n0 * svl, svl, nvalid, nullptr, sm.vt, tid);
+        if (tid < 64) {
+            const int j = n0 + tid;
+            const int jc = j < L ? j : L - 1;
+            sm.fk[tid] = (has_f && j < L) ? FF[(int64_t)j * sfl] : 0.f;
+            sm.cf[tid] = j < L ? COLF[j] : 0.f;
+            sm.gk[tid] = G[(int64_t)jc * sgl];
+        }
+        __syncthreads();
+        if (!live || n0 > q0 + 31) continue;          // every key of the tile is after every query of the wave
+        const bool diag = n0 + 63 >= q0;              // the wave's own 64-block (pairwise decay + causal mask)
+        float mid = 0.f;
+        if (!diag) mid = exp2_le0((ga - G[(int64_t)(n0 + 63) * sgl]) * LOG2E);
+
+        f32x4 sc[4][2], cb[4][2];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const frag8<T> k0 = frag_rows<T, DH>(sm.ks, kb * 16, 0, lane);
+            const frag8<T> k1 = frag_rows<T, DH>(sm.ks, kb * 16, 1, lane);
+            const frag8<T> bf = frag_rows<T, DS>(sm.bs, kb * 16, 0, lane);
+#pragma unroll
+            for (int cq = 0; cq < 2; ++cq) {
+                sc[kb][cq] = mma(k1, qf[cq][1], mma(k0, qf[cq][0], zero4()));
+                cb[kb][cq] = mma(bf, cfr[cq], zero4());
+            }
+        }
+        // scores (natural-log units), row maxima
+        float mloc[2] = {-__builtin_inff(), -__builtin_inff()};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int j = kb * 16 + 4 * grp + i;
+                const float fk = sm.fk[j];
+                if (diag) {
+                    const int jj = n0 + j;
+                    const float gk = sm.gk[j];
+#pragma unroll
+                    for (int cq = 0; cq < 2; ++cq) {
+                        const int qq = q0 + 16 * cq + lc;
+                        const bool valid = jj <= qq && jj < L;
+                        const float dec = valid ? exp2_le0((gq[cq] - gk) * LOG2E) : 0.f;
+                        float s = sc[kb][cq][i] * scale + (fq[cq] - fk);
+                        s = s + lam * (dec * cb[kb][cq][i]);
+                        s = valid ? s : -__builtin_inff();
+                        sc[kb][cq][i] = s;
+                        mloc[cq] = nmax(mloc[cq], s);
+                    }
+                } else {
+                    const float cfm = sm.cf[j] * mid;
+#pragma unroll
+                    for (int cq = 0; cq < 2; ++cq) {
+                        float s = sc[kb][cq][i] * scale + (fq[cq] - fk);
+                        s = s + rs[cq] * (cb[kb][cq][i] * cfm);
+                        sc[kb][cq][i] = s;
+                        mloc[cq] = nmax(mloc[cq], s);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int cq = 0; cq < 2; ++cq) {
+            float mn = nmax(m[cq], group_max(mloc[cq]) * LOG2E);
+            const float mu = (mn == -__builtin_inff()) ? 0.f : mn;
+            const float corr = fast_exp2(m[cq] - mu);
+            m[cq] = mu;
+            l[cq] *= corr;
+            lb[cq] *= corr;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) acc[cq][db] *= corr;
+            float ls = 0.f;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float pe = fast_exp2(fmaf(sc[kb][cq][i], LOG2E, -mu));
+                    sc[kb][cq][i] = pe;
+                    ls += pe;
+                }
+            l[cq] += ls;
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                const frag8<T> pf = pack8<T>(sc[2 * st][cq], sc[2 * st + 1][cq]);
+                lb[cq] += frag_sum<T>(pf);
+#pragma unroll
+                for (int db = 0; db < 4; ++db) acc[cq][db] = mma(frag_trn<T>(sm.vt, db * 16, st, lane), pf, acc[cq][db]);
+            }
+        }
+    }
+    if (!live) return;
+    T* O = (T*)a.o.ptr + (int64_t)b * a.o.sb + (int64_t)h * a.o.sh;
+#pragma unroll
+    for (int cq = 0; cq < 2; ++cq) {
+        const float lt = group_sum(l[cq]);
+        const float lbt = group_sum(lb[cq]);
+        const int qq = q0 + 16 * cq + lc;
+        if (qq >= L) continue;
+        const float ls = (lt == 0.f) ? 1.f : lt;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const int d = db * 16 + 4 * grp;
+            store4<T>(O + (int64_t)qq * a.o.sl + d, to_vec4<T>(acc[cq][db] / ls));
+        }
+        if (a.o32) {
+            const float lbs = (lbt == 0.f) ? 1.f : lbt;
+            float* O32 = a.o32 + ((int64_t)bh * L + qq) * DH;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) *reinterpret_cast<f32x4*>(O32 + db * 16 + 4 * grp) = acc[cq][db] / lbs;
+        }
+        if (grp == 0) a.lse[(int64_t)bh * L + qq] = m[cq] + __builtin_amdgcn_logf(ls);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ backward: dq
+// Row buffers handed from the dq kernel to the dkv kernel (workspace, each (B,H,L) fp32).
+enum { WS_DELTA = 0, WS_DDEL, WS_DSD, WS_RG, WS_RL, WS_RF, WS_N };
+
+template <class T>
+struct DqLds {
+    T ks[64 * (DH + LDS_PAD)];   // K, row-major (scores)
+    T kt[DH * (64 + LDS_PAD)];   // K, transposed (dq)
+    T vs[64 * (DH + LDS_PAD)];   // V, row-major (dP)
+    T bs[64 * (DS + LDS_PAD)];   // B~, row-major (scores)
+    T bt[DS * (64 + LDS_PAD)];   // B~, transposed (dc)
+    float fk[64], cf[64], gk[64];
+};
+
+template <class T, class TO>
+SISA_DEV void store_row4(TO* p, f32x4 v) {
+    store4<TO>(p, to_vec4<TO>(v));
+}
+
+template <class T>
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(sisa_attn_bwd_args a, float scale) {
+    __shared__ DqLds<T> sm;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, grp = lane >> 4, lc = lane & 15;
+    const int NQT = gridDim.x;
+    const int tile = NQT - 1 - (int)blockIdx.x;
+    const int bh = blockIdx.y;
+    const int H = a.H, L = a.L;
+    const int b = bh / H, h = bh % H;
+    const bool has_f = a.f.ptr != nullptr;
+    const T* Q = (const T*)a.q.ptr + (int64_t)b * a.q.sb + (int64_t)h * a.q.sh;
+    const T* K = (const T*)a.k.ptr + (int64_t)b * a.k.sb + (int64_t)h * a.k.sh;
+    const T* V = (const T*)a.v.ptr + (int64_t)b * a.v.sb + (int64_t)h * a.v.sh;
+    const T* C = (const T*)a.c.ptr + (int64_t)b * a.c.sb + (int64_t)h * a.c.sh;
+    const T* Bm = (const T*)a.b.ptr + (int64_t)b * a.b.sb + (int64_t)h * a.b.sh;
+    const T* O = (const T*)a.o.ptr + (int64_t)b * a.o.sb + (int64_t)h * a.o.sh;
+    const T* DO = (const T*)a.dout.ptr + (int64_t)b * a.dout.sb + (int64_t)h * a.dout.sh;
+    const float* G = (const float*)a.g.ptr + (int64_t)b * a.g.sb + (int64_t)h * a.g.sh;
+    const float* FF = has_f ? (const float*)a.f.ptr + (int64_t)b * a.f.sb + (int64_t)h * a.f.sh : nullptr;
+    const float* ROWF = a.rowf + (int64_t)bh * L;
+    const float* COLF = a.colf + (int64_t)bh * L;
+    const float* LSE = a.lse + (int64_t)bh * L;
+    const float lam = a.lam[(int64_t)h * a.s_lam];
+    const int64_t skl = a.k.sl, svl = a.v.sl, sbl = a.b.sl, sgl = a.g.sl;
+    const int64_t sfl = has_f ? a.f.sl : 0;
+    const int64_t BHL = (int64_t)a.B * H * L;
+    float* WS = (float*)a.workspace;
+
+    const int q0 = tile * 128 + 32 * w;
+    const bool live = q0 < L;
+
+    frag8<T> qf[2][2], cfr[2], dof[2][2];
+    float fq[2], rowfq[2], gq[2], lse[2], dhat[2];
+#pragma unroll
+    for (int cq = 0; cq < 2; ++cq) {
+        const int qq = q0 + 16 * cq + lc;
+        const bool ok = qq < L;
+        const int qc = ok ? qq : L - 1;
+        float part = 0.f;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            qf[cq][st] = ok ? load8<T>(Q + (int64_t)qq * a.q.sl + 32 * st + 8 * grp) : zero8<T>();
+            dof[cq][st] = ok ? load8<T>(DO + (int64_t)qq * a.dout.sl + 32 * st + 8 * grp) : zero8<T>();
+            if (ok) {
+                const frag8<T> ov = load8<T>(O + (int64_t)qq * a.o.sl + 32 * st + 8 * grp);
+                f32x4 o32a = zero4(), o32b = zero4();
+                if (a.o32) {
+                    const float* p32 = a.o32 + ((int64_t)bh * L + qq) * DH + 32 * st + 8 * grp;
+                    o32a = *reinterpret_cast<const f32x4*>(p32);
+                    o32b = *reinterpret_cast<const f32x4*>(p32 + 4);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    float o = (float)ov[j];
+                    if (a.o32) {
+                        // o'' agrees with the DT o to within 2^-15 relative: use the DT value (attention.py:341-349)
+                        const float o2 = j < 4 ? o32a[j] : o32b[j - 4];
+                        o = (fabsf(o2 - o) <= 3.0517578125e-05f * fabsf(o)) ? o : o2;
+                    }
+                    part += o * (float)dof[cq][st][j];
+                }
+            }
+        }
+        dhat[cq] = group_sum(part);
+        cfr[cq] = ok ? load8<T>(C + (int64_t)qq * a.c.sl + 8 * grp) : zero8<T>();
+        fq[cq] = (has_f && ok) ? FF[(int64_t)qq * sfl] : 0.f;
+        rowfq[cq] = ok ? ROWF[qq] : 0.f;
+        gq[cq] = G[(int64_t)qc * sgl];
+        lse[cq] = ok ? LSE[qq] : __builtin_inff();
+    }
+    const float ga = live ? G[(int64_t)(q0 / BLK * BLK) * sgl] : 0.f;
+
+    f32x4 dqa[2][4], dca[2][2], dcoa[2][2];
+#pragma unroll
+    for (int cq = 0; cq < 2; ++cq) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) dqa[cq][db] = zero4();
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) dca[cq][sb] = dcoa[cq][sb] = zero4();
+    }
+    // per-lane partial row sums (diagonal excluded): xa = sum dS^u (own block), ya = sum P u (own block),
+    // wa = D = sum dS^, za = Z = sum P, ptt = P_tt, dptt = dP_tt, xd = cb_tt, xo/yo = off-block parts of xa/ya / rowf
+    float xa[2] = {0.f, 0.f}, ya[2] = {0.f, 0.f}, wa[2] = {0.f, 0.f}, za[2] = {0.f, 0.f};
+    float ptt[2] = {0.f, 0.f}, dptt[2] = {0.f, 0.f}, xd[2] = {0.f, 0.f}, xo[2] = {0.f, 0.f}, yo[2] = {0.f, 0.f};
+
+    const int kend = (tile * 128 + 128 < L) ? tile * 128 + 128 : L;
+    for (int n0 = 0; n0 < kend; n0 += 64) {
+        __syncthreads();
+        const int nvalid = (L - n0 < 64) ? L - n0 : 64;
+        stage_tile<T, DH, true, true>(K + (int64_t)n0 * skl, skl, nvalid, sm.ks, sm.kt, tid);
+        stage_tile<T, DH, true, false>(V + (int64_t)n0 * svl, svl, nvalid, sm.vs, nullptr, tid);
+        stage_tile<T, DS, true, true>(Bm + (int64_t)n0 * sbl, sbl, nvalid, sm.bs, sm.bt, tid);
+        if (tid < 64) {
+            const int j = n0 + tid;
+            const int jc = j < L ? j : L - 1;
+            sm.fk[tid] = (has_f && j < L) ? FF[(int64_t)j * sfl] : 0.f;
+            sm.cf[tid] = j < L ? COLF[j] : 0.f;
+            sm.gk[tid] = G[(int64_t)jc * sgl];
+        }
+        __syncthreads();
+        if (!live || n0 > q0 + 31) continue;
+        const bool diag = n0 + 63 >= q0;
+        float mid = 0.f;
+        if (!diag) mid = exp2_le0((ga - G[(int64_t)(n0 + 63) * sgl]) * LOG2E);
+
+        f32x4 sc[4][2], cb[4][2], dp[4][2];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const frag8<T> k0 = frag_rows<T, DH>(sm.ks, kb * 16, 0, lane);
+            const frag8<T> k1 = frag_rows<T, DH>(sm.ks, kb * 16, 1, lane);
+            const frag8<T> v0 = frag_rows<T, DH>(sm.vs, kb * 16, 0, lane);
+            const frag8<T> v1 = frag_rows<T, DH>(sm.vs, kb * 16, 1, lane);
+            const frag8<T> bf = frag_rows<T, DS>(sm.bs, kb * 16, 0, lane);
+#pragma unroll
+            for (int cq = 0; cq < 2; ++cq) {
+                sc[kb][cq] = mma(k1, qf[cq][1], mma(k0, qf[cq][0], zero4()));
+                cb[kb][cq] = mma(bf, cfr[cq], zero4());
+                dp[kb][cq] = mma(v1, dof[cq][1], mma(v0, dof[cq][0], zero4()));
+            }
+        }
+        // sc <- dS^ operand values, cb <- dc operand values (before rounding)
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int j = kb * 16 + 4 * grp + i;
+                const float fk = sm.fk[j];
+                if (diag) {
+                    const int jj = n0 + j;
+                    const float gk = sm.gk[j];
+#pragma unroll
+                    for (int cq = 0; cq < 2; ++cq) {
+                        const int qq = q0 + 16 * cq + lc;
+                        const bool valid = jj <= qq && jj < L && qq < L;
+                        const bool eye = valid && jj == qq;
+                        const float dec = valid ? exp2_le0((gq[cq] - gk) * LOG2E) : 0.f;
+                        const float cbv = cb[kb][cq][i];
+                        const float u = dec * cbv;
+                        float s = sc[kb][cq][i] * scale + (fq[cq] - fk);
+                        s = s + lam * u;
+                        const float pr = valid ? fast_exp2(fmaf(s, LOG2E, -lse[cq])) : 0.f;
+                        const float dpv = dp[kb][cq][i];
+                        const float ds = pr * (dpv - dhat[cq]);
+                        const float dso = eye ? 0.f : ds;
+                        ptt[cq] += eye ? pr : 0.f;
+                        dptt[cq] += eye ? dpv : 0.f;
+                        xd[cq] += eye ? cbv : 0.f;
+                        const float po = eye ? 0.f : pr;
+                        za[cq] += po;
+                        ya[cq] += po * u;
+                        wa[cq] += dso;
+                        xa[cq] += dso * u;
+                        sc[kb][cq][i] = dso;
+                        cb[kb][cq][i] = dso * (lam * dec);
+                    }
+                } else {
+                    const float cfm = sm.cf[j] * mid;
+#pragma unroll
+                    for (int cq = 0; cq < 2; ++cq) {
+                        const float uc = cb[kb][cq][i] * cfm;
+                        float s = sc[kb][cq][i] * scale + (fq[cq] - fk);
+                        s = s + (lam * rowfq[cq]) * uc;
+                        const float pr = fast_exp2(fmaf(s, LOG2E, -lse[cq]));
+                        const float ds = pr * (dp[kb][cq][i] - dhat[cq]);
+                        xo[cq] += ds * uc;
+                        yo[cq] += pr * uc;
+                        za[cq] += pr;
+                        wa[cq] += ds;
+                        sc[kb][cq][i] = ds;
+                        cb[kb][cq][i] = ds * cfm;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int cq = 0; cq < 2; ++cq) {
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                const frag8<T> dsf = pack8<T>(sc[2 * st][cq], sc[2 * st + 1][cq]);
+                const frag8<T> wf = pack8<T>(cb[2 * st][cq], cb[2 * st + 1][cq]);
+#pragma unroll
+                for (int db = 0; db < 4; ++db) dqa[cq][db] = mma(frag_trn<T>(sm.kt, db * 16, st, lane), dsf, dqa[cq][db]);
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb) {
+                    const frag8<T> bt = frag_trn<T>(sm.bt, sb * 16, st, lane);
+                    if (diag) dca[cq][sb] = mma(bt, wf, dca[cq][sb]);
+                    else dcoa[cq][sb] = mma(bt, wf, dcoa[cq][sb]);
+                }
+            }
+        }
+    }
+    if (!live) return;
+    const bool dcb32 = a.dcb_dtype == SISA_F32;
+#pragma unroll
+    for (int cq = 0; cq < 2; ++cq) {
+        const float Xa = group_sum(xa[cq]), Ya = group_sum(ya[cq]), Wa = group_sum(wa[cq]), Za = group_sum(za[cq]);
+        const float Ptt = group_sum(ptt[cq]), Dptt = group_sum(dptt[cq]), Xd = group_sum(xd[cq]);
+        const float Xo = group_sum(xo[cq]), Yo = group_sum(yo[cq]);
+        const int qq = q0 + 16 * cq + lc;
+        if (qq >= L) continue;
+        const float rs = lam * rowfq[cq];
+        const float xat = Xa + rowfq[cq] * Xo;
+        const float yat = Ya + rowfq[cq] * Yo;
+        // self-normalised exact delta and the delta-free diagonal (attention.py:453-463)
+        float ssum = Ptt + Za;
+        ssum = ssum > 0.f ? ssum : 1.f;
+        const float x0 = Dptt - dhat[cq];
+        const float tt = dhat[cq] + (Ptt * x0 + Wa) / ssum;
+        const float dstt = Ptt * (Za * x0 - Wa) / ssum;
+        const float dl_row = xat + (dhat[cq] - tt) * yat;
+        const float dsq = (float)cvt<T>(dstt);           // one DT rounding of the diagonal operands
+        const float dsc = (float)cvt<T>(dstt * lam);
+        const T* krow = K + (int64_t)qq * skl;
+        const T* brow = Bm + (int64_t)qq * sbl;
+        T* dqp = (T*)a.dq.ptr + (int64_t)b * a.dq.sb + (int64_t)h * a.dq.sh + (int64_t)qq * a.dq.sl;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const int d = db * 16 + 4 * grp;
+            const vec4<T> kv = load4<T>(krow + d);
+            f32x4 r = dqa[cq][db];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r[i] = fmaf(dsq, (float)kv[i], r[i]);
+            store_row4<T, T>(dqp + d, r * scale);
+        }
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+            const int s0 = sb * 16 + 4 * grp;
+            const vec4<T> bv = load4<T>(brow + s0);
+            f32x4 r = dca[cq][sb] + rs * dcoa[cq][sb];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r[i] = fmaf(dsc, (float)bv[i], r[i]);
+            if (dcb32) {
+                float* dcp = (float*)a.dc.ptr + (int64_t)b * a.dc.sb + (int64_t)h * a.dc.sh + (int64_t)qq * a.dc.sl;
+                *reinterpret_cast<f32x4*>(dcp + s0) = r;
+            } else {
+                T* dcp = (T*)a.dc.ptr + (int64_t)b * a.dc.sb + (int64_t)h * a.dc.sh + (int64_t)qq * a.dc.sl;
+                store_row4<T, T>(dcp + s0, r);
+            }
+        }
+        if (grp == 0) {
+            const int64_t o = (int64_t)bh * L + qq;
+            WS[WS_DELTA * BHL + o] = dhat[cq];
+            WS[WS_DDEL * BHL + o] = tt - dhat[cq];
+            WS[WS_DSD * BHL + o] = dstt;
+            WS[WS_RG * BHL + o] = lam * dl_row;
+            WS[WS_RL * BHL + o] = dl_row + dstt * Xd;
+            WS[WS_RF * BHL + o] = Wa - Za * (tt - dhat[cq]);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ backward: dk dv db
+template <class T>
+struct DkvLds {
+    T qs[64 * (DH + LDS_PAD)];   // Q, row-major (scores)
+    T qt[DH * (64 + LDS_PAD)];   // Q, transposed (dk)
+    T cs[64 * (DS + LDS_PAD)];   // C~, row-major (scores)
+    T ct[DS * (64 + LDS_PAD)];   // C~, transposed (db)
+    T ds[64 * (DH + LDS_PAD)];   // dO, row-major (dP)
+    T dt[DH * (64 + LDS_PAD)];   // dO, transposed (dv)
+    float lse[64], dhat[64], ddel[64], rowf[64], fq[64], gq[64];
+};
+
+template <class T>
+__global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a, float scale) {
+    __shared__ DkvLds<T> sm;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, grp = lane >> 4, lc = lane & 15;
+    const int ktile = blockIdx.x;                  // early key tiles carry the most queries: first
+    const int bh = blockIdx.y;
+    const int H = a.H, L = a.L;
+    const int b = bh / H, h = bh % H;
+    const bool has_f = a.f.ptr != nullptr;
+    const T* Q = (const T*)a.q.ptr + (int64_t)b * a.q.sb + (int64_t)h * a.q.sh;
+    const T* K = (const T*)a.k.ptr + (int64_t)b * a.k.sb + (int64_t)h * a.k.sh;
+    const T* V = (const T*)a.v.ptr + (int64_t)b * a.v.sb + (int64_t)h * a.v.sh;
+    const T* C = (const T*)a.c.ptr + (int64_t)b * a.c.sb + (int64_t)h * a.c.sh;
+    const T* Bm = (const T*)a.b.ptr + (int64_t)b * a.b.sb + (int64_t)h * a.b.sh;
+    const T* DO = (const T*)a.dout.ptr + (int64_t)b * a.dout.sb + (int64_t)h * a.dout.sh;
+    const float* G = (const float*)a.g.ptr + (int64_t)b * a.g.sb + (int64_t)h * a.g.sh;
+    const float* FF = has_f ? (const float*)a.f.ptr + (int64_t)b * a.f.sb + (int64_t)h * a.f.sh : nullptr;
+    const float* ROWF = a.rowf + (int64_t)bh * L;
+    const float* COLF = a.colf + (int64_t)bh * L;
+    const float* LSE = a.lse + (int64_t)bh * L;
+    const float lam = a.lam[(int64_t)h * a.s_lam];
+    const int64_t sql = a.q.sl, scl = a.c.sl, sdl = a.dout.sl, sgl = a.g.sl;
+    const int64_t sfl = has_f ? a.f.sl : 0;
+    const int64_t BHL = (int64_t)a.B * H * L;
+    const float* WS = (const float*)a.workspace;
+    const float* DELTA = WS + WS_DELTA * BHL + (int64_t)bh * L;
+    const float* DDEL = WS + WS_DDEL * BHL + (int64_t)bh * L;
+
+    const int k0 = ktile * 128 + 32 * w;
+    const bool live = k0 < L;
+    const int kblk = k0 / BLK * BLK;
+
+    frag8<T> kf[2][2], vf[2][2], bfr[2];
+    float fk[2], colf[2], gk[2], dsd[2];
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+        const int kk = k0 + 16 * kc + lc;
+        const bool ok = kk < L;
+        const int kcl = ok ? kk : L - 1;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            kf[kc][st] = ok ? load8<T>(K + (int64_t)kk * a.k.sl + 32 * st + 8 * grp) : zero8<T>();
+            vf[kc][st] = ok ? load8<T>(V + (int64_t)kk * a.v.sl + 32 * st + 8 * grp) : zero8<T>();
+        }
+        bfr[kc] = ok ? load8<T>(Bm + (int64_t)kk * a.b.sl + 8 * grp) : zero8<T>();
+        fk[kc] = (has_f && ok) ? FF[(int64_t)kk * sfl] : 0.f;
+        colf[kc] = ok ? COLF[kk] : 0.f;
+        gk[kc] = G[(int64_t)kcl * sgl];
+        dsd[kc] = ok ? WS[WS_DSD * BHL + (int64_t)bh * L + kk] : 0.f;
+    }
+    const int kblk_end = (kblk + BLK - 1 < L - 1) ? kblk + BLK - 1 : L - 1;
+    const float ge = live ? G[(int64_t)kblk_end * sgl] : 0.f;
+
+    f32x4 dva[2][4], dka[2][4], dba[2][2], dboa[2][2];
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) dva[kc][db] = dka[kc][db] = zero4();
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) dba[kc][sb] = dboa[kc][sb] = zero4();
+    }
+    float dgu[2] = {0.f, 0.f}, dfs[2] = {0.f, 0.f}, dgo[2] = {0.f, 0.f};
+
+    for (int m0 = ktile * 128; m0 < L; m0 += 64) {
+        __syncthreads();
+        const int nvalid = (L - m0 < 64) ? L - m0 : 64;
+        stage_tile<T, DH, true, true>(Q + (int64_t)m0 * sql, sql, nvalid, sm.qs, sm.qt, tid);
+        stage_tile<T, DS, true, true>(C + (int64_t)m0 * scl, scl, nvalid, sm.cs, sm.ct, tid);
+        stage_tile<T, DH, true, true>(DO + (int64_t)m0 * sdl, sdl, nvalid, sm.ds, sm.dt, tid);
+        if (tid < 64) {
+            const int i = m0 + tid;
+            const bool ok = i < L;
+            const int ic = ok ? i : L - 1;
+            sm.lse[tid] = ok ? LSE[i] : __builtin_inff();
+            sm.dhat[tid] = ok ? DELTA[i] : 0.f;
+            sm.ddel[tid] = ok ? DDEL[i] : 0.f;
+            sm.rowf[tid] = ok ? ROWF[i] : 0.f;
+            sm.fq[tid] = (has_f && ok) ? FF[(int64_t)i * sfl] : 0.f;
+            sm.gq[tid] = G[(int64_t)ic * sgl];
+        }
+        __syncthreads();
+        if (!live || m0 + 63 < k0) continue;          // every query of the tile is before every key of the wave
+        const bool pair = m0 == kblk;                 // the keys' own 64-block: pairwise decay + causal mask
+        float mid = 0.f;
+        if (!pair) mid = exp2_le0((G[(int64_t)m0 * sgl] - ge) * LOG2E);
+
+        f32x4 sc[4][2], cb[4][2], dp[4][2];
+#pragma unroll
+        for (int qb = 0; qb < 4; ++qb) {
+            const frag8<T> q0f = frag_rows<T, DH>(sm.qs, qb * 16, 0, lane);
+            const frag8<T> q1f = frag_rows<T, DH>(sm.qs, qb * 16, 1, lane);
+            const frag8<T> d0f = frag_rows<T, DH>(sm.ds, qb * 16, 0, lane);
+            const frag8<T> d1f = frag_rows<T, DH>(sm.ds, qb * 16, 1, lane);
+            const frag8<T> cf = frag_rows<T, DS>(sm.cs, qb * 16, 0, lane);
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc) {
+                sc[qb][kc] = mma(q1f, kf[kc][1], mma(q0f, kf[kc][0], zero4()));
+                cb[qb][kc] = mma(cf, bfr[kc], zero4());
+                dp[qb][kc] = mma(d1f, vf[kc][1], mma(d0f, vf[kc][0], zero4()));
+            }
+        }
+        // sc <- P, dp <- dk operand, cb <- db operand
+#pragma unroll
+        for (int qb = 0; qb < 4; ++qb) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int qi = qb * 16 + 4 * grp + i;
+                const int qq = m0 + qi;
+                const float lq = sm.lse[qi], dh = sm.dhat[qi], dd = sm.ddel[qi], fqv = sm.fq[qi];
+                if (pair) {
+                    const float gqv = sm.gq[qi];
+#pragma unroll
+                    for (int kc = 0; kc < 2; ++kc) {
+                        const int kk = k0 + 16 * kc + lc;
+                        const bool valid = qq >= kk && qq < L;
+                        const bool strict = valid && qq > kk;
+                        const bool eye = valid && qq == kk;
+                        const float dec = valid ? exp2_le0((gqv - gk[kc]) * LOG2E) : 0.f;
+                        const float u = dec * cb[qb][kc][i];
+                        float s = sc[qb][kc][i] * scale + (fqv - fk[kc]);
+                        s = s + lam * u;
+                        const float p = valid ? fast_exp2(fmaf(s, LOG2E, -lq)) : 0.f;
+                        const float dsh = p * (dp[qb][kc][i] - dh);
+                        const float dsx = dsh - p * dd;
+                        const float dso = strict ? dsx : 0.f;
+                        dgu[kc] += dso * u;
+                        dfs[kc] += dso;
+                        sc[qb][kc][i] = p;
+                        dp[qb][kc][i] = eye ? dsd[kc] : dso;
+                        cb[qb][kc][i] = (eye ? dsd[kc] : (strict ? dsh : 0.f)) * (lam * dec);
+                    }
+                } else {
+                    const float rq = sm.rowf[qi] * mid;
+#pragma unroll
+                    for (int kc = 0; kc < 2; ++kc) {
+                        const float uc = cb[qb][kc][i] * rq;
+                        float s = sc[qb][kc][i] * scale + (fqv - fk[kc]);
+                        s = s + (lam * colf[kc]) * uc;
+                        const float p = fast_exp2(fmaf(s, LOG2E, -lq));
+                        const float dsh = p * (dp[qb][kc][i] - dh);
+                        const float dsx = dsh - p * dd;
+                        dgo[kc] += dsx * uc;
+                        dfs[kc] += dsx;
+                        sc[qb][kc][i] = p;
+                        dp[qb][kc][i] = dsx;
+                        cb[qb][kc][i] = dsh * rq;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                const frag8<T> pf = pack8<T>(sc[2 * st][kc], sc[2 * st + 1][kc]);
+                const frag8<T> kfr = pack8<T>(dp[2 * st][kc], dp[2 * st + 1][kc]);
+                const frag8<T> bf = pack8<T>(cb[2 * st][kc], cb[2 * st + 1][kc]);
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    dva[kc][db] = mma(frag_trn<T>(sm.dt, db * 16, st, lane), pf, dva[kc][db]);
+                    dka[kc][db] = mma(frag_trn<T>(sm.qt, db * 16, st, lane), kfr, dka[kc][db]);
+                }
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb) {
+                    const frag8<T> ct = frag_trn<T>(sm.ct, sb * 16, st, lane);
+                    if (pair) dba[kc][sb] = mma(ct, bf, dba[kc][sb]);
+                    else dboa[kc][sb] = mma(ct, bf, dboa[kc][sb]);
+                }
+            }
+        }
+    }
+    if (!live) return;
+    const bool dcb32 = a.dcb_dtype == SISA_F32;
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+        const float Dgu = group_sum(dgu[kc]), Dfs = group_sum(dfs[kc]), Dgo = group_sum(dgo[kc]);
+        const int kk = k0 + 16 * kc + lc;
+        if (kk >= L) continue;
+        const float rk = lam * colf[kc];
+        T* dkp = (T*)a.dk.ptr + (int64_t)b * a.dk.sb + (int64_t)h * a.dk.sh + (int64_t)kk * a.dk.sl;
+        T* dvp = (T*)a.dv.ptr + (int64_t)b * a.dv.sb + (int64_t)h * a.dv.sh + (int64_t)kk * a.dv.sl;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const int d = db * 16 + 4 * grp;
+            store_row4<T, T>(dkp + d, dka[kc][db] * scale);
+            store_row4<T, T>(dvp + d, dva[kc][db]);
+        }
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+            const int s0 = sb * 16 + 4 * grp;
+            const f32x4 r = dba[kc][sb] + rk * dboa[kc][sb];
+            if (dcb32) {
+                float* p = (float*)a.db.ptr + (int64_t)b * a.db.sb + (int64_t)h * a.db.sh + (int64_t)kk * a.db.sl;
+                *reinterpret_cast<f32x4*>(p + s0) = r;
+            } else {
+                T* p = (T*)a.db.ptr + (int64_t)b * a.db.sb + (int64_t)h * a.db.sh + (int64_t)kk * a.db.sl;
+                store_row4<T, T>(p + s0, r);
+            }
+        }
+        if (grp == 0) {
+            const int64_t o = (int64_t)bh * L + kk;
+            const float dgt = Dgu + colf[kc] * Dgo;
+            a.dg[o] = WS[WS_RG * BHL + o] - lam * dgt;
+            if (has_f) a.df[o] = WS[WS_RF * BHL + o] - Dfs;
+        }
+    }
+}
+
+// dlambda_h = sum over (b, t) of the per-row parts, in fp64 with a fixed reduction order (attention.py:781-783).
+__global__ __launch_bounds__(256) void dlam_kernel(const float* __restrict__ rl, float* __restrict__ dlam, int B, int H,
+                                                  int L) {
+    __shared__ double red[256];
+    const int h = blockIdx.x;
+    const int64_t n = (int64_t)B * L;
+    double s = 0.0;
+    for (int64_t t = threadIdx.x; t < n; t += 256) {
+        const int64_t bb = t / L, l = t % L;
+        s += (double)rl[(bb * H + h) * (int64_t)L + l];
+    }
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) dlam[h] = (float)red[0];
+}
+
+template <class T>
+int launch_fwd(const sisa_attn_fwd_args* a, hipStream_t st) {
+    dim3 grid((unsigned)sisa::cdiv(a->L, 128), (unsigned)(a->B * a->H));
+    attn_fwd_kernel<T><<<grid, 256, 0, st>>>(*a, 0.125f);
+    return sisa::launch_status("sisa_attn_fwd");
+}
+
+template <class T>
+int launch_bwd(const sisa_attn_bwd_args* a, hipStream_t st) {
+    dim3 grid((unsigned)sisa::cdiv(a->L, 128), (unsigned)(a->B * a->H));
+    attn_bwd_dq_kernel<T><<<grid, 256, 0, st>>>(*a, 0.125f);
+    int rc = sisa::launch_status("sisa_attn_bwd (dq)");
+    if (rc) return rc;
+    attn_bwd_dkv_kernel<T><<<grid, 256, 0, st>>>(*a, 0.125f);
+    rc = sisa::launch_status("sisa_attn_bwd (dkv)");
+    if (rc) return rc;
+    const int64_t BHL = (int64_t)a->B * a->H * a->L;
+    dlam_kernel<<<a->H, 256, 0, st>>>((const float*)a->workspace + WS_RL * BHL, a->dlam, a->B, a->H, a->L);
+    return sisa::launch_status("sisa_attn_bwd (dlam)");
+}
+
+bool g_view_ok(const sisa_view& v) {
+    return v.ptr != nullptr;
+}
+
+}  // namespace
+
+extern "C" int sisa_factors(const sisa_factors_args* a, void* stream) {
+    SISA_REQUIRE(a != nullptr, "sisa_factors: null args");
+    SISA_REQUIRE(a->B >= 1 && a->H >= 1 && a->L >= 1, "sisa_factors: bad shape B=%d H=%d L=%d", a->B, a->H, a->L);
+    SISA_REQUIRE(g_view_ok(a->g) && a->rowf && a->colf && a->mono, "sisa_factors: null pointer");
+    dim3 grid((unsigned)sisa::cdiv(a->L, BLK), (unsigned)(a->B * a->H));
+    factors_kernel<<<grid, 64, 0, (hipStream_t)stream>>>(*a);
+    return sisa::launch_status("sisa_factors");
+}
+
+extern "C" int sisa_attn_fwd(const sisa_attn_fwd_args* a, void* stream) {
+    SISA_REQUIRE(a != nullptr, "sisa_attn_fwd: null args");
+    SISA_REQUIRE(a->B >= 1 && a->H >= 1 && a->L >= 1, "sisa_attn_fwd: bad shape B=%d H=%d L=%d", a->B, a->H, a->L);
+    SISA_REQUIRE(a->dtype == SISA_BF16 || a->dtype == SISA_F16 || a->dtype == SISA_F32, "sisa_attn_fwd: dtype %d",
+                 a->dtype);
+    SISA_REQUIRE(sisa::view_ok(a->q, a->dtype) && sisa::view_ok(a->k, a->dtype) && sisa::view_ok(a->v, a->dtype) &&
+                     sisa::view_ok(a->c, a->dtype) && sisa::view_ok(a->b, a->dtype) && sisa::view_ok(a->o, a->dtype),
+                 "sisa_attn_fwd: q/k/v/c/b/o must be non-null with 16-byte aligned rows");
+    SISA_REQUIRE(g_view_ok(a->g) && a->lam && a->rowf && a->colf && a->lse, "sisa_attn_fwd: null pointer");
+    SISA_REQUIRE(a->o32 == nullptr || sisa::aligned16(a->o32), "sisa_attn_fwd: o32 not aligned");
+    hipStream_t st = (hipStream_t)stream;
+    switch (a->dtype) {
+        case SISA_BF16: return launch_fwd<__bf16>(a, st);
+        case SISA_F16: return launch_fwd<_Float16>(a, st);
+        default: {
+            SISA_REQUIRE(a->o32 == nullptr, "sisa_attn_fwd: o32 is for bf16/fp16 inputs");
+            return launch_fwd<float>(a, st);
+        }
+    }
+}
+
+extern "C" int64_t sisa_attn_bwd_workspace_bytes(int32_t B, int32_t H, int32_t L) {
+    return (int64_t)WS_N * B * H * L * (int64_t)sizeof(float);
+}
+
+extern "C" int sisa_attn_bwd(const sisa_attn_bwd_args* a, void* stream) {
+    SISA_REQUIRE(a != nullptr, "sisa_attn_bwd: null args");
+    SISA_REQUIRE(a->B >= 1 && a->H >= 1 && a->L >= 1, "sisa_attn_bwd: bad shape B=%d H=%d L=%d", a->B, a->H, a->L);
+    SISA_REQUIRE(a->dtype == SISA_BF16 || a->dtype == SISA_F16 || a->dtype == SISA_F32, "sisa_attn_bwd: dtype %d",
+                 a->dtype);
+    SISA_REQUIRE(a->dcb_dtype == a->dtype || a->dcb_dtype == SISA_F32, "sisa_attn_bwd: dc/db dtype %d",
+                 a->dcb_dtype);
+    const int dt = a->dtype;
+    SISA_REQUIRE(sisa::view_ok(a->q, dt) && sisa::view_ok(a->k, dt) && sisa::view_ok(a->v, dt) &&
+                     sisa::view_ok(a->c, dt) && sisa::view_ok(a->b, dt) && sisa::view_ok(a->o, dt) &&
+                     sisa::view_ok(a->dout, dt) && sisa::view_ok(a->dq, dt) && sisa::view_ok(a->dk, dt) &&
+                     sisa::view_ok(a->dv, dt) && sisa::view_ok(a->dc, a->dcb_dtype) &&
+                     sisa::view_ok(a->db, a->dcb_dtype),
+                 "sisa_attn_bwd: tensors must be non-null with 16-byte aligned rows");
+    SISA_REQUIRE(g_view_ok(a->g) && a->lam && a->rowf && a->colf && a->lse && a->dg && a->dlam && a->workspace,
+                 "sisa_attn_bwd: null pointer");
+    SISA_REQUIRE((a->f.ptr == nullptr) == (a->df == nullptr), "sisa_attn_bwd: f and df must both be given or null");
+    SISA_REQUIRE(a->o32 == nullptr || (sisa::aligned16(a->o32) && dt != SISA_F32), "sisa_attn_bwd: bad o32");
+    hipStream_t st = (hipStream_t)stream;
+    switch (dt) {
+        case SISA_BF16: return launch_bwd<__bf16>(a, st);
+        case SISA_F16: return launch_bwd<_Float16>(a, st);
+        default: return launch_bwd<float>(a, st);
+    }
+}

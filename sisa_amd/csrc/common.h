@@ -1,0 +1,156 @@
+// Device-side building blocks shared by the SISA kernels (gfx950 / CDNA4, wave64).
+//
+// MFMA fragments. All matrix products use the 16x16 output block of v_mfma_f32_16x16x32_{bf16,f16}
+// (fp32 inputs: eight v_mfma_f32_16x16x4_f32). The output (C) layout of every 16x16 MFMA is
+//     lane l holds C[row = 4*(l/16) + i][col = l%16], i = 0..3.
+// An operand fragment is 8 elements per lane: A fragments hold row l%16, B fragments column l%16, and the 8
+// elements of lane group grp = l/16 are the K-slots (grp, 0..7). The physical K index of a slot never matters as
+// long as A and B use the same slot->k map; two maps are used:
+//   feature-contracted products (k = feature):  slot (grp, j) -> k = 32*step + 8*grp + j   (16 contiguous bytes)
+//   sequence-contracted products (k = position): slot (grp, j) -> pos = (2*step + j/4)*16 + 4*grp + j%4
+// The second map lets the C blocks of a previous product be used directly as the B fragment of the next one
+// (block 2*step gives slots j<4, block 2*step+1 gives slots j>=4): no register shuffles, no LDS round trip.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define SISA_DEV __device__ __forceinline__
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+static constexpr float LOG2E = 1.4426950408889634f;
+static constexpr int LDS_PAD = 8;   // elements of padding per LDS tile row
+
+template <class T> struct Vec;
+template <> struct Vec<__bf16> { typedef bf16x8 x8; typedef bf16x4 x4; typedef bf16x2 x2; };
+template <> struct Vec<_Float16> { typedef f16x8 x8; typedef f16x4 x4; typedef f16x2 x2; };
+template <> struct Vec<float> { typedef f32x8 x8; typedef f32x4 x4; typedef f32x2 x2; };
+
+template <class T> using frag8 = typename Vec<T>::x8;
+template <class T> using vec4 = typename Vec<T>::x4;
+
+// 16x16 block += A(16 x 32 K-slots) * B(32 K-slots x 16)
+SISA_DEV f32x4 mma(bf16x8 a, bf16x8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
+SISA_DEV f32x4 mma(f16x8 a, f16x8 b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+SISA_DEV f32x4 mma(f32x8 a, f32x8 b, f32x4 c) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b[j], c, 0, 0, 0);
+    return c;
+}
+
+// Round-to-nearest-even conversion (v_cvt_pk_bf16_f32 on gfx950; identical to torch's .to(bfloat16)).
+template <class T> SISA_DEV T cvt(float x) { return (T)x; }
+
+// Packs 8 fp32 values into an operand fragment, rounding each once to T.
+template <class T> SISA_DEV frag8<T> pack8(f32x4 lo, f32x4 hi) {
+    f32x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_convertvector(v, frag8<T>);
+}
+
+// Sum of the 8 (rounded) fragment values in fp32 (exact conversions, fixed order).
+template <class T> SISA_DEV float frag_sum(const frag8<T>& f) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += (float)f[j];
+    return s;
+}
+
+// exp2 of an exponent clamped to <= 0 with NaN propagation (the reference's minimum(x, 0, propagate_nan=ALL)).
+SISA_DEV float exp2_le0(float x) { return __builtin_amdgcn_exp2f(x > 0.f ? 0.f : x); }
+SISA_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// NaN-propagating max (a NaN score must poison its row).
+SISA_DEV float nmax(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b); }
+
+// Cross-lane butterfly over the four lane groups (lanes l, l^16, l^32, l^48): every lane gets the result.
+SISA_DEV float group_max(float x) {
+    x = nmax(x, __shfl_xor(x, 16));
+    x = nmax(x, __shfl_xor(x, 32));
+    return x;
+}
+SISA_DEV float group_sum(float x) {
+    x += __shfl_xor(x, 16);
+    x += __shfl_xor(x, 32);
+    return x;
+}
+
+// 16-byte / 8-byte loads of 8 or 4 consecutive elements.
+template <class T> SISA_DEV frag8<T> load8(const T* p) { return *reinterpret_cast<const frag8<T>*>(p); }
+template <class T> SISA_DEV vec4<T> load4(const T* p) { return *reinterpret_cast<const vec4<T>*>(p); }
+template <class T> SISA_DEV void store4(T* p, vec4<T> v) { *reinterpret_cast<vec4<T>*>(p) = v; }
+
+template <class T> SISA_DEV frag8<T> join(vec4<T> lo, vec4<T> hi) {
+    frag8<T> r;
+    r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+    r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+    return r;
+}
+
+template <class T> SISA_DEV frag8<T> zero8() {
+    frag8<T> r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = (T)0.f;
+    return r;
+}
+
+SISA_DEV f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+template <class T> SISA_DEV vec4<T> to_vec4(f32x4 x) { return __builtin_convertvector(x, vec4<T>); }
+
+// Cooperative staging of a (64 x C) tile of a sequence-major tensor (rows = positions, C in {32, 64} contiguous
+// features) into LDS: row-major X[r][f] (stride C+LDS_PAD) and/or transposed Xt[f][r] (stride 64+LDS_PAD).
+// Rows >= nvalid are zero. 256 threads; each thread moves 4 rows x 4 features.
+template <class T, int C, bool ROW, bool TRN>
+SISA_DEV void stage_tile(const T* __restrict__ src, int64_t srow, int nvalid, T* __restrict__ X, T* __restrict__ Xt,
+                         int tid) {
+    constexpr int NBLK = 16 * (C / 4);
+    for (int blk = tid; blk < NBLK; blk += 256) {
+        const int rq = blk / (C / 4);
+        const int cq = blk % (C / 4);
+        vec4<T> v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = rq * 4 + r;
+            if (row < nvalid) {
+                v[r] = load4<T>(src + (int64_t)row * srow + cq * 4);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[r][j] = (T)0.f;
+            }
+        }
+        if (ROW) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) store4<T>(X + (rq * 4 + r) * (C + LDS_PAD) + cq * 4, v[r]);
+        }
+        if (TRN) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                vec4<T> t;
+                t[0] = v[0][j]; t[1] = v[1][j]; t[2] = v[2][j]; t[3] = v[3][j];
+                store4<T>(Xt + (cq * 4 + j) * (64 + LDS_PAD) + rq * 4, t);
+            }
+        }
+    }
+}
+
+// Operand fragment of a row-major LDS tile X: row (position) r0 + lane%16, features 32*step + 8*grp + 0..7.
+template <class T, int C>
+SISA_DEV frag8<T> frag_rows(const T* X, int r0, int step, int lane) {
+    return load8<T>(X + (r0 + (lane & 15)) * (C + LDS_PAD) + 32 * step + 8 * (lane >> 4));
+}
+
+// Operand fragment of a transposed LDS tile Xt: row (feature) f0 + lane%16, K = positions of the sequence map for
+// `step` (positions 32*step .. 32*step+31 of the tile).
+template <class T>
+SISA_DEV frag8<T> frag_trn(const T* Xt, int f0, int step, int lane) {
+    const T* base = Xt + (f0 + (lane & 15)) * (64 + LDS_PAD) + 4 * (lane >> 4);
+    return join<T>(load4<T>(base + (2 * step) * 16), load4<T>(base + (2 * step + 1) * 16));
+}
