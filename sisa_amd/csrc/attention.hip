@@ -26,10 +26,6 @@ constexpr int DH = 64;   // d_head
 constexpr int DS = 32;   // d_state
 constexpr int BLK = 64;  // decay-factor block (rowf/colf anchors)
 
-struct Ptrs {
-    int64_t sb, sh, sl;
-};
-
 // ------------------------------------------------------------------------------------------------ factors
 // rowf_t = exp2(min((g_t - g_{block start})*log2e, 0)), colf_t = exp2(min((g_{block end} - g_t)*log2e, 0)), and the
 // maximum increase g_t - g_{t-1} per block. Reference: attention.py:129-153.
@@ -63,18 +59,98 @@ __global__ __launch_bounds__(64) void factors_kernel(sisa_factors_args a) {
 }
 
 // ------------------------------------------------------------------------------------------------ forward
+// Key tiles are staged once per workgroup; each wave then runs one of two code paths, chosen per tile and wave
+// (uniform branch): off-block tiles (every key in an earlier 64-block than every query of the wave; chunk-factored
+// decay, no masks) or the wave's own block (pairwise decay and the causal mask). Column groups of 16 queries are
+// processed one after the other to keep the live register set small (two workgroups per CU).
 template <class T>
 struct FwdLds {
-    T ks[64 * (DH + LDS_PAD)];   // K tile, row-major
-    T bs[64 * (DS + LDS_PAD)];   // B~ tile, row-major
-    T vt[DH * (64 + LDS_PAD)];   // V tile, transposed
-    float fk[64], cf[64], gk[64];
+    T ks[64 * (DH + LDS_PAD)];          // K tile, row-major
+    T bs[64 * (DS + LDS_PAD)];          // B~ tile, row-major
+    T vt[(DH + 16) * (64 + LDS_PAD)];   // V tile transposed; row DH is all ones (sum of the rounded weights), DH+1.. 0
+    float fk[64], gk[64];               // F and g at the tile's keys
+    float cfm[2][64];                   // colf * mid for the workgroup's two query blocks
 };
 
+template <class T, bool DIAG>
+SISA_DEV void fwd_tile(const FwdLds<T>& sm, const float* cfm, int lane, int n0, int q0, int L,
+                       const frag8<T> (&qf)[2][2], const frag8<T> (&cfr)[2], const float (&fq)[2],
+                       const float (&rs)[2], const float (&gq)[2], float lam, float scale, float (&m)[2],
+                       float (&l)[2], f32x4 (&acc)[2][5]) {
+    const int grp = lane >> 4, lc = lane & 15;
+#pragma unroll
+    for (int cq = 0; cq < 2; ++cq) {
+        __builtin_amdgcn_sched_barrier(0);   // one column group at a time: bounded live registers
+        f32x4 sc[4], cb[4];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const frag8<T> k0 = frag_rows<T, DH>(sm.ks, kb * 16, 0, lane);
+            const frag8<T> k1 = frag_rows<T, DH>(sm.ks, kb * 16, 1, lane);
+            const frag8<T> bf = frag_rows<T, DS>(sm.bs, kb * 16, 0, lane);
+            sc[kb] = mma(k1, qf[cq][1], mma(k0, qf[cq][0], zero4()));
+            cb[kb] = mma(bf, cfr[cq], zero4());
+        }
+        const int qq = q0 + 16 * cq + lc;
+        float mloc = -__builtin_inff();
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const int j0 = kb * 16 + 4 * grp;
+            const f32x4 fk = lds4f(&sm.fk[j0]);
+            if (DIAG) {
+                const f32x4 gk = lds4f(&sm.gk[j0]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int jj = n0 + j0 + i;
+                    const bool valid = jj <= qq && jj < L;
+                    const float dec = valid ? exp2_le0((gq[cq] - gk[i]) * LOG2E) : 0.f;
+                    float s = sc[kb][i] * scale + (fq[cq] - fk[i]);
+                    s = s + lam * (dec * cb[kb][i]);
+                    s = valid ? s : -__builtin_inff();
+                    sc[kb][i] = s;
+                    mloc = fmaxf(mloc, s);
+                }
+            } else {
+                const f32x4 cf = lds4f(&cfm[j0]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float s = sc[kb][i] * scale + (fq[cq] - fk[i]);
+                    s = s + rs[cq] * (cb[kb][i] * cf[i]);
+                    sc[kb][i] = s;
+                    mloc = fmaxf(mloc, s);
+                }
+            }
+        }
+        // online softmax in log2 units; a NaN score reaches l through its exponential
+        const float mn = fmaxf(m[cq], group_max(mloc) * LOG2E);
+        const float mu = (mn == -__builtin_inff()) ? 0.f : mn;
+        const float corr = fast_exp2(m[cq] - mu);
+        m[cq] = mu;
+        float ls = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float pe = fast_exp2(fmaf(sc[kb][i], LOG2E, -mu));
+                sc[kb][i] = pe;
+                ls += pe;
+            }
+        l[cq] = l[cq] * corr + ls;
+#pragma unroll
+        for (int db = 0; db < 5; ++db) acc[cq][db] *= corr;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const frag8<T> pf = pack8<T>(sc[2 * st], sc[2 * st + 1]);
+#pragma unroll
+            for (int db = 0; db < 5; ++db) acc[cq][db] = mma(frag_trn<T>(sm.vt, db * 16, st, lane), pf, acc[cq][db]);
+        }
+    }
+}
+
 template <class T>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(sisa_attn_fwd_args a, float scale) {
+__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(sisa_attn_fwd_args a, float scale) {
     __shared__ FwdLds<T> sm;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, grp = lane >> 4, lc = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int NQT = gridDim.x;
     const int tile = NQT - 1 - (int)blockIdx.x;   // heavy (late) query tiles first
     const int bh = blockIdx.y;
@@ -94,8 +170,14 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(sisa_attn_fwd_args a, flo
     const int64_t sql = a.q.sl, skl = a.k.sl, svl = a.v.sl, scl = a.c.sl, sbl = a.b.sl, sgl = a.g.sl;
     const int64_t sfl = has_f ? a.f.sl : 0;
 
-    const int q0 = tile * 128 + 32 * w;
+    const int tile0 = tile * 128;
+    const int q0 = tile0 + 32 * w;
     const bool live = q0 < L;
+    // anchors g at the starts of the workgroup's two query blocks
+    const float ga0 = G[(int64_t)(tile0 < L ? tile0 : L - 1) * sgl];
+    const float ga1 = G[(int64_t)(tile0 + 64 < L ? tile0 + 64 : L - 1) * sgl];
+
+    for (int i = tid; i < 16 * (64 + LDS_PAD); i += 256) sm.vt[DH * (64 + LDS_PAD) + i] = (T)(i < 64 ? 1.f : 0.f);
 
     frag8<T> qf[2][2], cfr[2];
     float fq[2], rs[2], gq[2];
@@ -111,17 +193,16 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(sisa_attn_fwd_args a, flo
         rs[cq] = lam * (ok ? ROWF[qq] : 0.f);
         gq[cq] = G[(int64_t)qc * sgl];
     }
-    const float ga = live ? G[(int64_t)(q0 / BLK * BLK) * sgl] : 0.f;   // anchor of the wave's 64-block
 
     float m[2] = {-__builtin_inff(), -__builtin_inff()};
-    float l[2] = {0.f, 0.f}, lb[2] = {0.f, 0.f};
-    f32x4 acc[2][4];
+    float l[2] = {0.f, 0.f};
+    f32x4 acc[2][5];
 #pragma unroll
     for (int cq = 0; cq < 2; ++cq)
 #pragma unroll
-        for (int db = 0; db < 4; ++db) acc[cq][db] = zero4();
+        for (int db = 0; db < 5; ++db) acc[cq][db] = zero4();
 
-    const int kend = (tile * 128 + 128 < L) ? tile * 128 + 128 : L;
+    const int kend = (tile0 + 128 < L) ? tile0 + 128 : L;
     for (int n0 = 0; n0 < kend; n0 += 64) {
         __syncthreads();
         const int nvalid = (L - n0 < 64) ? L - n0 : 64;
@@ -132,104 +213,30 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(sisa_attn_fwd_args a, flo
             const int j = n0 + tid;
             const int jc = j < L ? j : L - 1;
             sm.fk[tid] = (has_f && j < L) ? FF[(int64_t)j * sfl] : 0.f;
-            sm.cf[tid] = j < L ? COLF[j] : 0.f;
             sm.gk[tid] = G[(int64_t)jc * sgl];
+            const float cf = j < L ? COLF[j] : 0.f;
+            const float ge = G[(int64_t)(n0 + 63 < L ? n0 + 63 : L - 1) * sgl];   // end of the key block
+            sm.cfm[0][tid] = cf * exp2_le0((ga0 - ge) * LOG2E);
+            sm.cfm[1][tid] = cf * exp2_le0((ga1 - ge) * LOG2E);
         }
         __syncthreads();
-        if (!live || n0 > q0 + 31) continue;          // every key of the tile is after every query of the wave
-        const bool diag = n0 + 63 >= q0;              // the wave's own 64-block (pairwise decay + causal mask)
-        float mid = 0.f;
-        if (!diag) mid = exp2_le0((ga - G[(int64_t)(n0 + 63) * sgl]) * LOG2E);
-
-        f32x4 sc[4][2], cb[4][2];
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            const frag8<T> k0 = frag_rows<T, DH>(sm.ks, kb * 16, 0, lane);
-            const frag8<T> k1 = frag_rows<T, DH>(sm.ks, kb * 16, 1, lane);
-            const frag8<T> bf = frag_rows<T, DS>(sm.bs, kb * 16, 0, lane);
-#pragma unroll
-            for (int cq = 0; cq < 2; ++cq) {
-                sc[kb][cq] = mma(k1, qf[cq][1], mma(k0, qf[cq][0], zero4()));
-                cb[kb][cq] = mma(bf, cfr[cq], zero4());
-            }
-        }
-        // scores (natural-log units), row maxima
-        float mloc[2] = {-__builtin_inff(), -__builtin_inff()};
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int j = kb * 16 + 4 * grp + i;
-                const float fk = sm.fk[j];
-                if (diag) {
-                    const int jj = n0 + j;
-                    const float gk = sm.gk[j];
-#pragma unroll
-                    for (int cq = 0; cq < 2; ++cq) {
-                        const int qq = q0 + 16 * cq + lc;
-                        const bool valid = jj <= qq && jj < L;
-                        const float dec = valid ? exp2_le0((gq[cq] - gk) * LOG2E) : 0.f;
-                        float s = sc[kb][cq][i] * scale + (fq[cq] - fk);
-                        s = s + lam * (dec * cb[kb][cq][i]);
-                        s = valid ? s : -__builtin_inff();
-                        sc[kb][cq][i] = s;
-                        mloc[cq] = nmax(mloc[cq], s);
-                    }
-                } else {
-                    const float cfm = sm.cf[j] * mid;
-#pragma unroll
-                    for (int cq = 0; cq < 2; ++cq) {
-                        float s = sc[kb][cq][i] * scale + (fq[cq] - fk);
-                        s = s + rs[cq] * (cb[kb][cq][i] * cfm);
-                        sc[kb][cq][i] = s;
-                        mloc[cq] = nmax(mloc[cq], s);
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int cq = 0; cq < 2; ++cq) {
-            float mn = nmax(m[cq], group_max(mloc[cq]) * LOG2E);
-            const float mu = (mn == -__builtin_inff()) ? 0.f : mn;
-            const float corr = fast_exp2(m[cq] - mu);
-            m[cq] = mu;
-            l[cq] *= corr;
-            lb[cq] *= corr;
-#pragma unroll
-            for (int db = 0; db < 4; ++db) acc[cq][db] *= corr;
-            float ls = 0.f;
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float pe = fast_exp2(fmaf(sc[kb][cq][i], LOG2E, -mu));
-                    sc[kb][cq][i] = pe;
-                    ls += pe;
-                }
-            l[cq] += ls;
-#pragma unroll
-            for (int st = 0; st < 2; ++st) {
-                const frag8<T> pf = pack8<T>(sc[2 * st][cq], sc[2 * st + 1][cq]);
-                lb[cq] += frag_sum<T>(pf);
-#pragma unroll
-                for (int db = 0; db < 4; ++db) acc[cq][db] = mma(frag_trn<T>(sm.vt, db * 16, st, lane), pf, acc[cq][db]);
-            }
-        }
+        if (!live) continue;
+        if (n0 + 63 < q0)
+            fwd_tile<T, false>(sm, sm.cfm[w >> 1], lane, n0, q0, L, qf, cfr, fq, rs, gq, lam, scale, m, l, acc);
+        else if (n0 <= q0 + 31)
+            fwd_tile<T, true>(sm, sm.cfm[w >> 1], lane, n0, q0, L, qf, cfr, fq, rs, gq, lam, scale, m, l, acc);
     }
     if (!live) return;
     T* O = (T*)a.o.ptr + (int64_t)b * a.o.sb + (int64_t)h * a.o.sh;
 #pragma unroll
     for (int cq = 0; cq < 2; ++cq) {
         const float lt = group_sum(l[cq]);
-        const float lbt = group_sum(lb[cq]);
+        const float lbt = group_bcast0(acc[cq][4][0], lane);   // row DH of O^T: sum of the rounded weights
         const int qq = q0 + 16 * cq + lc;
         if (qq >= L) continue;
         const float ls = (lt == 0.f) ? 1.f : lt;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
-            const int d = db * 16 + 4 * grp;
-            store4<T>(O + (int64_t)qq * a.o.sl + d, to_vec4<T>(acc[cq][db] / ls));
-        }
+        for (int db = 0; db < 4; ++db) store4<T>(O + (int64_t)qq * a.o.sl + db * 16 + 4 * grp, to_vec4<T>(acc[cq][db] / ls));
         if (a.o32) {
             const float lbs = (lbt == 0.f) ? 1.f : lbt;
             float* O32 = a.o32 + ((int64_t)bh * L + qq) * DH;
@@ -251,8 +258,108 @@ struct DqLds {
     T vs[64 * (DH + LDS_PAD)];   // V, row-major (dP)
     T bs[64 * (DS + LDS_PAD)];   // B~, row-major (scores)
     T bt[DS * (64 + LDS_PAD)];   // B~, transposed (dc)
-    float fk[64], cf[64], gk[64];
+    float fk[64], gk[64];
+    float cfm[2][64];            // colf * mid for the workgroup's two query blocks
 };
+
+// Per-query row sums of the dq kernel (diagonal excluded): xa = sum dS^ u, ya = sum P u, wa = D = sum dS^,
+// za = Z = sum P, ptt = P_tt, dptt = dP_tt, xd = cb_tt. Off-block tiles accumulate xa, ya without the row factor
+// rowf; a wave's own-block tile is its last one, and scale_offblock() applies rowf (and lam*rowf to dc) before it.
+struct RowSums {
+    float xa, ya, wa, za, ptt, dptt, xd;
+};
+
+// Backward kernels: 8 waves per workgroup, 16 rows (one column group) per wave, so that two workgroups fit on a CU.
+constexpr int BWD_NC = 1;                      // column groups of 16 rows per wave
+constexpr int BWD_WAVES = 8 / BWD_NC;          // waves per workgroup (128 rows)
+constexpr int BWD_THREADS = 64 * BWD_WAVES;
+
+template <class T, bool DIAG>
+SISA_DEV void dq_tile(const DqLds<T>& sm, const float* cfm, int lane, int n0, int q0, int L,
+                      const frag8<T> (&qf)[BWD_NC][2], const frag8<T> (&cfr)[BWD_NC],
+                      const frag8<T> (&dof)[BWD_NC][2], const float (&fq)[BWD_NC], const float (&rs)[BWD_NC],
+                      const float (&gq)[BWD_NC], const float (&lse)[BWD_NC], const float (&dhat)[BWD_NC], float lam,
+                      float scale, RowSums (&rsum)[BWD_NC], f32x4 (&dqa)[BWD_NC][4], f32x4 (&dca)[BWD_NC][2]) {
+    const int grp = lane >> 4, lc = lane & 15;
+#pragma unroll
+    for (int cq = 0; cq < BWD_NC; ++cq) {
+        const int qq = q0 + 16 * cq + lc;
+        RowSums& R = rsum[cq];
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {           // 32 keys (one K-step of the dq/dc products) at a time
+            __builtin_amdgcn_sched_barrier(0);
+            f32x4 sc[2], cb[2], dp[2];
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb) {
+                const int kb = 2 * st + hb;
+                const frag8<T> k0 = frag_rows<T, DH>(sm.ks, kb * 16, 0, lane);
+                const frag8<T> k1 = frag_rows<T, DH>(sm.ks, kb * 16, 1, lane);
+                const frag8<T> v0 = frag_rows<T, DH>(sm.vs, kb * 16, 0, lane);
+                const frag8<T> v1 = frag_rows<T, DH>(sm.vs, kb * 16, 1, lane);
+                const frag8<T> bf = frag_rows<T, DS>(sm.bs, kb * 16, 0, lane);
+                sc[hb] = mma(k1, qf[cq][1], mma(k0, qf[cq][0], zero4()));
+                cb[hb] = mma(bf, cfr[cq], zero4());
+                dp[hb] = mma(v1, dof[cq][1], mma(v0, dof[cq][0], zero4()));
+            }
+            // sc <- dq operand (dS^), cb <- dc operand
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb) {
+                const int j0 = (2 * st + hb) * 16 + 4 * grp;
+                const f32x4 fk = lds4f(&sm.fk[j0]);
+                if (DIAG) {
+                    const f32x4 gk = lds4f(&sm.gk[j0]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int jj = n0 + j0 + i;
+                        const bool valid = jj <= qq && jj < L && qq < L;
+                        const bool eye = valid && jj == qq;
+                        const float dec = valid ? exp2_le0((gq[cq] - gk[i]) * LOG2E) : 0.f;
+                        const float cbv = cb[hb][i];
+                        const float u = dec * cbv;
+                        float s = sc[hb][i] * scale + (fq[cq] - fk[i]);
+                        s = s + lam * u;
+                        const float pr = valid ? fast_exp2(fmaf(s, LOG2E, -lse[cq])) : 0.f;
+                        const float dpv = dp[hb][i];
+                        const float ds = pr * (dpv - dhat[cq]);
+                        const float dso = eye ? 0.f : ds;
+                        R.ptt += eye ? pr : 0.f;
+                        R.dptt += eye ? dpv : 0.f;
+                        R.xd += eye ? cbv : 0.f;
+                        const float po = eye ? 0.f : pr;
+                        R.za += po;
+                        R.ya += po * u;
+                        R.wa += dso;
+                        R.xa += dso * u;
+                        sc[hb][i] = dso;
+                        cb[hb][i] = dso * (lam * dec);
+                    }
+                } else {
+                    const f32x4 cf = lds4f(&cfm[j0]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float uc = cb[hb][i] * cf[i];
+                        float s = sc[hb][i] * scale + (fq[cq] - fk[i]);
+                        s = s + rs[cq] * uc;
+                        const float pr = fast_exp2(fmaf(s, LOG2E, -lse[cq]));
+                        const float ds = pr * (dp[hb][i] - dhat[cq]);
+                        R.xa += ds * uc;
+                        R.ya += pr * uc;
+                        R.za += pr;
+                        R.wa += ds;
+                        sc[hb][i] = ds;
+                        cb[hb][i] = ds * cf[i];
+                    }
+                }
+            }
+            const frag8<T> dsf = pack8<T>(sc[0], sc[1]);
+            const frag8<T> wf = pack8<T>(cb[0], cb[1]);
+#pragma unroll
+            for (int db = 0; db < 4; ++db) dqa[cq][db] = mma(frag_trn<T>(sm.kt, db * 16, st, lane), dsf, dqa[cq][db]);
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) dca[cq][sb] = mma(frag_trn<T>(sm.bt, sb * 16, st, lane), wf, dca[cq][sb]);
+        }
+    }
+}
 
 template <class T, class TO>
 SISA_DEV void store_row4(TO* p, f32x4 v) {
@@ -260,9 +367,10 @@ SISA_DEV void store_row4(TO* p, f32x4 v) {
 }
 
 template <class T>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(sisa_attn_bwd_args a, float scale) {
+__global__ __launch_bounds__(BWD_THREADS, 2) void attn_bwd_dq_kernel(sisa_attn_bwd_args a, float scale) {
     __shared__ DqLds<T> sm;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, grp = lane >> 4, lc = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int NQT = gridDim.x;
     const int tile = NQT - 1 - (int)blockIdx.x;
     const int bh = blockIdx.y;
@@ -287,13 +395,18 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(sisa_attn_bwd_args a, 
     const int64_t BHL = (int64_t)a.B * H * L;
     float* WS = (float*)a.workspace;
 
-    const int q0 = tile * 128 + 32 * w;
+    const int tile0 = tile * 128;
+    const int q0 = tile0 + 16 * BWD_NC * w;
+    const int qend = q0 + 16 * BWD_NC - 1;
+    const int qblk = (w * BWD_NC) >> 2;           // which of the workgroup's two query blocks
     const bool live = q0 < L;
+    const float ga0 = G[(int64_t)(tile0 < L ? tile0 : L - 1) * sgl];
+    const float ga1 = G[(int64_t)(tile0 + 64 < L ? tile0 + 64 : L - 1) * sgl];
 
-    frag8<T> qf[2][2], cfr[2], dof[2][2];
-    float fq[2], rowfq[2], gq[2], lse[2], dhat[2];
+    frag8<T> qf[BWD_NC][2], cfr[BWD_NC], dof[BWD_NC][2];
+    float fq[BWD_NC], rowfq[BWD_NC], rs[BWD_NC], gq[BWD_NC], lse[BWD_NC], dhat[BWD_NC];
 #pragma unroll
-    for (int cq = 0; cq < 2; ++cq) {
+    for (int cq = 0; cq < BWD_NC; ++cq) {
         const int qq = q0 + 16 * cq + lc;
         const bool ok = qq < L;
         const int qc = ok ? qq : L - 1;
@@ -326,142 +439,66 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(sisa_attn_bwd_args a, 
         cfr[cq] = ok ? load8<T>(C + (int64_t)qq * a.c.sl + 8 * grp) : zero8<T>();
         fq[cq] = (has_f && ok) ? FF[(int64_t)qq * sfl] : 0.f;
         rowfq[cq] = ok ? ROWF[qq] : 0.f;
+        rs[cq] = lam * rowfq[cq];
         gq[cq] = G[(int64_t)qc * sgl];
         lse[cq] = ok ? LSE[qq] : __builtin_inff();
     }
-    const float ga = live ? G[(int64_t)(q0 / BLK * BLK) * sgl] : 0.f;
 
-    f32x4 dqa[2][4], dca[2][2], dcoa[2][2];
+    f32x4 dqa[BWD_NC][4], dca[BWD_NC][2];
+    RowSums rsum[BWD_NC];
 #pragma unroll
-    for (int cq = 0; cq < 2; ++cq) {
+    for (int cq = 0; cq < BWD_NC; ++cq) {
 #pragma unroll
         for (int db = 0; db < 4; ++db) dqa[cq][db] = zero4();
 #pragma unroll
-        for (int sb = 0; sb < 2; ++sb) dca[cq][sb] = dcoa[cq][sb] = zero4();
+        for (int sb = 0; sb < 2; ++sb) dca[cq][sb] = zero4();
+        rsum[cq] = RowSums{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     }
-    // per-lane partial row sums (diagonal excluded): xa = sum dS^u (own block), ya = sum P u (own block),
-    // wa = D = sum dS^, za = Z = sum P, ptt = P_tt, dptt = dP_tt, xd = cb_tt, xo/yo = off-block parts of xa/ya / rowf
-    float xa[2] = {0.f, 0.f}, ya[2] = {0.f, 0.f}, wa[2] = {0.f, 0.f}, za[2] = {0.f, 0.f};
-    float ptt[2] = {0.f, 0.f}, dptt[2] = {0.f, 0.f}, xd[2] = {0.f, 0.f}, xo[2] = {0.f, 0.f}, yo[2] = {0.f, 0.f};
 
-    const int kend = (tile * 128 + 128 < L) ? tile * 128 + 128 : L;
+    const int kend = (tile0 + 128 < L) ? tile0 + 128 : L;
     for (int n0 = 0; n0 < kend; n0 += 64) {
         __syncthreads();
         const int nvalid = (L - n0 < 64) ? L - n0 : 64;
-        stage_tile<T, DH, true, true>(K + (int64_t)n0 * skl, skl, nvalid, sm.ks, sm.kt, tid);
-        stage_tile<T, DH, true, false>(V + (int64_t)n0 * svl, svl, nvalid, sm.vs, nullptr, tid);
-        stage_tile<T, DS, true, true>(Bm + (int64_t)n0 * sbl, sbl, nvalid, sm.bs, sm.bt, tid);
+        stage_tile<T, DH, true, true, BWD_THREADS>(K + (int64_t)n0 * skl, skl, nvalid, sm.ks, sm.kt, tid);
+        stage_tile<T, DH, true, false, BWD_THREADS>(V + (int64_t)n0 * svl, svl, nvalid, sm.vs, nullptr, tid);
+        stage_tile<T, DS, true, true, BWD_THREADS>(Bm + (int64_t)n0 * sbl, sbl, nvalid, sm.bs, sm.bt, tid);
         if (tid < 64) {
             const int j = n0 + tid;
             const int jc = j < L ? j : L - 1;
             sm.fk[tid] = (has_f && j < L) ? FF[(int64_t)j * sfl] : 0.f;
-            sm.cf[tid] = j < L ? COLF[j] : 0.f;
             sm.gk[tid] = G[(int64_t)jc * sgl];
+            const float cf = j < L ? COLF[j] : 0.f;
+            const float ge = G[(int64_t)(n0 + 63 < L ? n0 + 63 : L - 1) * sgl];
+            sm.cfm[0][tid] = cf * exp2_le0((ga0 - ge) * LOG2E);
+            sm.cfm[1][tid] = cf * exp2_le0((ga1 - ge) * LOG2E);
         }
         __syncthreads();
-        if (!live || n0 > q0 + 31) continue;
-        const bool diag = n0 + 63 >= q0;
-        float mid = 0.f;
-        if (!diag) mid = exp2_le0((ga - G[(int64_t)(n0 + 63) * sgl]) * LOG2E);
-
-        f32x4 sc[4][2], cb[4][2], dp[4][2];
+        if (!live) continue;
+        if (n0 + 63 < q0) {
+            dq_tile<T, false>(sm, sm.cfm[qblk], lane, n0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, scale,
+                              rsum, dqa, dca);
+        } else if (n0 <= qend) {
+            // the wave's own 64-block is its last tile: apply the off-block row factors once, in fp32
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            const frag8<T> k0 = frag_rows<T, DH>(sm.ks, kb * 16, 0, lane);
-            const frag8<T> k1 = frag_rows<T, DH>(sm.ks, kb * 16, 1, lane);
-            const frag8<T> v0 = frag_rows<T, DH>(sm.vs, kb * 16, 0, lane);
-            const frag8<T> v1 = frag_rows<T, DH>(sm.vs, kb * 16, 1, lane);
-            const frag8<T> bf = frag_rows<T, DS>(sm.bs, kb * 16, 0, lane);
+            for (int cq = 0; cq < BWD_NC; ++cq) {
+                rsum[cq].xa *= rowfq[cq];
+                rsum[cq].ya *= rowfq[cq];
 #pragma unroll
-            for (int cq = 0; cq < 2; ++cq) {
-                sc[kb][cq] = mma(k1, qf[cq][1], mma(k0, qf[cq][0], zero4()));
-                cb[kb][cq] = mma(bf, cfr[cq], zero4());
-                dp[kb][cq] = mma(v1, dof[cq][1], mma(v0, dof[cq][0], zero4()));
+                for (int sb = 0; sb < 2; ++sb) dca[cq][sb] *= rs[cq];
             }
-        }
-        // sc <- dS^ operand values, cb <- dc operand values (before rounding)
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int j = kb * 16 + 4 * grp + i;
-                const float fk = sm.fk[j];
-                if (diag) {
-                    const int jj = n0 + j;
-                    const float gk = sm.gk[j];
-#pragma unroll
-                    for (int cq = 0; cq < 2; ++cq) {
-                        const int qq = q0 + 16 * cq + lc;
-                        const bool valid = jj <= qq && jj < L && qq < L;
-                        const bool eye = valid && jj == qq;
-                        const float dec = valid ? exp2_le0((gq[cq] - gk) * LOG2E) : 0.f;
-                        const float cbv = cb[kb][cq][i];
-                        const float u = dec * cbv;
-                        float s = sc[kb][cq][i] * scale + (fq[cq] - fk);
-                        s = s + lam * u;
-                        const float pr = valid ? fast_exp2(fmaf(s, LOG2E, -lse[cq])) : 0.f;
-                        const float dpv = dp[kb][cq][i];
-                        const float ds = pr * (dpv - dhat[cq]);
-                        const float dso = eye ? 0.f : ds;
-                        ptt[cq] += eye ? pr : 0.f;
-                        dptt[cq] += eye ? dpv : 0.f;
-                        xd[cq] += eye ? cbv : 0.f;
-                        const float po = eye ? 0.f : pr;
-                        za[cq] += po;
-                        ya[cq] += po * u;
-                        wa[cq] += dso;
-                        xa[cq] += dso * u;
-                        sc[kb][cq][i] = dso;
-                        cb[kb][cq][i] = dso * (lam * dec);
-                    }
-                } else {
-                    const float cfm = sm.cf[j] * mid;
-#pragma unroll
-                    for (int cq = 0; cq < 2; ++cq) {
-                        const float uc = cb[kb][cq][i] * cfm;
-                        float s = sc[kb][cq][i] * scale + (fq[cq] - fk);
-                        s = s + (lam * rowfq[cq]) * uc;
-                        const float pr = fast_exp2(fmaf(s, LOG2E, -lse[cq]));
-                        const float ds = pr * (dp[kb][cq][i] - dhat[cq]);
-                        xo[cq] += ds * uc;
-                        yo[cq] += pr * uc;
-                        za[cq] += pr;
-                        wa[cq] += ds;
-                        sc[kb][cq][i] = ds;
-                        cb[kb][cq][i] = ds * cfm;
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int cq = 0; cq < 2; ++cq) {
-#pragma unroll
-            for (int st = 0; st < 2; ++st) {
-                const frag8<T> dsf = pack8<T>(sc[2 * st][cq], sc[2 * st + 1][cq]);
-                const frag8<T> wf = pack8<T>(cb[2 * st][cq], cb[2 * st + 1][cq]);
-#pragma unroll
-                for (int db = 0; db < 4; ++db) dqa[cq][db] = mma(frag_trn<T>(sm.kt, db * 16, st, lane), dsf, dqa[cq][db]);
-#pragma unroll
-                for (int sb = 0; sb < 2; ++sb) {
-                    const frag8<T> bt = frag_trn<T>(sm.bt, sb * 16, st, lane);
-                    if (diag) dca[cq][sb] = mma(bt, wf, dca[cq][sb]);
-                    else dcoa[cq][sb] = mma(bt, wf, dcoa[cq][sb]);
-                }
-            }
+            dq_tile<T, true>(sm, sm.cfm[qblk], lane, n0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, scale,
+                             rsum, dqa, dca);
         }
     }
     if (!live) return;
     const bool dcb32 = a.dcb_dtype == SISA_F32;
 #pragma unroll
-    for (int cq = 0; cq < 2; ++cq) {
-        const float Xa = group_sum(xa[cq]), Ya = group_sum(ya[cq]), Wa = group_sum(wa[cq]), Za = group_sum(za[cq]);
-        const float Ptt = group_sum(ptt[cq]), Dptt = group_sum(dptt[cq]), Xd = group_sum(xd[cq]);
-        const float Xo = group_sum(xo[cq]), Yo = group_sum(yo[cq]);
+    for (int cq = 0; cq < BWD_NC; ++cq) {
+        const RowSums& R = rsum[cq];
+        const float xat = group_sum(R.xa), yat = group_sum(R.ya), Wa = group_sum(R.wa), Za = group_sum(R.za);
+        const float Ptt = group_sum(R.ptt), Dptt = group_sum(R.dptt), Xd = group_sum(R.xd);
         const int qq = q0 + 16 * cq + lc;
         if (qq >= L) continue;
-        const float rs = lam * rowfq[cq];
-        const float xat = Xa + rowfq[cq] * Xo;
-        const float yat = Ya + rowfq[cq] * Yo;
         // self-normalised exact delta and the delta-free diagonal (attention.py:453-463)
         float ssum = Ptt + Za;
         ssum = ssum > 0.f ? ssum : 1.f;
@@ -487,7 +524,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(sisa_attn_bwd_args a, 
         for (int sb = 0; sb < 2; ++sb) {
             const int s0 = sb * 16 + 4 * grp;
             const vec4<T> bv = load4<T>(brow + s0);
-            f32x4 r = dca[cq][sb] + rs * dcoa[cq][sb];
+            f32x4 r = dca[cq][sb];
 #pragma unroll
             for (int i = 0; i < 4; ++i) r[i] = fmaf(dsc, (float)bv[i], r[i]);
             if (dcb32) {
@@ -519,13 +556,102 @@ struct DkvLds {
     T ct[DS * (64 + LDS_PAD)];   // C~, transposed (db)
     T ds[64 * (DH + LDS_PAD)];   // dO, row-major (dP)
     T dt[DH * (64 + LDS_PAD)];   // dO, transposed (dv)
-    float lse[64], dhat[64], ddel[64], rowf[64], fq[64], gq[64];
+    float lse[64], dhat[64], ddel[64], fq[64], gq[64];
+    float rq[2][64];             // rowf * mid for the workgroup's two key blocks
 };
 
+template <class T, bool PAIR>
+SISA_DEV void dkv_tile(const DkvLds<T>& sm, const float* rqm, int lane, int m0, int k0, int L,
+                       const frag8<T> (&kf)[BWD_NC][2], const frag8<T> (&vf)[BWD_NC][2],
+                       const frag8<T> (&bfr)[BWD_NC], const float (&fk)[BWD_NC], const float (&rk)[BWD_NC],
+                       const float (&gk)[BWD_NC], const float (&dsd)[BWD_NC], float lam, float scale,
+                       float (&dgu)[BWD_NC], float (&dfs)[BWD_NC], f32x4 (&dva)[BWD_NC][4], f32x4 (&dka)[BWD_NC][4],
+                       f32x4 (&dba)[BWD_NC][2]) {
+    const int grp = lane >> 4, lc = lane & 15;
+#pragma unroll
+    for (int kc = 0; kc < BWD_NC; ++kc) {
+        const int kk = k0 + 16 * kc + lc;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {           // 32 queries (one K-step of the dk/dv/db products) at a time
+            __builtin_amdgcn_sched_barrier(0);
+            f32x4 sc[2], cb[2], dp[2];
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb) {
+                const int qb = 2 * st + hb;
+                const frag8<T> q0f = frag_rows<T, DH>(sm.qs, qb * 16, 0, lane);
+                const frag8<T> q1f = frag_rows<T, DH>(sm.qs, qb * 16, 1, lane);
+                const frag8<T> d0f = frag_rows<T, DH>(sm.ds, qb * 16, 0, lane);
+                const frag8<T> d1f = frag_rows<T, DH>(sm.ds, qb * 16, 1, lane);
+                const frag8<T> cf = frag_rows<T, DS>(sm.cs, qb * 16, 0, lane);
+                sc[hb] = mma(q1f, kf[kc][1], mma(q0f, kf[kc][0], zero4()));
+                cb[hb] = mma(cf, bfr[kc], zero4());
+                dp[hb] = mma(d1f, vf[kc][1], mma(d0f, vf[kc][0], zero4()));
+            }
+            // sc <- P, dp <- dk operand, cb <- db operand
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb) {
+                const int i0 = (2 * st + hb) * 16 + 4 * grp;
+                const f32x4 lq = lds4f(&sm.lse[i0]), dh = lds4f(&sm.dhat[i0]), dd = lds4f(&sm.ddel[i0]);
+                const f32x4 fq = lds4f(&sm.fq[i0]);
+                if (PAIR) {
+                    const f32x4 gq = lds4f(&sm.gq[i0]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int qq = m0 + i0 + i;
+                        const bool valid = qq >= kk && qq < L;
+                        const bool strict = valid && qq > kk;
+                        const bool eye = valid && qq == kk;
+                        const float dec = valid ? exp2_le0((gq[i] - gk[kc]) * LOG2E) : 0.f;
+                        const float u = dec * cb[hb][i];
+                        float s = sc[hb][i] * scale + (fq[i] - fk[kc]);
+                        s = s + lam * u;
+                        const float p = valid ? fast_exp2(fmaf(s, LOG2E, -lq[i])) : 0.f;
+                        const float dsh = p * (dp[hb][i] - dh[i]);
+                        const float dsx = dsh - p * dd[i];
+                        const float dso = strict ? dsx : 0.f;
+                        dgu[kc] += dso * u;
+                        dfs[kc] += dso;
+                        sc[hb][i] = p;
+                        dp[hb][i] = eye ? dsd[kc] : dso;
+                        cb[hb][i] = (eye ? dsd[kc] : (strict ? dsh : 0.f)) * (lam * dec);
+                    }
+                } else {
+                    const f32x4 rq = lds4f(&rqm[i0]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float uc = cb[hb][i] * rq[i];
+                        float s = sc[hb][i] * scale + (fq[i] - fk[kc]);
+                        s = s + rk[kc] * uc;
+                        const float p = fast_exp2(fmaf(s, LOG2E, -lq[i]));
+                        const float dsh = p * (dp[hb][i] - dh[i]);
+                        const float dsx = dsh - p * dd[i];
+                        dgu[kc] += dsx * uc;
+                        dfs[kc] += dsx;
+                        sc[hb][i] = p;
+                        dp[hb][i] = dsx;
+                        cb[hb][i] = dsh * rq[i];
+                    }
+                }
+            }
+            const frag8<T> pf = pack8<T>(sc[0], sc[1]);
+            const frag8<T> kfr = pack8<T>(dp[0], dp[1]);
+            const frag8<T> bf = pack8<T>(cb[0], cb[1]);
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                dva[kc][db] = mma(frag_trn<T>(sm.dt, db * 16, st, lane), pf, dva[kc][db]);
+                dka[kc][db] = mma(frag_trn<T>(sm.qt, db * 16, st, lane), kfr, dka[kc][db]);
+            }
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) dba[kc][sb] = mma(frag_trn<T>(sm.ct, sb * 16, st, lane), bf, dba[kc][sb]);
+        }
+    }
+}
+
 template <class T>
-__global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a, float scale) {
+__global__ __launch_bounds__(BWD_THREADS, 2) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a, float scale) {
     __shared__ DkvLds<T> sm;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, grp = lane >> 4, lc = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ktile = blockIdx.x;                  // early key tiles carry the most queries: first
     const int bh = blockIdx.y;
     const int H = a.H, L = a.L;
@@ -550,14 +676,19 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a,
     const float* DELTA = WS + WS_DELTA * BHL + (int64_t)bh * L;
     const float* DDEL = WS + WS_DDEL * BHL + (int64_t)bh * L;
 
-    const int k0 = ktile * 128 + 32 * w;
+    const int ktile0 = ktile * 128;
+    const int k0 = ktile0 + 16 * BWD_NC * w;
+    const int kblkw = (w * BWD_NC) >> 2;          // which of the workgroup's two key blocks
     const bool live = k0 < L;
     const int kblk = k0 / BLK * BLK;
+    // g at the ends of the workgroup's two key blocks
+    const float ge0 = G[(int64_t)(ktile0 + 63 < L ? ktile0 + 63 : L - 1) * sgl];
+    const float ge1 = G[(int64_t)(ktile0 + 127 < L ? ktile0 + 127 : L - 1) * sgl];
 
-    frag8<T> kf[2][2], vf[2][2], bfr[2];
-    float fk[2], colf[2], gk[2], dsd[2];
+    frag8<T> kf[BWD_NC][2], vf[BWD_NC][2], bfr[BWD_NC];
+    float fk[BWD_NC], colf[BWD_NC], rk[BWD_NC], gk[BWD_NC], dsd[BWD_NC];
 #pragma unroll
-    for (int kc = 0; kc < 2; ++kc) {
+    for (int kc = 0; kc < BWD_NC; ++kc) {
         const int kk = k0 + 16 * kc + lc;
         const bool ok = kk < L;
         const int kcl = ok ? kk : L - 1;
@@ -569,28 +700,31 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a,
         bfr[kc] = ok ? load8<T>(Bm + (int64_t)kk * a.b.sl + 8 * grp) : zero8<T>();
         fk[kc] = (has_f && ok) ? FF[(int64_t)kk * sfl] : 0.f;
         colf[kc] = ok ? COLF[kk] : 0.f;
+        rk[kc] = lam * colf[kc];
         gk[kc] = G[(int64_t)kcl * sgl];
         dsd[kc] = ok ? WS[WS_DSD * BHL + (int64_t)bh * L + kk] : 0.f;
     }
-    const int kblk_end = (kblk + BLK - 1 < L - 1) ? kblk + BLK - 1 : L - 1;
-    const float ge = live ? G[(int64_t)kblk_end * sgl] : 0.f;
 
-    f32x4 dva[2][4], dka[2][4], dba[2][2], dboa[2][2];
+    f32x4 dva[BWD_NC][4], dka[BWD_NC][4], dba[BWD_NC][2];
+    // column sums (diagonal excluded); off-block tiles accumulate dgu without the column factor colf
+    float dgu[BWD_NC], dfs[BWD_NC];
 #pragma unroll
-    for (int kc = 0; kc < 2; ++kc) {
+    for (int kc = 0; kc < BWD_NC; ++kc) {
 #pragma unroll
         for (int db = 0; db < 4; ++db) dva[kc][db] = dka[kc][db] = zero4();
 #pragma unroll
-        for (int sb = 0; sb < 2; ++sb) dba[kc][sb] = dboa[kc][sb] = zero4();
+        for (int sb = 0; sb < 2; ++sb) dba[kc][sb] = zero4();
+        dgu[kc] = dfs[kc] = 0.f;
     }
-    float dgu[2] = {0.f, 0.f}, dfs[2] = {0.f, 0.f}, dgo[2] = {0.f, 0.f};
 
-    for (int m0 = ktile * 128; m0 < L; m0 += 64) {
+    // query tiles in descending order: the keys' own 64-block comes last for every wave
+    const int mlast = (L - 1) / 64 * 64;
+    for (int m0 = mlast; m0 >= ktile0; m0 -= 64) {
         __syncthreads();
         const int nvalid = (L - m0 < 64) ? L - m0 : 64;
-        stage_tile<T, DH, true, true>(Q + (int64_t)m0 * sql, sql, nvalid, sm.qs, sm.qt, tid);
-        stage_tile<T, DS, true, true>(C + (int64_t)m0 * scl, scl, nvalid, sm.cs, sm.ct, tid);
-        stage_tile<T, DH, true, true>(DO + (int64_t)m0 * sdl, sdl, nvalid, sm.ds, sm.dt, tid);
+        stage_tile<T, DH, true, true, BWD_THREADS>(Q + (int64_t)m0 * sql, sql, nvalid, sm.qs, sm.qt, tid);
+        stage_tile<T, DS, true, true, BWD_THREADS>(C + (int64_t)m0 * scl, scl, nvalid, sm.cs, sm.ct, tid);
+        stage_tile<T, DH, true, true, BWD_THREADS>(DO + (int64_t)m0 * sdl, sdl, nvalid, sm.ds, sm.dt, tid);
         if (tid < 64) {
             const int i = m0 + tid;
             const bool ok = i < L;
@@ -598,109 +732,37 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a,
             sm.lse[tid] = ok ? LSE[i] : __builtin_inff();
             sm.dhat[tid] = ok ? DELTA[i] : 0.f;
             sm.ddel[tid] = ok ? DDEL[i] : 0.f;
-            sm.rowf[tid] = ok ? ROWF[i] : 0.f;
             sm.fq[tid] = (has_f && ok) ? FF[(int64_t)i * sfl] : 0.f;
             sm.gq[tid] = G[(int64_t)ic * sgl];
+            const float rowf = ok ? ROWF[i] : 0.f;
+            const float gm = G[(int64_t)m0 * sgl];   // start of the query block
+            sm.rq[0][tid] = rowf * exp2_le0((gm - ge0) * LOG2E);
+            sm.rq[1][tid] = rowf * exp2_le0((gm - ge1) * LOG2E);
         }
         __syncthreads();
-        if (!live || m0 + 63 < k0) continue;          // every query of the tile is before every key of the wave
-        const bool pair = m0 == kblk;                 // the keys' own 64-block: pairwise decay + causal mask
-        float mid = 0.f;
-        if (!pair) mid = exp2_le0((G[(int64_t)m0 * sgl] - ge) * LOG2E);
-
-        f32x4 sc[4][2], cb[4][2], dp[4][2];
+        if (!live || m0 + 63 < k0) continue;      // every query of the tile is before every key of the wave
+        if (m0 == kblk) {
+            // apply the off-block column factors once, in fp32, before the own-block contributions
 #pragma unroll
-        for (int qb = 0; qb < 4; ++qb) {
-            const frag8<T> q0f = frag_rows<T, DH>(sm.qs, qb * 16, 0, lane);
-            const frag8<T> q1f = frag_rows<T, DH>(sm.qs, qb * 16, 1, lane);
-            const frag8<T> d0f = frag_rows<T, DH>(sm.ds, qb * 16, 0, lane);
-            const frag8<T> d1f = frag_rows<T, DH>(sm.ds, qb * 16, 1, lane);
-            const frag8<T> cf = frag_rows<T, DS>(sm.cs, qb * 16, 0, lane);
+            for (int kc = 0; kc < BWD_NC; ++kc) {
+                dgu[kc] *= colf[kc];
 #pragma unroll
-            for (int kc = 0; kc < 2; ++kc) {
-                sc[qb][kc] = mma(q1f, kf[kc][1], mma(q0f, kf[kc][0], zero4()));
-                cb[qb][kc] = mma(cf, bfr[kc], zero4());
-                dp[qb][kc] = mma(d1f, vf[kc][1], mma(d0f, vf[kc][0], zero4()));
+                for (int sb = 0; sb < 2; ++sb) dba[kc][sb] *= rk[kc];
             }
-        }
-        // sc <- P, dp <- dk operand, cb <- db operand
-#pragma unroll
-        for (int qb = 0; qb < 4; ++qb) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int qi = qb * 16 + 4 * grp + i;
-                const int qq = m0 + qi;
-                const float lq = sm.lse[qi], dh = sm.dhat[qi], dd = sm.ddel[qi], fqv = sm.fq[qi];
-                if (pair) {
-                    const float gqv = sm.gq[qi];
-#pragma unroll
-                    for (int kc = 0; kc < 2; ++kc) {
-                        const int kk = k0 + 16 * kc + lc;
-                        const bool valid = qq >= kk && qq < L;
-                        const bool strict = valid && qq > kk;
-                        const bool eye = valid && qq == kk;
-                        const float dec = valid ? exp2_le0((gqv - gk[kc]) * LOG2E) : 0.f;
-                        const float u = dec * cb[qb][kc][i];
-                        float s = sc[qb][kc][i] * scale + (fqv - fk[kc]);
-                        s = s + lam * u;
-                        const float p = valid ? fast_exp2(fmaf(s, LOG2E, -lq)) : 0.f;
-                        const float dsh = p * (dp[qb][kc][i] - dh);
-                        const float dsx = dsh - p * dd;
-                        const float dso = strict ? dsx : 0.f;
-                        dgu[kc] += dso * u;
-                        dfs[kc] += dso;
-                        sc[qb][kc][i] = p;
-                        dp[qb][kc][i] = eye ? dsd[kc] : dso;
-                        cb[qb][kc][i] = (eye ? dsd[kc] : (strict ? dsh : 0.f)) * (lam * dec);
-                    }
-                } else {
-                    const float rq = sm.rowf[qi] * mid;
-#pragma unroll
-                    for (int kc = 0; kc < 2; ++kc) {
-                        const float uc = cb[qb][kc][i] * rq;
-                        float s = sc[qb][kc][i] * scale + (fqv - fk[kc]);
-                        s = s + (lam * colf[kc]) * uc;
-                        const float p = fast_exp2(fmaf(s, LOG2E, -lq));
-                        const float dsh = p * (dp[qb][kc][i] - dh);
-                        const float dsx = dsh - p * dd;
-                        dgo[kc] += dsx * uc;
-                        dfs[kc] += dsx;
-                        sc[qb][kc][i] = p;
-                        dp[qb][kc][i] = dsx;
-                        cb[qb][kc][i] = dsh * rq;
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-#pragma unroll
-            for (int st = 0; st < 2; ++st) {
-                const frag8<T> pf = pack8<T>(sc[2 * st][kc], sc[2 * st + 1][kc]);
-                const frag8<T> kfr = pack8<T>(dp[2 * st][kc], dp[2 * st + 1][kc]);
-                const frag8<T> bf = pack8<T>(cb[2 * st][kc], cb[2 * st + 1][kc]);
-#pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    dva[kc][db] = mma(frag_trn<T>(sm.dt, db * 16, st, lane), pf, dva[kc][db]);
-                    dka[kc][db] = mma(frag_trn<T>(sm.qt, db * 16, st, lane), kfr, dka[kc][db]);
-                }
-#pragma unroll
-                for (int sb = 0; sb < 2; ++sb) {
-                    const frag8<T> ct = frag_trn<T>(sm.ct, sb * 16, st, lane);
-                    if (pair) dba[kc][sb] = mma(ct, bf, dba[kc][sb]);
-                    else dboa[kc][sb] = mma(ct, bf, dboa[kc][sb]);
-                }
-            }
+            dkv_tile<T, true>(sm, sm.rq[kblkw], lane, m0, k0, L, kf, vf, bfr, fk, rk, gk, dsd, lam, scale, dgu, dfs,
+                              dva, dka, dba);
+        } else {
+            dkv_tile<T, false>(sm, sm.rq[kblkw], lane, m0, k0, L, kf, vf, bfr, fk, rk, gk, dsd, lam, scale, dgu,
+                               dfs, dva, dka, dba);
         }
     }
     if (!live) return;
     const bool dcb32 = a.dcb_dtype == SISA_F32;
 #pragma unroll
-    for (int kc = 0; kc < 2; ++kc) {
-        const float Dgu = group_sum(dgu[kc]), Dfs = group_sum(dfs[kc]), Dgo = group_sum(dgo[kc]);
+    for (int kc = 0; kc < BWD_NC; ++kc) {
+        const float Dgu = group_sum(dgu[kc]), Dfs = group_sum(dfs[kc]);
         const int kk = k0 + 16 * kc + lc;
         if (kk >= L) continue;
-        const float rk = lam * colf[kc];
         T* dkp = (T*)a.dk.ptr + (int64_t)b * a.dk.sb + (int64_t)h * a.dk.sh + (int64_t)kk * a.dk.sl;
         T* dvp = (T*)a.dv.ptr + (int64_t)b * a.dv.sb + (int64_t)h * a.dv.sh + (int64_t)kk * a.dv.sl;
 #pragma unroll
@@ -712,7 +774,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a,
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb) {
             const int s0 = sb * 16 + 4 * grp;
-            const f32x4 r = dba[kc][sb] + rk * dboa[kc][sb];
+            const f32x4 r = dba[kc][sb];
             if (dcb32) {
                 float* p = (float*)a.db.ptr + (int64_t)b * a.db.sb + (int64_t)h * a.db.sh + (int64_t)kk * a.db.sl;
                 *reinterpret_cast<f32x4*>(p + s0) = r;
@@ -723,27 +785,26 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a,
         }
         if (grp == 0) {
             const int64_t o = (int64_t)bh * L + kk;
-            const float dgt = Dgu + colf[kc] * Dgo;
-            a.dg[o] = WS[WS_RG * BHL + o] - lam * dgt;
+            a.dg[o] = WS[WS_RG * BHL + o] - lam * Dgu;
             if (has_f) a.df[o] = WS[WS_RF * BHL + o] - Dfs;
         }
     }
 }
 
 // dlambda_h = sum over (b, t) of the per-row parts, in fp64 with a fixed reduction order (attention.py:781-783).
-__global__ __launch_bounds__(256) void dlam_kernel(const float* __restrict__ rl, float* __restrict__ dlam, int B, int H,
-                                                  int L) {
-    __shared__ double red[256];
+__global__ __launch_bounds__(1024) void dlam_kernel(const float* __restrict__ rl, float* __restrict__ dlam, int B,
+                                                   int H, int L) {
+    __shared__ double red[1024];
     const int h = blockIdx.x;
     const int64_t n = (int64_t)B * L;
     double s = 0.0;
-    for (int64_t t = threadIdx.x; t < n; t += 256) {
+    for (int64_t t = threadIdx.x; t < n; t += 1024) {
         const int64_t bb = t / L, l = t % L;
         s += (double)rl[(bb * H + h) * (int64_t)L + l];
     }
     red[threadIdx.x] = s;
     __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
+    for (int o = 512; o > 0; o >>= 1) {
         if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
         __syncthreads();
     }
@@ -760,14 +821,14 @@ int launch_fwd(const sisa_attn_fwd_args* a, hipStream_t st) {
 template <class T>
 int launch_bwd(const sisa_attn_bwd_args* a, hipStream_t st) {
     dim3 grid((unsigned)sisa::cdiv(a->L, 128), (unsigned)(a->B * a->H));
-    attn_bwd_dq_kernel<T><<<grid, 256, 0, st>>>(*a, 0.125f);
+    attn_bwd_dq_kernel<T><<<grid, BWD_THREADS, 0, st>>>(*a, 0.125f);
     int rc = sisa::launch_status("sisa_attn_bwd (dq)");
     if (rc) return rc;
-    attn_bwd_dkv_kernel<T><<<grid, 256, 0, st>>>(*a, 0.125f);
+    attn_bwd_dkv_kernel<T><<<grid, BWD_THREADS, 0, st>>>(*a, 0.125f);
     rc = sisa::launch_status("sisa_attn_bwd (dkv)");
     if (rc) return rc;
     const int64_t BHL = (int64_t)a->B * a->H * a->L;
-    dlam_kernel<<<a->H, 256, 0, st>>>((const float*)a->workspace + WS_RL * BHL, a->dlam, a->B, a->H, a->L);
+    dlam_kernel<<<a->H, 1024, 0, st>>>((const float*)a->workspace + WS_RL * BHL, a->dlam, a->B, a->H, a->L);
     return sisa::launch_status("sisa_attn_bwd (dlam)");
 }
 

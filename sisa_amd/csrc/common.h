@@ -67,19 +67,37 @@ template <class T> SISA_DEV float frag_sum(const frag8<T>& f) {
 SISA_DEV float exp2_le0(float x) { return __builtin_amdgcn_exp2f(x > 0.f ? 0.f : x); }
 SISA_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// NaN-propagating max (a NaN score must poison its row).
+// NaN-propagating max.
 SISA_DEV float nmax(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b); }
 
-// Cross-lane butterfly over the four lane groups (lanes l, l^16, l^32, l^48): every lane gets the result.
+SISA_DEV f32x4 lds4f(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+
+// Cross-lane butterfly over the four lane groups (lanes l, l^16, l^32, l^48) with the gfx950 permlane swaps:
+// every lane of a group gets the same result (the pairwise combination order is identical in all four lanes).
+SISA_DEV float xswap32_max(float x) {
+    const unsigned u = __float_as_uint(x);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 SISA_DEV float group_max(float x) {
-    x = nmax(x, __shfl_xor(x, 16));
-    x = nmax(x, __shfl_xor(x, 32));
-    return x;
+    x = xswap32_max(x);
+    const unsigned u = __float_as_uint(x);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 SISA_DEV float group_sum(float x) {
-    x += __shfl_xor(x, 16);
-    x += __shfl_xor(x, 32);
-    return x;
+    unsigned u = __float_as_uint(x);
+    auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    u = __float_as_uint(x);
+    r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// Value of lane (l % 16) (lane group 0) broadcast to the four lanes of its group.
+SISA_DEV float group_bcast0(float x, int lane) {
+    const unsigned u = __float_as_uint(x);
+    const unsigned v = (unsigned)__builtin_amdgcn_ds_bpermute((lane & 15) << 2, (int)u);
+    return __uint_as_float(v);
 }
 
 // 16-byte / 8-byte loads of 8 or 4 consecutive elements.
@@ -107,12 +125,12 @@ template <class T> SISA_DEV vec4<T> to_vec4(f32x4 x) { return __builtin_convertv
 
 // Cooperative staging of a (64 x C) tile of a sequence-major tensor (rows = positions, C in {32, 64} contiguous
 // features) into LDS: row-major X[r][f] (stride C+LDS_PAD) and/or transposed Xt[f][r] (stride 64+LDS_PAD).
-// Rows >= nvalid are zero. 256 threads; each thread moves 4 rows x 4 features.
-template <class T, int C, bool ROW, bool TRN>
+// Rows >= nvalid are zero. NTH threads; each thread moves 4 rows x 4 features.
+template <class T, int C, bool ROW, bool TRN, int NTH = 256>
 SISA_DEV void stage_tile(const T* __restrict__ src, int64_t srow, int nvalid, T* __restrict__ X, T* __restrict__ Xt,
                          int tid) {
     constexpr int NBLK = 16 * (C / 4);
-    for (int blk = tid; blk < NBLK; blk += 256) {
+    for (int blk = tid; blk < NBLK; blk += NTH) {
         const int rq = blk / (C / 4);
         const int cq = blk % (C / 4);
         vec4<T> v[4];
