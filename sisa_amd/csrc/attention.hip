@@ -10,12 +10,12 @@
 // before log2e, the self-normalised fp32 o'' for the exact delta, and the delta-free diagonal dS_tt. The kernel
 // structure (tiles, wave ownership, MFMA layouts, LDS staging) is this library's own.
 //
-// Work decomposition (256 threads = 4 waves per workgroup):
-//   forward, dq kernel: a workgroup owns 128 consecutive queries, each wave 32 of them (two 16-query column groups);
-//     key tiles of 64 positions are staged in LDS. Scores are computed transposed (S^T = K Q^T) so that one lane owns
-//     one query's softmax state and the 16x16 C blocks of S^T are directly the B fragments of O^T += V^T P^T.
-//   dkv kernel: a workgroup owns 128 consecutive keys, each wave 32; query tiles of 64 positions are staged.
-//     Scores are computed as S = Q K^T so that one lane owns one key's column sums.
+// Work decomposition (512 threads = 8 waves per workgroup, two workgroups per CU):
+//   forward, dq kernel: a workgroup owns 128 consecutive queries, each wave 16 of them; key tiles of 64 positions
+//     are staged row-major in LDS (the next tile's global loads are in flight during the current tile's math).
+//   dkv kernel: a workgroup owns 128 consecutive keys, each wave 16; query tiles of 64 positions are staged.
+//   Operands of the sequence-contracted products (P V, dS K, ...) are read from the row-major tiles with the gfx950
+//   LDS transpose read, so no transposed copy is ever stored.
 //   Ownership is exclusive (no atomics): dq/dc by query tiles, dk/dv/db/dg/dF by key tiles.
 #include "common.h"
 #include "host.h"
@@ -25,6 +25,11 @@ namespace {
 constexpr int DH = 64;   // d_head
 constexpr int DS = 32;   // d_state
 constexpr int BLK = 64;  // decay-factor block (rowf/colf anchors)
+
+// Every attention kernel: 8 waves per workgroup, 16 rows (one column group of the MFMA block) per wave, 128 rows per
+// workgroup, 64-position tiles of the other operand staged row-major in LDS; two workgroups fit on a CU.
+constexpr int NW = 8;
+constexpr int NTH = 64 * NW;
 
 // ------------------------------------------------------------------------------------------------ factors
 // rowf_t = exp2(min((g_t - g_{block start})*log2e, 0)), colf_t = exp2(min((g_{block end} - g_t)*log2e, 0)), and the
@@ -53,101 +58,101 @@ __global__ __launch_bounds__(64) void factors_kernel(sisa_factors_args a) {
     const int tp = tc - 1 > 0 ? tc - 1 : 0;
     const float prv = G[(int64_t)tp * sgl];
     float inc = (msk && t > 0) ? g - prv : -__builtin_inff();
-    // wave max (64 lanes)
     for (int o = 32; o > 0; o >>= 1) inc = nmax(inc, __shfl_xor(inc, o));
     if (threadIdx.x == 0) a.mono[(int64_t)bh * gridDim.x + p] = inc;
 }
 
+template <class T, class TO>
+SISA_DEV void store_row4(TO* p, f32x4 v) {
+    store4<TO>(p, to_vec4<TO>(v));
+}
+
 // ------------------------------------------------------------------------------------------------ forward
-// Key tiles are staged once per workgroup; each wave then runs one of two code paths, chosen per tile and wave
-// (uniform branch): off-block tiles (every key in an earlier 64-block than every query of the wave; chunk-factored
-// decay, no masks) or the wave's own block (pairwise decay and the causal mask). Column groups of 16 queries are
-// processed one after the other to keep the live register set small (two workgroups per CU).
+// Scores are computed transposed (S^T = K Q^T): a lane owns one query's softmax state and the 16x16 C blocks of S^T
+// are directly the B fragments of O^T += V^T P^T. Per tile and wave one of two code paths runs (uniform branch):
+// off-block tiles (every key in an earlier 64-block than the wave's queries; chunk-factored decay, no masks) or the
+// wave's own block (pairwise decay and the causal mask).
 template <class T>
 struct FwdLds {
-    T ks[64 * (DH + LDS_PAD)];          // K tile, row-major
-    T bs[64 * (DS + LDS_PAD)];          // B~ tile, row-major
-    T vt[(DH + 16) * (64 + LDS_PAD)];   // V tile transposed; row DH is all ones (sum of the rounded weights), DH+1.. 0
-    float fk[64], gk[64];               // F and g at the tile's keys
-    float cfm[2][64];                   // colf * mid for the workgroup's two query blocks
+    T ks[64 * (DH + LDS_PAD)];   // K tile
+    T bs[64 * (DS + LDS_PAD)];   // B~ tile
+    T vs[64 * (DH + LDS_PAD)];   // V tile
+    float fk[64], gk[64];        // F and g at the tile's keys
+    float cfm[2][64];            // colf * mid for the workgroup's two query blocks
 };
 
 template <class T, bool DIAG>
-SISA_DEV void fwd_tile(const FwdLds<T>& sm, const float* cfm, int lane, int n0, int q0, int L,
-                       const frag8<T> (&qf)[2][2], const frag8<T> (&cfr)[2], const float (&fq)[2],
-                       const float (&rs)[2], const float (&gq)[2], float lam, float scale, float (&m)[2],
-                       float (&l)[2], f32x4 (&acc)[2][5]) {
+SISA_DEV void fwd_tile(const FwdLds<T>& sm, const float* cfm, int lane, int n0, int q0, int L, const frag8<T> (&qf)[2],
+                       const frag8<T>& cfr, const frag8<T>& onesf, float fq, float rs, float gq, float lam, float scale,
+                       float& m, float& l, f32x4 (&acc)[5]) {
     const int grp = lane >> 4, lc = lane & 15;
+    const int qq = q0 + lc;
+    f32x4 sc[4], cb[4];
 #pragma unroll
-    for (int cq = 0; cq < 2; ++cq) {
-        __builtin_amdgcn_sched_barrier(0);   // one column group at a time: bounded live registers
-        f32x4 sc[4], cb[4];
+    for (int kb = 0; kb < 4; ++kb) {
+        const frag8<T> k0 = frag_rows<T, DH>(sm.ks, kb * 16, 0, lane);
+        const frag8<T> k1 = frag_rows<T, DH>(sm.ks, kb * 16, 1, lane);
+        const frag8<T> bf = frag_rows<T, DS>(sm.bs, kb * 16, 0, lane);
+        sc[kb] = mma(k1, qf[1], mma(k0, qf[0], zero4()));
+        cb[kb] = mma(bf, cfr, zero4());
+    }
+    float mloc = -__builtin_inff();
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            const frag8<T> k0 = frag_rows<T, DH>(sm.ks, kb * 16, 0, lane);
-            const frag8<T> k1 = frag_rows<T, DH>(sm.ks, kb * 16, 1, lane);
-            const frag8<T> bf = frag_rows<T, DS>(sm.bs, kb * 16, 0, lane);
-            sc[kb] = mma(k1, qf[cq][1], mma(k0, qf[cq][0], zero4()));
-            cb[kb] = mma(bf, cfr[cq], zero4());
-        }
-        const int qq = q0 + 16 * cq + lc;
-        float mloc = -__builtin_inff();
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            const int j0 = kb * 16 + 4 * grp;
-            const f32x4 fk = lds4f(&sm.fk[j0]);
-            if (DIAG) {
-                const f32x4 gk = lds4f(&sm.gk[j0]);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int jj = n0 + j0 + i;
-                    const bool valid = jj <= qq && jj < L;
-                    const float dec = valid ? exp2_le0((gq[cq] - gk[i]) * LOG2E) : 0.f;
-                    float s = sc[kb][i] * scale + (fq[cq] - fk[i]);
-                    s = s + lam * (dec * cb[kb][i]);
-                    s = valid ? s : -__builtin_inff();
-                    sc[kb][i] = s;
-                    mloc = fmaxf(mloc, s);
-                }
-            } else {
-                const f32x4 cf = lds4f(&cfm[j0]);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float s = sc[kb][i] * scale + (fq[cq] - fk[i]);
-                    s = s + rs[cq] * (cb[kb][i] * cf[i]);
-                    sc[kb][i] = s;
-                    mloc = fmaxf(mloc, s);
-                }
-            }
-        }
-        // online softmax in log2 units; a NaN score reaches l through its exponential
-        const float mn = fmaxf(m[cq], group_max(mloc) * LOG2E);
-        const float mu = (mn == -__builtin_inff()) ? 0.f : mn;
-        const float corr = fast_exp2(m[cq] - mu);
-        m[cq] = mu;
-        float ls = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < 4; ++kb) {
+        const int j0 = kb * 16 + 4 * grp;
+        const f32x4 fk = lds4f(&sm.fk[j0]);
+        if (DIAG) {
+            const f32x4 gk = lds4f(&sm.gk[j0]);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float pe = fast_exp2(fmaf(sc[kb][i], LOG2E, -mu));
-                sc[kb][i] = pe;
-                ls += pe;
+                const int jj = n0 + j0 + i;
+                const bool valid = jj <= qq && jj < L;
+                const float dec = valid ? exp2_le0((gq - gk[i]) * LOG2E) : 0.f;
+                float s = sc[kb][i] * scale + (fq - fk[i]);
+                s = s + lam * (dec * cb[kb][i]);
+                s = valid ? s : -__builtin_inff();
+                sc[kb][i] = s;
+                mloc = fmaxf(mloc, s);
             }
-        l[cq] = l[cq] * corr + ls;
+        } else {
+            const f32x4 cf = lds4f(&cfm[j0]);
 #pragma unroll
-        for (int db = 0; db < 5; ++db) acc[cq][db] *= corr;
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            const frag8<T> pf = pack8<T>(sc[2 * st], sc[2 * st + 1]);
-#pragma unroll
-            for (int db = 0; db < 5; ++db) acc[cq][db] = mma(frag_trn<T>(sm.vt, db * 16, st, lane), pf, acc[cq][db]);
+            for (int i = 0; i < 4; ++i) {
+                float s = sc[kb][i] * scale + (fq - fk[i]);
+                s = s + rs * (cb[kb][i] * cf[i]);
+                sc[kb][i] = s;
+                mloc = fmaxf(mloc, s);
+            }
         }
+    }
+    // online softmax in log2 units; a NaN score reaches l through its exponential
+    const float mn = fmaxf(m, group_max(mloc) * LOG2E);
+    const float mu = (mn == -__builtin_inff()) ? 0.f : mn;
+    const float corr = fast_exp2(m - mu);
+    m = mu;
+    float ls = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float pe = fast_exp2(fmaf(sc[kb][i], LOG2E, -mu));
+            sc[kb][i] = pe;
+            ls += pe;
+        }
+    l = l * corr + ls;
+#pragma unroll
+    for (int db = 0; db < 5; ++db) acc[db] *= corr;
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+        const frag8<T> pf = pack8<T>(sc[2 * st], sc[2 * st + 1]);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) acc[db] = mma(frag_tr<T, DH>(sm.vs, db * 16, st, lane), pf, acc[db]);
+        acc[4] = mma(onesf, pf, acc[4]);   // row 0 of block 4: the sum of the rounded weights (o'' normaliser)
     }
 }
 
 template <class T>
-__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(sisa_attn_fwd_args a, float scale) {
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void attn_fwd_kernel(sisa_attn_fwd_args a, float scale) {
     __shared__ FwdLds<T> sm;
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -171,44 +176,42 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(sisa_attn_fwd_args a, 
     const int64_t sfl = has_f ? a.f.sl : 0;
 
     const int tile0 = tile * 128;
-    const int q0 = tile0 + 32 * w;
+    const int q0 = tile0 + 16 * w;
+    const int qblk = w >> 2;                       // which of the workgroup's two query blocks
     const bool live = q0 < L;
-    // anchors g at the starts of the workgroup's two query blocks
     const float ga0 = G[(int64_t)(tile0 < L ? tile0 : L - 1) * sgl];
     const float ga1 = G[(int64_t)(tile0 + 64 < L ? tile0 + 64 : L - 1) * sgl];
 
-    for (int i = tid; i < 16 * (64 + LDS_PAD); i += 256) sm.vt[DH * (64 + LDS_PAD) + i] = (T)(i < 64 ? 1.f : 0.f);
-
-    frag8<T> qf[2][2], cfr[2];
-    float fq[2], rs[2], gq[2];
-#pragma unroll
-    for (int cq = 0; cq < 2; ++cq) {
-        const int qq = q0 + 16 * cq + lc;
+    frag8<T> qf[2], cfr;
+    float fq, rs, gq;
+    {
+        const int qq = q0 + lc;
         const bool ok = qq < L;
-        const int qc = ok ? qq : L - 1;
-        qf[cq][0] = ok ? load8<T>(Q + (int64_t)qq * sql + 8 * grp) : zero8<T>();
-        qf[cq][1] = ok ? load8<T>(Q + (int64_t)qq * sql + 32 + 8 * grp) : zero8<T>();
-        cfr[cq] = ok ? load8<T>(C + (int64_t)qq * scl + 8 * grp) : zero8<T>();
-        fq[cq] = (has_f && ok) ? FF[(int64_t)qq * sfl] : 0.f;
-        rs[cq] = lam * (ok ? ROWF[qq] : 0.f);
-        gq[cq] = G[(int64_t)qc * sgl];
+        qf[0] = ok ? load8<T>(Q + (int64_t)qq * sql + 8 * grp) : zero8<T>();
+        qf[1] = ok ? load8<T>(Q + (int64_t)qq * sql + 32 + 8 * grp) : zero8<T>();
+        cfr = ok ? load8<T>(C + (int64_t)qq * scl + 8 * grp) : zero8<T>();
+        fq = (has_f && ok) ? FF[(int64_t)qq * sfl] : 0.f;
+        rs = lam * (ok ? ROWF[qq] : 0.f);
+        gq = G[(int64_t)(ok ? qq : L - 1) * sgl];
     }
+    const frag8<T> onesf = ones_row_frag<T>(lane);
 
-    float m[2] = {-__builtin_inff(), -__builtin_inff()};
-    float l[2] = {0.f, 0.f};
-    f32x4 acc[2][5];
+    float m = -__builtin_inff(), l = 0.f;
+    f32x4 acc[5];
 #pragma unroll
-    for (int cq = 0; cq < 2; ++cq)
-#pragma unroll
-        for (int db = 0; db < 5; ++db) acc[cq][db] = zero4();
+    for (int db = 0; db < 5; ++db) acc[db] = zero4();
 
+    TileStage<T, DH, NTH> stk, stv;
+    TileStage<T, DS, NTH> stb;
     const int kend = (tile0 + 128 < L) ? tile0 + 128 : L;
+    stk.load(K, skl, L < 64 ? L : 64, tid);
+    stv.load(V, svl, L < 64 ? L : 64, tid);
+    stb.load(Bm, sbl, L < 64 ? L : 64, tid);
     for (int n0 = 0; n0 < kend; n0 += 64) {
         __syncthreads();
-        const int nvalid = (L - n0 < 64) ? L - n0 : 64;
-        stage_tile<T, DH, true, false>(K + (int64_t)n0 * skl, skl, nvalid, sm.ks, nullptr, tid);
-        stage_tile<T, DS, true, false>(Bm + (int64_t)n0 * sbl, sbl, nvalid, sm.bs, nullptr, tid);
-        stage_tile<T, DH, false, true>(V + (int64_t)n0 * svl, svl, nvalid, nullptr, sm.vt, tid);
+        stk.store(sm.ks, tid);
+        stv.store(sm.vs, tid);
+        stb.store(sm.bs, tid);
         if (tid < 64) {
             const int j = n0 + tid;
             const int jc = j < L ? j : L - 1;
@@ -220,31 +223,35 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(sisa_attn_fwd_args a, 
             sm.cfm[1][tid] = cf * exp2_le0((ga1 - ge) * LOG2E);
         }
         __syncthreads();
+        const int n1 = n0 + 64;
+        if (n1 < kend) {                           // next tile's loads are in flight during this tile's math
+            const int nv = (L - n1 < 64) ? L - n1 : 64;
+            stk.load(K + (int64_t)n1 * skl, skl, nv, tid);
+            stv.load(V + (int64_t)n1 * svl, svl, nv, tid);
+            stb.load(Bm + (int64_t)n1 * sbl, sbl, nv, tid);
+        }
         if (!live) continue;
         if (n0 + 63 < q0)
-            fwd_tile<T, false>(sm, sm.cfm[w >> 1], lane, n0, q0, L, qf, cfr, fq, rs, gq, lam, scale, m, l, acc);
-        else if (n0 <= q0 + 31)
-            fwd_tile<T, true>(sm, sm.cfm[w >> 1], lane, n0, q0, L, qf, cfr, fq, rs, gq, lam, scale, m, l, acc);
+            fwd_tile<T, false>(sm, sm.cfm[qblk], lane, n0, q0, L, qf, cfr, onesf, fq, rs, gq, lam, scale, m, l, acc);
+        else if (n0 <= q0 + 15)
+            fwd_tile<T, true>(sm, sm.cfm[qblk], lane, n0, q0, L, qf, cfr, onesf, fq, rs, gq, lam, scale, m, l, acc);
     }
     if (!live) return;
     T* O = (T*)a.o.ptr + (int64_t)b * a.o.sb + (int64_t)h * a.o.sh;
+    const float lt = group_sum(l);
+    const float lbt = group_bcast0(acc[4][0], lane);   // row 0 of block 4: sum of the rounded weights
+    const int qq = q0 + lc;
+    if (qq >= L) return;
+    const float ls = (lt == 0.f) ? 1.f : lt;
 #pragma unroll
-    for (int cq = 0; cq < 2; ++cq) {
-        const float lt = group_sum(l[cq]);
-        const float lbt = group_bcast0(acc[cq][4][0], lane);   // row DH of O^T: sum of the rounded weights
-        const int qq = q0 + 16 * cq + lc;
-        if (qq >= L) continue;
-        const float ls = (lt == 0.f) ? 1.f : lt;
+    for (int db = 0; db < 4; ++db) store4<T>(O + (int64_t)qq * a.o.sl + db * 16 + 4 * grp, to_vec4<T>(acc[db] / ls));
+    if (a.o32) {
+        const float lbs = (lbt == 0.f) ? 1.f : lbt;
+        float* O32 = a.o32 + ((int64_t)bh * L + qq) * DH;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) store4<T>(O + (int64_t)qq * a.o.sl + db * 16 + 4 * grp, to_vec4<T>(acc[cq][db] / ls));
-        if (a.o32) {
-            const float lbs = (lbt == 0.f) ? 1.f : lbt;
-            float* O32 = a.o32 + ((int64_t)bh * L + qq) * DH;
-#pragma unroll
-            for (int db = 0; db < 4; ++db) *reinterpret_cast<f32x4*>(O32 + db * 16 + 4 * grp) = acc[cq][db] / lbs;
-        }
-        if (grp == 0) a.lse[(int64_t)bh * L + qq] = m[cq] + __builtin_amdgcn_logf(ls);
+        for (int db = 0; db < 4; ++db) *reinterpret_cast<f32x4*>(O32 + db * 16 + 4 * grp) = acc[db] / lbs;
     }
+    if (grp == 0) a.lse[(int64_t)bh * L + qq] = m + __builtin_amdgcn_logf(ls);
 }
 
 // ------------------------------------------------------------------------------------------------ backward: dq
@@ -253,121 +260,103 @@ enum { WS_DELTA = 0, WS_DDEL, WS_DSD, WS_RG, WS_RL, WS_RF, WS_N };
 
 template <class T>
 struct DqLds {
-    T ks[64 * (DH + LDS_PAD)];   // K, row-major (scores)
-    T kt[DH * (64 + LDS_PAD)];   // K, transposed (dq)
-    T vs[64 * (DH + LDS_PAD)];   // V, row-major (dP)
-    T bs[64 * (DS + LDS_PAD)];   // B~, row-major (scores)
-    T bt[DS * (64 + LDS_PAD)];   // B~, transposed (dc)
+    T ks[64 * (DH + LDS_PAD)];   // K (scores; transposed reads for dq)
+    T vs[64 * (DH + LDS_PAD)];   // V (dP)
+    T bs[64 * (DS + LDS_PAD)];   // B~ (scores; transposed reads for dc)
     float fk[64], gk[64];
     float cfm[2][64];            // colf * mid for the workgroup's two query blocks
 };
 
 // Per-query row sums of the dq kernel (diagonal excluded): xa = sum dS^ u, ya = sum P u, wa = D = sum dS^,
 // za = Z = sum P, ptt = P_tt, dptt = dP_tt, xd = cb_tt. Off-block tiles accumulate xa, ya without the row factor
-// rowf; a wave's own-block tile is its last one, and scale_offblock() applies rowf (and lam*rowf to dc) before it.
+// rowf; a wave's own-block tile is its last one, and rowf (lam*rowf for dc) is applied once before it.
 struct RowSums {
     float xa, ya, wa, za, ptt, dptt, xd;
 };
 
-// Backward kernels: 8 waves per workgroup, 16 rows (one column group) per wave, so that two workgroups fit on a CU.
-constexpr int BWD_NC = 1;                      // column groups of 16 rows per wave
-constexpr int BWD_WAVES = 8 / BWD_NC;          // waves per workgroup (128 rows)
-constexpr int BWD_THREADS = 64 * BWD_WAVES;
-
 template <class T, bool DIAG>
-SISA_DEV void dq_tile(const DqLds<T>& sm, const float* cfm, int lane, int n0, int q0, int L,
-                      const frag8<T> (&qf)[BWD_NC][2], const frag8<T> (&cfr)[BWD_NC],
-                      const frag8<T> (&dof)[BWD_NC][2], const float (&fq)[BWD_NC], const float (&rs)[BWD_NC],
-                      const float (&gq)[BWD_NC], const float (&lse)[BWD_NC], const float (&dhat)[BWD_NC], float lam,
-                      float scale, RowSums (&rsum)[BWD_NC], f32x4 (&dqa)[BWD_NC][4], f32x4 (&dca)[BWD_NC][2]) {
+SISA_DEV void dq_tile(const DqLds<T>& sm, const float* cfm, int lane, int n0, int q0, int L, const frag8<T> (&qf)[2],
+                      const frag8<T>& cfr, const frag8<T> (&dof)[2], float fq, float rs, float gq, float lse,
+                      float dhat, float lam, float scale, RowSums& R, f32x4 (&dqa)[4], f32x4 (&dca)[2]) {
     const int grp = lane >> 4, lc = lane & 15;
+    const int qq = q0 + lc;
 #pragma unroll
-    for (int cq = 0; cq < BWD_NC; ++cq) {
-        const int qq = q0 + 16 * cq + lc;
-        RowSums& R = rsum[cq];
+    for (int st = 0; st < 2; ++st) {           // 32 keys (one K-step of the dq/dc products) at a time
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4 sc[2], cb[2], dp[2];
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {           // 32 keys (one K-step of the dq/dc products) at a time
-            __builtin_amdgcn_sched_barrier(0);
-            f32x4 sc[2], cb[2], dp[2];
+        for (int hb = 0; hb < 2; ++hb) {
+            const int kb = 2 * st + hb;
+            const frag8<T> k0 = frag_rows<T, DH>(sm.ks, kb * 16, 0, lane);
+            const frag8<T> k1 = frag_rows<T, DH>(sm.ks, kb * 16, 1, lane);
+            const frag8<T> v0 = frag_rows<T, DH>(sm.vs, kb * 16, 0, lane);
+            const frag8<T> v1 = frag_rows<T, DH>(sm.vs, kb * 16, 1, lane);
+            const frag8<T> bf = frag_rows<T, DS>(sm.bs, kb * 16, 0, lane);
+            sc[hb] = mma(k1, qf[1], mma(k0, qf[0], zero4()));
+            cb[hb] = mma(bf, cfr, zero4());
+            dp[hb] = mma(v1, dof[1], mma(v0, dof[0], zero4()));
+        }
+        // sc <- dq operand (dS^), cb <- dc operand
 #pragma unroll
-            for (int hb = 0; hb < 2; ++hb) {
-                const int kb = 2 * st + hb;
-                const frag8<T> k0 = frag_rows<T, DH>(sm.ks, kb * 16, 0, lane);
-                const frag8<T> k1 = frag_rows<T, DH>(sm.ks, kb * 16, 1, lane);
-                const frag8<T> v0 = frag_rows<T, DH>(sm.vs, kb * 16, 0, lane);
-                const frag8<T> v1 = frag_rows<T, DH>(sm.vs, kb * 16, 1, lane);
-                const frag8<T> bf = frag_rows<T, DS>(sm.bs, kb * 16, 0, lane);
-                sc[hb] = mma(k1, qf[cq][1], mma(k0, qf[cq][0], zero4()));
-                cb[hb] = mma(bf, cfr[cq], zero4());
-                dp[hb] = mma(v1, dof[cq][1], mma(v0, dof[cq][0], zero4()));
-            }
-            // sc <- dq operand (dS^), cb <- dc operand
+        for (int hb = 0; hb < 2; ++hb) {
+            const int j0 = (2 * st + hb) * 16 + 4 * grp;
+            const f32x4 fk = lds4f(&sm.fk[j0]);
+            if (DIAG) {
+                const f32x4 gk = lds4f(&sm.gk[j0]);
 #pragma unroll
-            for (int hb = 0; hb < 2; ++hb) {
-                const int j0 = (2 * st + hb) * 16 + 4 * grp;
-                const f32x4 fk = lds4f(&sm.fk[j0]);
-                if (DIAG) {
-                    const f32x4 gk = lds4f(&sm.gk[j0]);
+                for (int i = 0; i < 4; ++i) {
+                    const int jj = n0 + j0 + i;
+                    const bool valid = jj <= qq && jj < L && qq < L;
+                    const bool eye = valid && jj == qq;
+                    const float dec = valid ? exp2_le0((gq - gk[i]) * LOG2E) : 0.f;
+                    const float cbv = cb[hb][i];
+                    const float u = dec * cbv;
+                    float s = sc[hb][i] * scale + (fq - fk[i]);
+                    s = s + lam * u;
+                    const float pr = valid ? fast_exp2(fmaf(s, LOG2E, -lse)) : 0.f;
+                    const float dpv = dp[hb][i];
+                    const float ds = pr * (dpv - dhat);
+                    const float dso = eye ? 0.f : ds;
+                    R.ptt += eye ? pr : 0.f;
+                    R.dptt += eye ? dpv : 0.f;
+                    R.xd += eye ? cbv : 0.f;
+                    const float po = eye ? 0.f : pr;
+                    R.za += po;
+                    R.ya += po * u;
+                    R.wa += dso;
+                    R.xa += dso * u;
+                    sc[hb][i] = dso;
+                    cb[hb][i] = dso * (lam * dec);
+                }
+            } else {
+                const f32x4 cf = lds4f(&cfm[j0]);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int jj = n0 + j0 + i;
-                        const bool valid = jj <= qq && jj < L && qq < L;
-                        const bool eye = valid && jj == qq;
-                        const float dec = valid ? exp2_le0((gq[cq] - gk[i]) * LOG2E) : 0.f;
-                        const float cbv = cb[hb][i];
-                        const float u = dec * cbv;
-                        float s = sc[hb][i] * scale + (fq[cq] - fk[i]);
-                        s = s + lam * u;
-                        const float pr = valid ? fast_exp2(fmaf(s, LOG2E, -lse[cq])) : 0.f;
-                        const float dpv = dp[hb][i];
-                        const float ds = pr * (dpv - dhat[cq]);
-                        const float dso = eye ? 0.f : ds;
-                        R.ptt += eye ? pr : 0.f;
-                        R.dptt += eye ? dpv : 0.f;
-                        R.xd += eye ? cbv : 0.f;
-                        const float po = eye ? 0.f : pr;
-                        R.za += po;
-                        R.ya += po * u;
-                        R.wa += dso;
-                        R.xa += dso * u;
-                        sc[hb][i] = dso;
-                        cb[hb][i] = dso * (lam * dec);
-                    }
-                } else {
-                    const f32x4 cf = lds4f(&cfm[j0]);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float uc = cb[hb][i] * cf[i];
-                        float s = sc[hb][i] * scale + (fq[cq] - fk[i]);
-                        s = s + rs[cq] * uc;
-                        const float pr = fast_exp2(fmaf(s, LOG2E, -lse[cq]));
-                        const float ds = pr * (dp[hb][i] - dhat[cq]);
-                        R.xa += ds * uc;
-                        R.ya += pr * uc;
-                        R.za += pr;
-                        R.wa += ds;
-                        sc[hb][i] = ds;
-                        cb[hb][i] = ds * cf[i];
-                    }
+                for (int i = 0; i < 4; ++i) {
+                    const float uc = cb[hb][i] * cf[i];
+                    float s = sc[hb][i] * scale + (fq - fk[i]);
+                    s = s + rs * uc;
+                    const float pr = fast_exp2(fmaf(s, LOG2E, -lse));
+                    const float ds = pr * (dp[hb][i] - dhat);
+                    R.xa += ds * uc;
+                    R.ya += pr * uc;
+                    R.za += pr;
+                    R.wa += ds;
+                    sc[hb][i] = ds;
+                    cb[hb][i] = ds * cf[i];
                 }
             }
-            const frag8<T> dsf = pack8<T>(sc[0], sc[1]);
-            const frag8<T> wf = pack8<T>(cb[0], cb[1]);
-#pragma unroll
-            for (int db = 0; db < 4; ++db) dqa[cq][db] = mma(frag_trn<T>(sm.kt, db * 16, st, lane), dsf, dqa[cq][db]);
-#pragma unroll
-            for (int sb = 0; sb < 2; ++sb) dca[cq][sb] = mma(frag_trn<T>(sm.bt, sb * 16, st, lane), wf, dca[cq][sb]);
         }
+        const frag8<T> dsf = pack8<T>(sc[0], sc[1]);
+        const frag8<T> wf = pack8<T>(cb[0], cb[1]);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) dqa[db] = mma(frag_tr<T, DH>(sm.ks, db * 16, st, lane), dsf, dqa[db]);
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) dca[sb] = mma(frag_tr<T, DS>(sm.bs, sb * 16, st, lane), wf, dca[sb]);
     }
 }
 
-template <class T, class TO>
-SISA_DEV void store_row4(TO* p, f32x4 v) {
-    store4<TO>(p, to_vec4<TO>(v));
-}
-
 template <class T>
-__global__ __launch_bounds__(BWD_THREADS, 2) void attn_bwd_dq_kernel(sisa_attn_bwd_args a, float scale) {
+__global__ __launch_bounds__(NTH, 2) void attn_bwd_dq_kernel(sisa_attn_bwd_args a, float scale) {
     __shared__ DqLds<T> sm;
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -396,25 +385,22 @@ __global__ __launch_bounds__(BWD_THREADS, 2) void attn_bwd_dq_kernel(sisa_attn_b
     float* WS = (float*)a.workspace;
 
     const int tile0 = tile * 128;
-    const int q0 = tile0 + 16 * BWD_NC * w;
-    const int qend = q0 + 16 * BWD_NC - 1;
-    const int qblk = (w * BWD_NC) >> 2;           // which of the workgroup's two query blocks
+    const int q0 = tile0 + 16 * w;
+    const int qblk = w >> 2;
     const bool live = q0 < L;
     const float ga0 = G[(int64_t)(tile0 < L ? tile0 : L - 1) * sgl];
     const float ga1 = G[(int64_t)(tile0 + 64 < L ? tile0 + 64 : L - 1) * sgl];
 
-    frag8<T> qf[BWD_NC][2], cfr[BWD_NC], dof[BWD_NC][2];
-    float fq[BWD_NC], rowfq[BWD_NC], rs[BWD_NC], gq[BWD_NC], lse[BWD_NC], dhat[BWD_NC];
-#pragma unroll
-    for (int cq = 0; cq < BWD_NC; ++cq) {
-        const int qq = q0 + 16 * cq + lc;
+    frag8<T> qf[2], cfr, dof[2];
+    float fq, rowfq, rs, gq, lse, dhat;
+    {
+        const int qq = q0 + lc;
         const bool ok = qq < L;
-        const int qc = ok ? qq : L - 1;
         float part = 0.f;
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
-            qf[cq][st] = ok ? load8<T>(Q + (int64_t)qq * a.q.sl + 32 * st + 8 * grp) : zero8<T>();
-            dof[cq][st] = ok ? load8<T>(DO + (int64_t)qq * a.dout.sl + 32 * st + 8 * grp) : zero8<T>();
+            qf[st] = ok ? load8<T>(Q + (int64_t)qq * a.q.sl + 32 * st + 8 * grp) : zero8<T>();
+            dof[st] = ok ? load8<T>(DO + (int64_t)qq * a.dout.sl + 32 * st + 8 * grp) : zero8<T>();
             if (ok) {
                 const frag8<T> ov = load8<T>(O + (int64_t)qq * a.o.sl + 32 * st + 8 * grp);
                 f32x4 o32a = zero4(), o32b = zero4();
@@ -431,37 +417,36 @@ __global__ __launch_bounds__(BWD_THREADS, 2) void attn_bwd_dq_kernel(sisa_attn_b
                         const float o2 = j < 4 ? o32a[j] : o32b[j - 4];
                         o = (fabsf(o2 - o) <= 3.0517578125e-05f * fabsf(o)) ? o : o2;
                     }
-                    part += o * (float)dof[cq][st][j];
+                    part += o * (float)dof[st][j];
                 }
             }
         }
-        dhat[cq] = group_sum(part);
-        cfr[cq] = ok ? load8<T>(C + (int64_t)qq * a.c.sl + 8 * grp) : zero8<T>();
-        fq[cq] = (has_f && ok) ? FF[(int64_t)qq * sfl] : 0.f;
-        rowfq[cq] = ok ? ROWF[qq] : 0.f;
-        rs[cq] = lam * rowfq[cq];
-        gq[cq] = G[(int64_t)qc * sgl];
-        lse[cq] = ok ? LSE[qq] : __builtin_inff();
+        dhat = group_sum(part);
+        cfr = ok ? load8<T>(C + (int64_t)qq * a.c.sl + 8 * grp) : zero8<T>();
+        fq = (has_f && ok) ? FF[(int64_t)qq * sfl] : 0.f;
+        rowfq = ok ? ROWF[qq] : 0.f;
+        rs = lam * rowfq;
+        gq = G[(int64_t)(ok ? qq : L - 1) * sgl];
+        lse = ok ? LSE[qq] : __builtin_inff();
     }
 
-    f32x4 dqa[BWD_NC][4], dca[BWD_NC][2];
-    RowSums rsum[BWD_NC];
+    f32x4 dqa[4], dca[2];
 #pragma unroll
-    for (int cq = 0; cq < BWD_NC; ++cq) {
-#pragma unroll
-        for (int db = 0; db < 4; ++db) dqa[cq][db] = zero4();
-#pragma unroll
-        for (int sb = 0; sb < 2; ++sb) dca[cq][sb] = zero4();
-        rsum[cq] = RowSums{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    }
+    for (int db = 0; db < 4; ++db) dqa[db] = zero4();
+    dca[0] = dca[1] = zero4();
+    RowSums R{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 
+    TileStage<T, DH, NTH> stk, stv;
+    TileStage<T, DS, NTH> stb;
     const int kend = (tile0 + 128 < L) ? tile0 + 128 : L;
+    stk.load(K, skl, L < 64 ? L : 64, tid);
+    stv.load(V, svl, L < 64 ? L : 64, tid);
+    stb.load(Bm, sbl, L < 64 ? L : 64, tid);
     for (int n0 = 0; n0 < kend; n0 += 64) {
         __syncthreads();
-        const int nvalid = (L - n0 < 64) ? L - n0 : 64;
-        stage_tile<T, DH, true, true, BWD_THREADS>(K + (int64_t)n0 * skl, skl, nvalid, sm.ks, sm.kt, tid);
-        stage_tile<T, DH, true, false, BWD_THREADS>(V + (int64_t)n0 * svl, svl, nvalid, sm.vs, nullptr, tid);
-        stage_tile<T, DS, true, true, BWD_THREADS>(Bm + (int64_t)n0 * sbl, sbl, nvalid, sm.bs, sm.bt, tid);
+        stk.store(sm.ks, tid);
+        stv.store(sm.vs, tid);
+        stb.store(sm.bs, tid);
         if (tid < 64) {
             const int j = n0 + tid;
             const int jc = j < L ? j : L - 1;
@@ -473,182 +458,174 @@ __global__ __launch_bounds__(BWD_THREADS, 2) void attn_bwd_dq_kernel(sisa_attn_b
             sm.cfm[1][tid] = cf * exp2_le0((ga1 - ge) * LOG2E);
         }
         __syncthreads();
+        const int n1 = n0 + 64;
+        if (n1 < kend) {
+            const int nv = (L - n1 < 64) ? L - n1 : 64;
+            stk.load(K + (int64_t)n1 * skl, skl, nv, tid);
+            stv.load(V + (int64_t)n1 * svl, svl, nv, tid);
+            stb.load(Bm + (int64_t)n1 * sbl, sbl, nv, tid);
+        }
         if (!live) continue;
         if (n0 + 63 < q0) {
-            dq_tile<T, false>(sm, sm.cfm[qblk], lane, n0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, scale,
-                              rsum, dqa, dca);
-        } else if (n0 <= qend) {
+            dq_tile<T, false>(sm, sm.cfm[qblk], lane, n0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, scale, R,
+                              dqa, dca);
+        } else if (n0 <= q0 + 15) {
             // the wave's own 64-block is its last tile: apply the off-block row factors once, in fp32
-#pragma unroll
-            for (int cq = 0; cq < BWD_NC; ++cq) {
-                rsum[cq].xa *= rowfq[cq];
-                rsum[cq].ya *= rowfq[cq];
-#pragma unroll
-                for (int sb = 0; sb < 2; ++sb) dca[cq][sb] *= rs[cq];
-            }
-            dq_tile<T, true>(sm, sm.cfm[qblk], lane, n0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, scale,
-                             rsum, dqa, dca);
+            R.xa *= rowfq;
+            R.ya *= rowfq;
+            dca[0] *= rs;
+            dca[1] *= rs;
+            dq_tile<T, true>(sm, sm.cfm[qblk], lane, n0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, scale, R,
+                             dqa, dca);
         }
     }
     if (!live) return;
-    const bool dcb32 = a.dcb_dtype == SISA_F32;
+    const float xat = group_sum(R.xa), yat = group_sum(R.ya), Wa = group_sum(R.wa), Za = group_sum(R.za);
+    const float Ptt = group_sum(R.ptt), Dptt = group_sum(R.dptt), Xd = group_sum(R.xd);
+    const int qq = q0 + lc;
+    if (qq >= L) return;
+    // self-normalised exact delta and the delta-free diagonal (attention.py:453-463)
+    float ssum = Ptt + Za;
+    ssum = ssum > 0.f ? ssum : 1.f;
+    const float x0 = Dptt - dhat;
+    const float tt = dhat + (Ptt * x0 + Wa) / ssum;
+    const float dstt = Ptt * (Za * x0 - Wa) / ssum;
+    const float dl_row = xat + (dhat - tt) * yat;
+    const float dsq = (float)cvt<T>(dstt);           // one DT rounding of the diagonal operands
+    const float dsc = (float)cvt<T>(dstt * lam);
+    const T* krow = K + (int64_t)qq * skl;
+    const T* brow = Bm + (int64_t)qq * sbl;
+    T* dqp = (T*)a.dq.ptr + (int64_t)b * a.dq.sb + (int64_t)h * a.dq.sh + (int64_t)qq * a.dq.sl;
 #pragma unroll
-    for (int cq = 0; cq < BWD_NC; ++cq) {
-        const RowSums& R = rsum[cq];
-        const float xat = group_sum(R.xa), yat = group_sum(R.ya), Wa = group_sum(R.wa), Za = group_sum(R.za);
-        const float Ptt = group_sum(R.ptt), Dptt = group_sum(R.dptt), Xd = group_sum(R.xd);
-        const int qq = q0 + 16 * cq + lc;
-        if (qq >= L) continue;
-        // self-normalised exact delta and the delta-free diagonal (attention.py:453-463)
-        float ssum = Ptt + Za;
-        ssum = ssum > 0.f ? ssum : 1.f;
-        const float x0 = Dptt - dhat[cq];
-        const float tt = dhat[cq] + (Ptt * x0 + Wa) / ssum;
-        const float dstt = Ptt * (Za * x0 - Wa) / ssum;
-        const float dl_row = xat + (dhat[cq] - tt) * yat;
-        const float dsq = (float)cvt<T>(dstt);           // one DT rounding of the diagonal operands
-        const float dsc = (float)cvt<T>(dstt * lam);
-        const T* krow = K + (int64_t)qq * skl;
-        const T* brow = Bm + (int64_t)qq * sbl;
-        T* dqp = (T*)a.dq.ptr + (int64_t)b * a.dq.sb + (int64_t)h * a.dq.sh + (int64_t)qq * a.dq.sl;
+    for (int db = 0; db < 4; ++db) {
+        const int d = db * 16 + 4 * grp;
+        const vec4<T> kv = load4<T>(krow + d);
+        f32x4 r = dqa[db];
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
-            const int d = db * 16 + 4 * grp;
-            const vec4<T> kv = load4<T>(krow + d);
-            f32x4 r = dqa[cq][db];
+        for (int i = 0; i < 4; ++i) r[i] = fmaf(dsq, (float)kv[i], r[i]);
+        store_row4<T, T>(dqp + d, r * scale);
+    }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) r[i] = fmaf(dsq, (float)kv[i], r[i]);
-            store_row4<T, T>(dqp + d, r * scale);
+    for (int sb = 0; sb < 2; ++sb) {
+        const int s0 = sb * 16 + 4 * grp;
+        const vec4<T> bv = load4<T>(brow + s0);
+        f32x4 r = dca[sb];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = fmaf(dsc, (float)bv[i], r[i]);
+        if (a.dcb_dtype == SISA_F32) {
+            float* dcp = (float*)a.dc.ptr + (int64_t)b * a.dc.sb + (int64_t)h * a.dc.sh + (int64_t)qq * a.dc.sl;
+            *reinterpret_cast<f32x4*>(dcp + s0) = r;
+        } else {
+            T* dcp = (T*)a.dc.ptr + (int64_t)b * a.dc.sb + (int64_t)h * a.dc.sh + (int64_t)qq * a.dc.sl;
+            store_row4<T, T>(dcp + s0, r);
         }
-#pragma unroll
-        for (int sb = 0; sb < 2; ++sb) {
-            const int s0 = sb * 16 + 4 * grp;
-            const vec4<T> bv = load4<T>(brow + s0);
-            f32x4 r = dca[cq][sb];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) r[i] = fmaf(dsc, (float)bv[i], r[i]);
-            if (dcb32) {
-                float* dcp = (float*)a.dc.ptr + (int64_t)b * a.dc.sb + (int64_t)h * a.dc.sh + (int64_t)qq * a.dc.sl;
-                *reinterpret_cast<f32x4*>(dcp + s0) = r;
-            } else {
-                T* dcp = (T*)a.dc.ptr + (int64_t)b * a.dc.sb + (int64_t)h * a.dc.sh + (int64_t)qq * a.dc.sl;
-                store_row4<T, T>(dcp + s0, r);
-            }
-        }
-        if (grp == 0) {
-            const int64_t o = (int64_t)bh * L + qq;
-            WS[WS_DELTA * BHL + o] = dhat[cq];
-            WS[WS_DDEL * BHL + o] = tt - dhat[cq];
-            WS[WS_DSD * BHL + o] = dstt;
-            WS[WS_RG * BHL + o] = lam * dl_row;
-            WS[WS_RL * BHL + o] = dl_row + dstt * Xd;
-            WS[WS_RF * BHL + o] = Wa - Za * (tt - dhat[cq]);
-        }
+    }
+    if (grp == 0) {
+        const int64_t o = (int64_t)bh * L + qq;
+        WS[WS_DELTA * BHL + o] = dhat;
+        WS[WS_DDEL * BHL + o] = tt - dhat;
+        WS[WS_DSD * BHL + o] = dstt;
+        WS[WS_RG * BHL + o] = lam * dl_row;
+        WS[WS_RL * BHL + o] = dl_row + dstt * Xd;
+        WS[WS_RF * BHL + o] = Wa - Za * (tt - dhat);
     }
 }
 
 // ------------------------------------------------------------------------------------------------ backward: dk dv db
+// Scores are computed as S = Q K^T (a lane owns one key's column sums); query tiles are visited in descending order
+// so that the keys' own 64-block is every wave's last tile.
 template <class T>
 struct DkvLds {
-    T qs[64 * (DH + LDS_PAD)];   // Q, row-major (scores)
-    T qt[DH * (64 + LDS_PAD)];   // Q, transposed (dk)
-    T cs[64 * (DS + LDS_PAD)];   // C~, row-major (scores)
-    T ct[DS * (64 + LDS_PAD)];   // C~, transposed (db)
-    T ds[64 * (DH + LDS_PAD)];   // dO, row-major (dP)
-    T dt[DH * (64 + LDS_PAD)];   // dO, transposed (dv)
+    T qs[64 * (DH + LDS_PAD)];   // Q (scores; transposed reads for dk)
+    T cs[64 * (DS + LDS_PAD)];   // C~ (scores; transposed reads for db)
+    T ds[64 * (DH + LDS_PAD)];   // dO (dP; transposed reads for dv)
     float lse[64], dhat[64], ddel[64], fq[64], gq[64];
     float rq[2][64];             // rowf * mid for the workgroup's two key blocks
 };
 
 template <class T, bool PAIR>
-SISA_DEV void dkv_tile(const DkvLds<T>& sm, const float* rqm, int lane, int m0, int k0, int L,
-                       const frag8<T> (&kf)[BWD_NC][2], const frag8<T> (&vf)[BWD_NC][2],
-                       const frag8<T> (&bfr)[BWD_NC], const float (&fk)[BWD_NC], const float (&rk)[BWD_NC],
-                       const float (&gk)[BWD_NC], const float (&dsd)[BWD_NC], float lam, float scale,
-                       float (&dgu)[BWD_NC], float (&dfs)[BWD_NC], f32x4 (&dva)[BWD_NC][4], f32x4 (&dka)[BWD_NC][4],
-                       f32x4 (&dba)[BWD_NC][2]) {
+SISA_DEV void dkv_tile(const DkvLds<T>& sm, const float* rqm, int lane, int m0, int k0, int L, const frag8<T> (&kf)[2],
+                       const frag8<T> (&vf)[2], const frag8<T>& bfr, float fk, float rk, float gk, float dsd, float lam,
+                       float scale, float& dgu, float& dfs, f32x4 (&dva)[4], f32x4 (&dka)[4], f32x4 (&dba)[2]) {
     const int grp = lane >> 4, lc = lane & 15;
+    const int kk = k0 + lc;
 #pragma unroll
-    for (int kc = 0; kc < BWD_NC; ++kc) {
-        const int kk = k0 + 16 * kc + lc;
+    for (int st = 0; st < 2; ++st) {           // 32 queries (one K-step of the dk/dv/db products) at a time
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4 sc[2], cb[2], dp[2];
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {           // 32 queries (one K-step of the dk/dv/db products) at a time
-            __builtin_amdgcn_sched_barrier(0);
-            f32x4 sc[2], cb[2], dp[2];
+        for (int hb = 0; hb < 2; ++hb) {
+            const int qb = 2 * st + hb;
+            const frag8<T> q0f = frag_rows<T, DH>(sm.qs, qb * 16, 0, lane);
+            const frag8<T> q1f = frag_rows<T, DH>(sm.qs, qb * 16, 1, lane);
+            const frag8<T> d0f = frag_rows<T, DH>(sm.ds, qb * 16, 0, lane);
+            const frag8<T> d1f = frag_rows<T, DH>(sm.ds, qb * 16, 1, lane);
+            const frag8<T> cf = frag_rows<T, DS>(sm.cs, qb * 16, 0, lane);
+            sc[hb] = mma(q1f, kf[1], mma(q0f, kf[0], zero4()));
+            cb[hb] = mma(cf, bfr, zero4());
+            dp[hb] = mma(d1f, vf[1], mma(d0f, vf[0], zero4()));
+        }
+        // sc <- P, dp <- dk operand, cb <- db operand
 #pragma unroll
-            for (int hb = 0; hb < 2; ++hb) {
-                const int qb = 2 * st + hb;
-                const frag8<T> q0f = frag_rows<T, DH>(sm.qs, qb * 16, 0, lane);
-                const frag8<T> q1f = frag_rows<T, DH>(sm.qs, qb * 16, 1, lane);
-                const frag8<T> d0f = frag_rows<T, DH>(sm.ds, qb * 16, 0, lane);
-                const frag8<T> d1f = frag_rows<T, DH>(sm.ds, qb * 16, 1, lane);
-                const frag8<T> cf = frag_rows<T, DS>(sm.cs, qb * 16, 0, lane);
-                sc[hb] = mma(q1f, kf[kc][1], mma(q0f, kf[kc][0], zero4()));
-                cb[hb] = mma(cf, bfr[kc], zero4());
-                dp[hb] = mma(d1f, vf[kc][1], mma(d0f, vf[kc][0], zero4()));
-            }
-            // sc <- P, dp <- dk operand, cb <- db operand
+        for (int hb = 0; hb < 2; ++hb) {
+            const int i0 = (2 * st + hb) * 16 + 4 * grp;
+            const f32x4 lq = lds4f(&sm.lse[i0]), dh = lds4f(&sm.dhat[i0]), dd = lds4f(&sm.ddel[i0]);
+            const f32x4 fq = lds4f(&sm.fq[i0]);
+            if (PAIR) {
+                const f32x4 gq = lds4f(&sm.gq[i0]);
 #pragma unroll
-            for (int hb = 0; hb < 2; ++hb) {
-                const int i0 = (2 * st + hb) * 16 + 4 * grp;
-                const f32x4 lq = lds4f(&sm.lse[i0]), dh = lds4f(&sm.dhat[i0]), dd = lds4f(&sm.ddel[i0]);
-                const f32x4 fq = lds4f(&sm.fq[i0]);
-                if (PAIR) {
-                    const f32x4 gq = lds4f(&sm.gq[i0]);
+                for (int i = 0; i < 4; ++i) {
+                    const int qq = m0 + i0 + i;
+                    const bool valid = qq >= kk && qq < L;
+                    const bool strict = valid && qq > kk;
+                    const bool eye = valid && qq == kk;
+                    const float dec = valid ? exp2_le0((gq[i] - gk) * LOG2E) : 0.f;
+                    const float u = dec * cb[hb][i];
+                    float s = sc[hb][i] * scale + (fq[i] - fk);
+                    s = s + lam * u;
+                    const float p = valid ? fast_exp2(fmaf(s, LOG2E, -lq[i])) : 0.f;
+                    const float dsh = p * (dp[hb][i] - dh[i]);
+                    const float dsx = dsh - p * dd[i];
+                    const float dso = strict ? dsx : 0.f;
+                    dgu += dso * u;
+                    dfs += dso;
+                    sc[hb][i] = p;
+                    dp[hb][i] = eye ? dsd : dso;
+                    cb[hb][i] = (eye ? dsd : (strict ? dsh : 0.f)) * (lam * dec);
+                }
+            } else {
+                const f32x4 rq = lds4f(&rqm[i0]);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int qq = m0 + i0 + i;
-                        const bool valid = qq >= kk && qq < L;
-                        const bool strict = valid && qq > kk;
-                        const bool eye = valid && qq == kk;
-                        const float dec = valid ? exp2_le0((gq[i] - gk[kc]) * LOG2E) : 0.f;
-                        const float u = dec * cb[hb][i];
-                        float s = sc[hb][i] * scale + (fq[i] - fk[kc]);
-                        s = s + lam * u;
-                        const float p = valid ? fast_exp2(fmaf(s, LOG2E, -lq[i])) : 0.f;
-                        const float dsh = p * (dp[hb][i] - dh[i]);
-                        const float dsx = dsh - p * dd[i];
-                        const float dso = strict ? dsx : 0.f;
-                        dgu[kc] += dso * u;
-                        dfs[kc] += dso;
-                        sc[hb][i] = p;
-                        dp[hb][i] = eye ? dsd[kc] : dso;
-                        cb[hb][i] = (eye ? dsd[kc] : (strict ? dsh : 0.f)) * (lam * dec);
-                    }
-                } else {
-                    const f32x4 rq = lds4f(&rqm[i0]);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float uc = cb[hb][i] * rq[i];
-                        float s = sc[hb][i] * scale + (fq[i] - fk[kc]);
-                        s = s + rk[kc] * uc;
-                        const float p = fast_exp2(fmaf(s, LOG2E, -lq[i]));
-                        const float dsh = p * (dp[hb][i] - dh[i]);
-                        const float dsx = dsh - p * dd[i];
-                        dgu[kc] += dsx * uc;
-                        dfs[kc] += dsx;
-                        sc[hb][i] = p;
-                        dp[hb][i] = dsx;
-                        cb[hb][i] = dsh * rq[i];
-                    }
+                for (int i = 0; i < 4; ++i) {
+                    const float uc = cb[hb][i] * rq[i];
+                    float s = sc[hb][i] * scale + (fq[i] - fk);
+                    s = s + rk * uc;
+                    const float p = fast_exp2(fmaf(s, LOG2E, -lq[i]));
+                    const float dsh = p * (dp[hb][i] - dh[i]);
+                    const float dsx = dsh - p * dd[i];
+                    dgu += dsx * uc;
+                    dfs += dsx;
+                    sc[hb][i] = p;
+                    dp[hb][i] = dsx;
+                    cb[hb][i] = dsh * rq[i];
                 }
             }
-            const frag8<T> pf = pack8<T>(sc[0], sc[1]);
-            const frag8<T> kfr = pack8<T>(dp[0], dp[1]);
-            const frag8<T> bf = pack8<T>(cb[0], cb[1]);
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                dva[kc][db] = mma(frag_trn<T>(sm.dt, db * 16, st, lane), pf, dva[kc][db]);
-                dka[kc][db] = mma(frag_trn<T>(sm.qt, db * 16, st, lane), kfr, dka[kc][db]);
-            }
-#pragma unroll
-            for (int sb = 0; sb < 2; ++sb) dba[kc][sb] = mma(frag_trn<T>(sm.ct, sb * 16, st, lane), bf, dba[kc][sb]);
         }
+        const frag8<T> pf = pack8<T>(sc[0], sc[1]);
+        const frag8<T> kfr = pack8<T>(dp[0], dp[1]);
+        const frag8<T> bf = pack8<T>(cb[0], cb[1]);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            dva[db] = mma(frag_tr<T, DH>(sm.ds, db * 16, st, lane), pf, dva[db]);
+            dka[db] = mma(frag_tr<T, DH>(sm.qs, db * 16, st, lane), kfr, dka[db]);
+        }
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) dba[sb] = mma(frag_tr<T, DS>(sm.cs, sb * 16, st, lane), bf, dba[sb]);
     }
 }
 
 template <class T>
-__global__ __launch_bounds__(BWD_THREADS, 2) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a, float scale) {
+__global__ __launch_bounds__(NTH, 2) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a, float scale) {
     __shared__ DkvLds<T> sm;
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -677,54 +654,52 @@ __global__ __launch_bounds__(BWD_THREADS, 2) void attn_bwd_dkv_kernel(sisa_attn_
     const float* DDEL = WS + WS_DDEL * BHL + (int64_t)bh * L;
 
     const int ktile0 = ktile * 128;
-    const int k0 = ktile0 + 16 * BWD_NC * w;
-    const int kblkw = (w * BWD_NC) >> 2;          // which of the workgroup's two key blocks
+    const int k0 = ktile0 + 16 * w;
+    const int kblkw = w >> 2;                      // which of the workgroup's two key blocks
     const bool live = k0 < L;
     const int kblk = k0 / BLK * BLK;
-    // g at the ends of the workgroup's two key blocks
     const float ge0 = G[(int64_t)(ktile0 + 63 < L ? ktile0 + 63 : L - 1) * sgl];
     const float ge1 = G[(int64_t)(ktile0 + 127 < L ? ktile0 + 127 : L - 1) * sgl];
 
-    frag8<T> kf[BWD_NC][2], vf[BWD_NC][2], bfr[BWD_NC];
-    float fk[BWD_NC], colf[BWD_NC], rk[BWD_NC], gk[BWD_NC], dsd[BWD_NC];
-#pragma unroll
-    for (int kc = 0; kc < BWD_NC; ++kc) {
-        const int kk = k0 + 16 * kc + lc;
+    frag8<T> kf[2], vf[2], bfr;
+    float fk, colf, rk, gk, dsd;
+    {
+        const int kk = k0 + lc;
         const bool ok = kk < L;
-        const int kcl = ok ? kk : L - 1;
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
-            kf[kc][st] = ok ? load8<T>(K + (int64_t)kk * a.k.sl + 32 * st + 8 * grp) : zero8<T>();
-            vf[kc][st] = ok ? load8<T>(V + (int64_t)kk * a.v.sl + 32 * st + 8 * grp) : zero8<T>();
+            kf[st] = ok ? load8<T>(K + (int64_t)kk * a.k.sl + 32 * st + 8 * grp) : zero8<T>();
+            vf[st] = ok ? load8<T>(V + (int64_t)kk * a.v.sl + 32 * st + 8 * grp) : zero8<T>();
         }
-        bfr[kc] = ok ? load8<T>(Bm + (int64_t)kk * a.b.sl + 8 * grp) : zero8<T>();
-        fk[kc] = (has_f && ok) ? FF[(int64_t)kk * sfl] : 0.f;
-        colf[kc] = ok ? COLF[kk] : 0.f;
-        rk[kc] = lam * colf[kc];
-        gk[kc] = G[(int64_t)kcl * sgl];
-        dsd[kc] = ok ? WS[WS_DSD * BHL + (int64_t)bh * L + kk] : 0.f;
+        bfr = ok ? load8<T>(Bm + (int64_t)kk * a.b.sl + 8 * grp) : zero8<T>();
+        fk = (has_f && ok) ? FF[(int64_t)kk * sfl] : 0.f;
+        colf = ok ? COLF[kk] : 0.f;
+        rk = lam * colf;
+        gk = G[(int64_t)(ok ? kk : L - 1) * sgl];
+        dsd = ok ? WS[WS_DSD * BHL + (int64_t)bh * L + kk] : 0.f;
     }
 
-    f32x4 dva[BWD_NC][4], dka[BWD_NC][4], dba[BWD_NC][2];
+    f32x4 dva[4], dka[4], dba[2];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) dva[db] = dka[db] = zero4();
+    dba[0] = dba[1] = zero4();
     // column sums (diagonal excluded); off-block tiles accumulate dgu without the column factor colf
-    float dgu[BWD_NC], dfs[BWD_NC];
-#pragma unroll
-    for (int kc = 0; kc < BWD_NC; ++kc) {
-#pragma unroll
-        for (int db = 0; db < 4; ++db) dva[kc][db] = dka[kc][db] = zero4();
-#pragma unroll
-        for (int sb = 0; sb < 2; ++sb) dba[kc][sb] = zero4();
-        dgu[kc] = dfs[kc] = 0.f;
-    }
+    float dgu = 0.f, dfs = 0.f;
 
-    // query tiles in descending order: the keys' own 64-block comes last for every wave
+    TileStage<T, DH, NTH> stq, std_;
+    TileStage<T, DS, NTH> stc;
     const int mlast = (L - 1) / 64 * 64;
+    {
+        const int nv = L - mlast;
+        stq.load(Q + (int64_t)mlast * sql, sql, nv, tid);
+        std_.load(DO + (int64_t)mlast * sdl, sdl, nv, tid);
+        stc.load(C + (int64_t)mlast * scl, scl, nv, tid);
+    }
     for (int m0 = mlast; m0 >= ktile0; m0 -= 64) {
         __syncthreads();
-        const int nvalid = (L - m0 < 64) ? L - m0 : 64;
-        stage_tile<T, DH, true, true, BWD_THREADS>(Q + (int64_t)m0 * sql, sql, nvalid, sm.qs, sm.qt, tid);
-        stage_tile<T, DS, true, true, BWD_THREADS>(C + (int64_t)m0 * scl, scl, nvalid, sm.cs, sm.ct, tid);
-        stage_tile<T, DH, true, true, BWD_THREADS>(DO + (int64_t)m0 * sdl, sdl, nvalid, sm.ds, sm.dt, tid);
+        stq.store(sm.qs, tid);
+        std_.store(sm.ds, tid);
+        stc.store(sm.cs, tid);
         if (tid < 64) {
             const int i = m0 + tid;
             const bool ok = i < L;
@@ -740,54 +715,52 @@ __global__ __launch_bounds__(BWD_THREADS, 2) void attn_bwd_dkv_kernel(sisa_attn_
             sm.rq[1][tid] = rowf * exp2_le0((gm - ge1) * LOG2E);
         }
         __syncthreads();
+        const int m1 = m0 - 64;
+        if (m1 >= ktile0) {                        // every tile below mlast is full
+            stq.load(Q + (int64_t)m1 * sql, sql, 64, tid);
+            std_.load(DO + (int64_t)m1 * sdl, sdl, 64, tid);
+            stc.load(C + (int64_t)m1 * scl, scl, 64, tid);
+        }
         if (!live || m0 + 63 < k0) continue;      // every query of the tile is before every key of the wave
         if (m0 == kblk) {
-            // apply the off-block column factors once, in fp32, before the own-block contributions
-#pragma unroll
-            for (int kc = 0; kc < BWD_NC; ++kc) {
-                dgu[kc] *= colf[kc];
-#pragma unroll
-                for (int sb = 0; sb < 2; ++sb) dba[kc][sb] *= rk[kc];
-            }
+            // the keys' own block is the wave's last tile: apply the off-block column factors once, in fp32
+            dgu *= colf;
+            dba[0] *= rk;
+            dba[1] *= rk;
             dkv_tile<T, true>(sm, sm.rq[kblkw], lane, m0, k0, L, kf, vf, bfr, fk, rk, gk, dsd, lam, scale, dgu, dfs,
                               dva, dka, dba);
         } else {
-            dkv_tile<T, false>(sm, sm.rq[kblkw], lane, m0, k0, L, kf, vf, bfr, fk, rk, gk, dsd, lam, scale, dgu,
-                               dfs, dva, dka, dba);
+            dkv_tile<T, false>(sm, sm.rq[kblkw], lane, m0, k0, L, kf, vf, bfr, fk, rk, gk, dsd, lam, scale, dgu, dfs,
+                               dva, dka, dba);
         }
     }
     if (!live) return;
-    const bool dcb32 = a.dcb_dtype == SISA_F32;
+    const float Dgu = group_sum(dgu), Dfs = group_sum(dfs);
+    const int kk = k0 + lc;
+    if (kk >= L) return;
+    T* dkp = (T*)a.dk.ptr + (int64_t)b * a.dk.sb + (int64_t)h * a.dk.sh + (int64_t)kk * a.dk.sl;
+    T* dvp = (T*)a.dv.ptr + (int64_t)b * a.dv.sb + (int64_t)h * a.dv.sh + (int64_t)kk * a.dv.sl;
 #pragma unroll
-    for (int kc = 0; kc < BWD_NC; ++kc) {
-        const float Dgu = group_sum(dgu[kc]), Dfs = group_sum(dfs[kc]);
-        const int kk = k0 + 16 * kc + lc;
-        if (kk >= L) continue;
-        T* dkp = (T*)a.dk.ptr + (int64_t)b * a.dk.sb + (int64_t)h * a.dk.sh + (int64_t)kk * a.dk.sl;
-        T* dvp = (T*)a.dv.ptr + (int64_t)b * a.dv.sb + (int64_t)h * a.dv.sh + (int64_t)kk * a.dv.sl;
+    for (int db = 0; db < 4; ++db) {
+        const int d = db * 16 + 4 * grp;
+        store_row4<T, T>(dkp + d, dka[db] * scale);
+        store_row4<T, T>(dvp + d, dva[db]);
+    }
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
-            const int d = db * 16 + 4 * grp;
-            store_row4<T, T>(dkp + d, dka[kc][db] * scale);
-            store_row4<T, T>(dvp + d, dva[kc][db]);
+    for (int sb = 0; sb < 2; ++sb) {
+        const int s0 = sb * 16 + 4 * grp;
+        if (a.dcb_dtype == SISA_F32) {
+            float* p = (float*)a.db.ptr + (int64_t)b * a.db.sb + (int64_t)h * a.db.sh + (int64_t)kk * a.db.sl;
+            *reinterpret_cast<f32x4*>(p + s0) = dba[sb];
+        } else {
+            T* p = (T*)a.db.ptr + (int64_t)b * a.db.sb + (int64_t)h * a.db.sh + (int64_t)kk * a.db.sl;
+            store_row4<T, T>(p + s0, dba[sb]);
         }
-#pragma unroll
-        for (int sb = 0; sb < 2; ++sb) {
-            const int s0 = sb * 16 + 4 * grp;
-            const f32x4 r = dba[kc][sb];
-            if (dcb32) {
-                float* p = (float*)a.db.ptr + (int64_t)b * a.db.sb + (int64_t)h * a.db.sh + (int64_t)kk * a.db.sl;
-                *reinterpret_cast<f32x4*>(p + s0) = r;
-            } else {
-                T* p = (T*)a.db.ptr + (int64_t)b * a.db.sb + (int64_t)h * a.db.sh + (int64_t)kk * a.db.sl;
-                store_row4<T, T>(p + s0, r);
-            }
-        }
-        if (grp == 0) {
-            const int64_t o = (int64_t)bh * L + kk;
-            a.dg[o] = WS[WS_RG * BHL + o] - lam * Dgu;
-            if (has_f) a.df[o] = WS[WS_RF * BHL + o] - Dfs;
-        }
+    }
+    if (grp == 0) {
+        const int64_t o = (int64_t)bh * L + kk;
+        a.dg[o] = WS[WS_RG * BHL + o] - lam * Dgu;
+        if (has_f) a.df[o] = WS[WS_RF * BHL + o] - Dfs;
     }
 }
 
@@ -814,17 +787,17 @@ __global__ __launch_bounds__(1024) void dlam_kernel(const float* __restrict__ rl
 template <class T>
 int launch_fwd(const sisa_attn_fwd_args* a, hipStream_t st) {
     dim3 grid((unsigned)sisa::cdiv(a->L, 128), (unsigned)(a->B * a->H));
-    attn_fwd_kernel<T><<<grid, 256, 0, st>>>(*a, 0.125f);
+    attn_fwd_kernel<T><<<grid, NTH, 0, st>>>(*a, 0.125f);
     return sisa::launch_status("sisa_attn_fwd");
 }
 
 template <class T>
 int launch_bwd(const sisa_attn_bwd_args* a, hipStream_t st) {
     dim3 grid((unsigned)sisa::cdiv(a->L, 128), (unsigned)(a->B * a->H));
-    attn_bwd_dq_kernel<T><<<grid, BWD_THREADS, 0, st>>>(*a, 0.125f);
+    attn_bwd_dq_kernel<T><<<grid, NTH, 0, st>>>(*a, 0.125f);
     int rc = sisa::launch_status("sisa_attn_bwd (dq)");
     if (rc) return rc;
-    attn_bwd_dkv_kernel<T><<<grid, BWD_THREADS, 0, st>>>(*a, 0.125f);
+    attn_bwd_dkv_kernel<T><<<grid, NTH, 0, st>>>(*a, 0.125f);
     rc = sisa::launch_status("sisa_attn_bwd (dkv)");
     if (rc) return rc;
     const int64_t BHL = (int64_t)a->B * a->H * a->L;

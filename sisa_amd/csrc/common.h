@@ -124,51 +124,88 @@ SISA_DEV f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 template <class T> SISA_DEV vec4<T> to_vec4(f32x4 x) { return __builtin_convertvector(x, vec4<T>); }
 
 // Cooperative staging of a (64 x C) tile of a sequence-major tensor (rows = positions, C in {32, 64} contiguous
-// features) into LDS: row-major X[r][f] (stride C+LDS_PAD) and/or transposed Xt[f][r] (stride 64+LDS_PAD).
-// Rows >= nvalid are zero. NTH threads; each thread moves 4 rows x 4 features.
-template <class T, int C, bool ROW, bool TRN, int NTH = 256>
-SISA_DEV void stage_tile(const T* __restrict__ src, int64_t srow, int nvalid, T* __restrict__ X, T* __restrict__ Xt,
-                         int tid) {
-    constexpr int NBLK = 16 * (C / 4);
-    for (int blk = tid; blk < NBLK; blk += NTH) {
-        const int rq = blk / (C / 4);
-        const int cq = blk % (C / 4);
-        vec4<T> v[4];
+// features) into a row-major LDS tile X[r][f] (row stride C + LDS_PAD), in two phases so that the global loads of the
+// next tile are in flight while the current one is being used: load() issues 16-byte (8-element) vector loads into
+// registers, store() writes them to LDS. Rows >= nvalid are zero. Consecutive threads read consecutive 16-byte
+// pieces of a row (coalesced).
+template <class T, int C, int NTH>
+struct TileStage {
+    static constexpr int NVEC = 64 * C / 8;
+    static constexpr int PER = (NVEC + NTH - 1) / NTH;
+    frag8<T> v[PER];
+
+    SISA_DEV void load(const T* __restrict__ src, int64_t srow, int nvalid, int tid) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = rq * 4 + r;
-            if (row < nvalid) {
-                v[r] = load4<T>(src + (int64_t)row * srow + cq * 4);
-            } else {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) v[r][j] = (T)0.f;
-            }
-        }
-        if (ROW) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) store4<T>(X + (rq * 4 + r) * (C + LDS_PAD) + cq * 4, v[r]);
-        }
-        if (TRN) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                vec4<T> t;
-                t[0] = v[0][j]; t[1] = v[1][j]; t[2] = v[2][j]; t[3] = v[3][j];
-                store4<T>(Xt + (cq * 4 + j) * (64 + LDS_PAD) + rq * 4, t);
-            }
+        for (int p = 0; p < PER; ++p) {
+            const int idx = tid + p * NTH;
+            const int row = idx / (C / 8), c8 = idx % (C / 8);
+            if (idx < NVEC && row < nvalid) v[p] = load8<T>(src + (int64_t)row * srow + c8 * 8);
+            else v[p] = zero8<T>();
         }
     }
-}
+    SISA_DEV void store(T* __restrict__ X, int tid) const {
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            const int idx = tid + p * NTH;
+            const int row = idx / (C / 8), c8 = idx % (C / 8);
+            if (idx < NVEC) *reinterpret_cast<frag8<T>*>(X + row * (C + LDS_PAD) + c8 * 8) = v[p];
+        }
+    }
+};
 
-// Operand fragment of a row-major LDS tile X: row (position) r0 + lane%16, features 32*step + 8*grp + 0..7.
+// Operand fragment of a row-major LDS tile X: row (position) r0 + lane%16, features 32*step + 8*grp + 0..7
+// (feature-contracted products: A/B operand whose row is a position).
 template <class T, int C>
 SISA_DEV frag8<T> frag_rows(const T* X, int r0, int step, int lane) {
     return load8<T>(X + (r0 + (lane & 15)) * (C + LDS_PAD) + 32 * step + 8 * (lane >> 4));
 }
 
-// Operand fragment of a transposed LDS tile Xt: row (feature) f0 + lane%16, K = positions of the sequence map for
-// `step` (positions 32*step .. 32*step+31 of the tile).
+// Operand fragment of the transpose of a row-major LDS tile X (rows = positions): row (feature) f0 + lane%16,
+// K = the positions of the sequence map for `step` (positions 32*step .. 32*step+31 of the tile).
+// 16-bit types use the gfx950 LDS transpose read ds_read_b64_tr_b16: within each block of 16 lanes, destination
+// lane d receives, as element j, element d%4 of the 8 bytes addressed by source lane 4j + d/4. Source lane
+// s = 4j + q of lane group grp therefore addresses position 16*blk + 4*grp + j, features f0 + 4q .. f0 + 4q + 3, and
+// destination lane d gets feature f0 + d at positions 16*blk + 4*grp + 0..3 -- slots j (blk = 2*step) and j + 4
+// (blk = 2*step + 1) of the sequence map.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 template <class T>
-SISA_DEV frag8<T> frag_trn(const T* Xt, int f0, int step, int lane) {
-    const T* base = Xt + (f0 + (lane & 15)) * (64 + LDS_PAD) + 4 * (lane >> 4);
-    return join<T>(load4<T>(base + (2 * step) * 16), load4<T>(base + (2 * step + 1) * 16));
+SISA_DEV vec4<T> lds_tr4(const T* p) {
+    const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
+    return __builtin_bit_cast(vec4<T>, r);
+}
+
+template <class T, int C>
+SISA_DEV frag8<T> frag_tr(const T* X, int f0, int step, int lane) {
+    const int s = lane & 15, grp = lane >> 4;
+    const T* p0 = X + ((2 * step) * 16 + 4 * grp + (s >> 2)) * (C + LDS_PAD) + f0 + 4 * (s & 3);
+    return join<T>(lds_tr4<T>(p0), lds_tr4<T>(p0 + 16 * (C + LDS_PAD)));
+}
+
+// fp32 tiles: plain element gathers (the fp32 path exists for correctness, not speed).
+template <>
+SISA_DEV frag8<float> frag_tr<float, 64>(const float* X, int f0, int step, int lane) {
+    const int m = lane & 15, grp = lane >> 4;
+    frag8<float> r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = X[((2 * step + j / 4) * 16 + 4 * grp + j % 4) * (64 + LDS_PAD) + f0 + m];
+    return r;
+}
+template <>
+SISA_DEV frag8<float> frag_tr<float, 32>(const float* X, int f0, int step, int lane) {
+    const int m = lane & 15, grp = lane >> 4;
+    frag8<float> r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = X[((2 * step + j / 4) * 16 + 4 * grp + j % 4) * (32 + LDS_PAD) + f0 + m];
+    return r;
+}
+
+// The A fragment of a 16-row block whose row 0 is all ones and rows 1..15 are zero: MFMA with it sums the B
+// operand over K into row 0 of the output block.
+template <class T>
+SISA_DEV frag8<T> ones_row_frag(int lane) {
+    frag8<T> r;
+    const float v = (lane & 15) == 0 ? 1.f : 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = (T)v;
+    return r;
 }
