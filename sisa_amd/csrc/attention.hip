@@ -30,6 +30,11 @@ constexpr int BLK = 64;  // decay-factor block (rowf/colf anchors)
 // workgroup, 64-position tiles of the other operand staged row-major in LDS; two workgroups fit on a CU.
 constexpr int NW = 8;
 constexpr int NTH = 64 * NW;
+// Backward kernels: 4 waves x 16 rows = one 64-row decay block per workgroup, so that every tile before the block is
+// an off-block tile for all waves and the block's own tile comes last (two code regions with small register sets;
+// three workgroups per CU).
+constexpr int NWB = 4;
+constexpr int NTHB = 64 * NWB;
 
 // ------------------------------------------------------------------------------------------------ factors
 // rowf_t = exp2(min((g_t - g_{block start})*log2e, 0)), colf_t = exp2(min((g_{block end} - g_t)*log2e, 0)), and the
@@ -264,7 +269,7 @@ struct DqLds {
     T vs[64 * (DH + LDS_PAD)];   // V (dP)
     T bs[64 * (DS + LDS_PAD)];   // B~ (scores; transposed reads for dc)
     float fk[64], gk[64];
-    float cfm[2][64];            // colf * mid for the workgroup's two query blocks
+    float cfm[64];               // colf * mid for the workgroup's query block
 };
 
 // Per-query row sums of the dq kernel (diagonal excluded): xa = sum dS^ u, ya = sum P u, wa = D = sum dS^,
@@ -282,24 +287,17 @@ SISA_DEV void dq_tile(const DqLds<T>& sm, const float* cfm, int lane, int n0, in
     const int qq = q0 + lc;
 #pragma unroll
     for (int st = 0; st < 2; ++st) {           // 32 keys (one K-step of the dq/dc products) at a time
-        __builtin_amdgcn_sched_barrier(0);
-        f32x4 sc[2], cb[2], dp[2];
+        f32x4 dsv[2], wv[2];                   // dq and dc operands of the two 16-key blocks (before rounding)
 #pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {
+        for (int hb = 0; hb < 2; ++hb) {       // one 16-key block at a time keeps the live set small
+            __builtin_amdgcn_sched_barrier(0);
             const int kb = 2 * st + hb;
-            const frag8<T> k0 = frag_rows<T, DH>(sm.ks, kb * 16, 0, lane);
-            const frag8<T> k1 = frag_rows<T, DH>(sm.ks, kb * 16, 1, lane);
-            const frag8<T> v0 = frag_rows<T, DH>(sm.vs, kb * 16, 0, lane);
-            const frag8<T> v1 = frag_rows<T, DH>(sm.vs, kb * 16, 1, lane);
-            const frag8<T> bf = frag_rows<T, DS>(sm.bs, kb * 16, 0, lane);
-            sc[hb] = mma(k1, qf[1], mma(k0, qf[0], zero4()));
-            cb[hb] = mma(bf, cfr, zero4());
-            dp[hb] = mma(v1, dof[1], mma(v0, dof[0], zero4()));
-        }
-        // sc <- dq operand (dS^), cb <- dc operand
-#pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {
-            const int j0 = (2 * st + hb) * 16 + 4 * grp;
+            const f32x4 sc = mma(frag_rows<T, DH>(sm.ks, kb * 16, 1, lane), qf[1],
+                                 mma(frag_rows<T, DH>(sm.ks, kb * 16, 0, lane), qf[0], zero4()));
+            const f32x4 cb = mma(frag_rows<T, DS>(sm.bs, kb * 16, 0, lane), cfr, zero4());
+            const f32x4 dp = mma(frag_rows<T, DH>(sm.vs, kb * 16, 1, lane), dof[1],
+                                 mma(frag_rows<T, DH>(sm.vs, kb * 16, 0, lane), dof[0], zero4()));
+            const int j0 = kb * 16 + 4 * grp;
             const f32x4 fk = lds4f(&sm.fk[j0]);
             if (DIAG) {
                 const f32x4 gk = lds4f(&sm.gk[j0]);
@@ -309,12 +307,12 @@ SISA_DEV void dq_tile(const DqLds<T>& sm, const float* cfm, int lane, int n0, in
                     const bool valid = jj <= qq && jj < L && qq < L;
                     const bool eye = valid && jj == qq;
                     const float dec = valid ? exp2_le0((gq - gk[i]) * LOG2E) : 0.f;
-                    const float cbv = cb[hb][i];
+                    const float cbv = cb[i];
                     const float u = dec * cbv;
-                    float s = sc[hb][i] * scale + (fq - fk[i]);
+                    float s = sc[i] * scale + (fq - fk[i]);
                     s = s + lam * u;
                     const float pr = valid ? fast_exp2(fmaf(s, LOG2E, -lse)) : 0.f;
-                    const float dpv = dp[hb][i];
+                    const float dpv = dp[i];
                     const float ds = pr * (dpv - dhat);
                     const float dso = eye ? 0.f : ds;
                     R.ptt += eye ? pr : 0.f;
@@ -325,29 +323,30 @@ SISA_DEV void dq_tile(const DqLds<T>& sm, const float* cfm, int lane, int n0, in
                     R.ya += po * u;
                     R.wa += dso;
                     R.xa += dso * u;
-                    sc[hb][i] = dso;
-                    cb[hb][i] = dso * (lam * dec);
+                    dsv[hb][i] = dso;
+                    wv[hb][i] = dso * (lam * dec);
                 }
             } else {
                 const f32x4 cf = lds4f(&cfm[j0]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float uc = cb[hb][i] * cf[i];
-                    float s = sc[hb][i] * scale + (fq - fk[i]);
+                    const float uc = cb[i] * cf[i];
+                    float s = sc[i] * scale + (fq - fk[i]);
                     s = s + rs * uc;
                     const float pr = fast_exp2(fmaf(s, LOG2E, -lse));
-                    const float ds = pr * (dp[hb][i] - dhat);
+                    const float ds = pr * (dp[i] - dhat);
                     R.xa += ds * uc;
                     R.ya += pr * uc;
                     R.za += pr;
                     R.wa += ds;
-                    sc[hb][i] = ds;
-                    cb[hb][i] = ds * cf[i];
+                    dsv[hb][i] = ds;
+                    wv[hb][i] = ds * cf[i];
                 }
             }
         }
-        const frag8<T> dsf = pack8<T>(sc[0], sc[1]);
-        const frag8<T> wf = pack8<T>(cb[0], cb[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        const frag8<T> dsf = pack8<T>(dsv[0], dsv[1]);
+        const frag8<T> wf = pack8<T>(wv[0], wv[1]);
 #pragma unroll
         for (int db = 0; db < 4; ++db) dqa[db] = mma(frag_tr<T, DH>(sm.ks, db * 16, st, lane), dsf, dqa[db]);
 #pragma unroll
@@ -356,7 +355,7 @@ SISA_DEV void dq_tile(const DqLds<T>& sm, const float* cfm, int lane, int n0, in
 }
 
 template <class T>
-__global__ __launch_bounds__(NTH, 2) void attn_bwd_dq_kernel(sisa_attn_bwd_args a, float scale) {
+__global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void attn_bwd_dq_kernel(sisa_attn_bwd_args a, float scale) {
     __shared__ DqLds<T> sm;
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -384,12 +383,10 @@ __global__ __launch_bounds__(NTH, 2) void attn_bwd_dq_kernel(sisa_attn_bwd_args 
     const int64_t BHL = (int64_t)a.B * H * L;
     float* WS = (float*)a.workspace;
 
-    const int tile0 = tile * 128;
+    const int tile0 = tile * 64;                   // the workgroup's 64-row decay block
     const int q0 = tile0 + 16 * w;
-    const int qblk = w >> 2;
     const bool live = q0 < L;
-    const float ga0 = G[(int64_t)(tile0 < L ? tile0 : L - 1) * sgl];
-    const float ga1 = G[(int64_t)(tile0 + 64 < L ? tile0 + 64 : L - 1) * sgl];
+    const float ga = G[(int64_t)tile0 * sgl];      // anchor: g at the start of the block
 
     frag8<T> qf[2], cfr, dof[2];
     float fq, rowfq, rs, gq, lse, dhat;
@@ -436,13 +433,13 @@ __global__ __launch_bounds__(NTH, 2) void attn_bwd_dq_kernel(sisa_attn_bwd_args 
     dca[0] = dca[1] = zero4();
     RowSums R{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 
-    TileStage<T, DH, NTH> stk, stv;
-    TileStage<T, DS, NTH> stb;
-    const int kend = (tile0 + 128 < L) ? tile0 + 128 : L;
+    TileStage<T, DH, NTHB> stk, stv;
+    TileStage<T, DS, NTHB> stb;
     stk.load(K, skl, L < 64 ? L : 64, tid);
     stv.load(V, svl, L < 64 ? L : 64, tid);
     stb.load(Bm, sbl, L < 64 ? L : 64, tid);
-    for (int n0 = 0; n0 < kend; n0 += 64) {
+    // key tiles before the block (all off-block), then the block's own tile
+    for (int n0 = 0; n0 <= tile0; n0 += 64) {
         __syncthreads();
         stk.store(sm.ks, tid);
         stv.store(sm.vs, tid);
@@ -454,30 +451,29 @@ __global__ __launch_bounds__(NTH, 2) void attn_bwd_dq_kernel(sisa_attn_bwd_args 
             sm.gk[tid] = G[(int64_t)jc * sgl];
             const float cf = j < L ? COLF[j] : 0.f;
             const float ge = G[(int64_t)(n0 + 63 < L ? n0 + 63 : L - 1) * sgl];
-            sm.cfm[0][tid] = cf * exp2_le0((ga0 - ge) * LOG2E);
-            sm.cfm[1][tid] = cf * exp2_le0((ga1 - ge) * LOG2E);
+            sm.cfm[tid] = cf * exp2_le0((ga - ge) * LOG2E);
         }
         __syncthreads();
         const int n1 = n0 + 64;
-        if (n1 < kend) {
+        if (n1 <= tile0) {                         // next tile: full, or the block's own (ragged at the end)
             const int nv = (L - n1 < 64) ? L - n1 : 64;
             stk.load(K + (int64_t)n1 * skl, skl, nv, tid);
             stv.load(V + (int64_t)n1 * svl, svl, nv, tid);
             stb.load(Bm + (int64_t)n1 * sbl, sbl, nv, tid);
         }
         if (!live) continue;
-        if (n0 + 63 < q0) {
-            dq_tile<T, false>(sm, sm.cfm[qblk], lane, n0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, scale, R,
-                              dqa, dca);
-        } else if (n0 <= q0 + 15) {
-            // the wave's own 64-block is its last tile: apply the off-block row factors once, in fp32
-            R.xa *= rowfq;
-            R.ya *= rowfq;
-            dca[0] *= rs;
-            dca[1] *= rs;
-            dq_tile<T, true>(sm, sm.cfm[qblk], lane, n0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, scale, R,
-                             dqa, dca);
-        }
+        if (n0 < tile0)
+            dq_tile<T, false>(sm, sm.cfm, lane, n0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, scale, R, dqa,
+                              dca);
+    }
+    if (live) {
+        // the block's own tile (still in LDS): apply the off-block row factors once, in fp32, then the diagonal path
+        R.xa *= rowfq;
+        R.ya *= rowfq;
+        dca[0] *= rs;
+        dca[1] *= rs;
+        dq_tile<T, true>(sm, sm.cfm, lane, tile0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, scale, R, dqa,
+                         dca);
     }
     if (!live) return;
     const float xat = group_sum(R.xa), yat = group_sum(R.ya), Wa = group_sum(R.wa), Za = group_sum(R.za);
@@ -540,7 +536,7 @@ struct DkvLds {
     T cs[64 * (DS + LDS_PAD)];   // C~ (scores; transposed reads for db)
     T ds[64 * (DH + LDS_PAD)];   // dO (dP; transposed reads for dv)
     float lse[64], dhat[64], ddel[64], fq[64], gq[64];
-    float rq[2][64];             // rowf * mid for the workgroup's two key blocks
+    float rq[64];                // rowf * mid for the query block against the workgroup's key block
 };
 
 template <class T, bool PAIR>
@@ -551,24 +547,17 @@ SISA_DEV void dkv_tile(const DkvLds<T>& sm, const float* rqm, int lane, int m0, 
     const int kk = k0 + lc;
 #pragma unroll
     for (int st = 0; st < 2; ++st) {           // 32 queries (one K-step of the dk/dv/db products) at a time
-        __builtin_amdgcn_sched_barrier(0);
-        f32x4 sc[2], cb[2], dp[2];
+        f32x4 pv[2], kv[2], bv[2];             // dv, dk and db operands of the two 16-query blocks (before rounding)
 #pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {
+        for (int hb = 0; hb < 2; ++hb) {       // one 16-query block at a time keeps the live set small
+            __builtin_amdgcn_sched_barrier(0);
             const int qb = 2 * st + hb;
-            const frag8<T> q0f = frag_rows<T, DH>(sm.qs, qb * 16, 0, lane);
-            const frag8<T> q1f = frag_rows<T, DH>(sm.qs, qb * 16, 1, lane);
-            const frag8<T> d0f = frag_rows<T, DH>(sm.ds, qb * 16, 0, lane);
-            const frag8<T> d1f = frag_rows<T, DH>(sm.ds, qb * 16, 1, lane);
-            const frag8<T> cf = frag_rows<T, DS>(sm.cs, qb * 16, 0, lane);
-            sc[hb] = mma(q1f, kf[1], mma(q0f, kf[0], zero4()));
-            cb[hb] = mma(cf, bfr, zero4());
-            dp[hb] = mma(d1f, vf[1], mma(d0f, vf[0], zero4()));
-        }
-        // sc <- P, dp <- dk operand, cb <- db operand
-#pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {
-            const int i0 = (2 * st + hb) * 16 + 4 * grp;
+            const f32x4 sc = mma(frag_rows<T, DH>(sm.qs, qb * 16, 1, lane), kf[1],
+                                 mma(frag_rows<T, DH>(sm.qs, qb * 16, 0, lane), kf[0], zero4()));
+            const f32x4 cb = mma(frag_rows<T, DS>(sm.cs, qb * 16, 0, lane), bfr, zero4());
+            const f32x4 dp = mma(frag_rows<T, DH>(sm.ds, qb * 16, 1, lane), vf[1],
+                                 mma(frag_rows<T, DH>(sm.ds, qb * 16, 0, lane), vf[0], zero4()));
+            const int i0 = qb * 16 + 4 * grp;
             const f32x4 lq = lds4f(&sm.lse[i0]), dh = lds4f(&sm.dhat[i0]), dd = lds4f(&sm.ddel[i0]);
             const f32x4 fq = lds4f(&sm.fq[i0]);
             if (PAIR) {
@@ -580,40 +569,41 @@ SISA_DEV void dkv_tile(const DkvLds<T>& sm, const float* rqm, int lane, int m0, 
                     const bool strict = valid && qq > kk;
                     const bool eye = valid && qq == kk;
                     const float dec = valid ? exp2_le0((gq[i] - gk) * LOG2E) : 0.f;
-                    const float u = dec * cb[hb][i];
-                    float s = sc[hb][i] * scale + (fq[i] - fk);
+                    const float u = dec * cb[i];
+                    float s = sc[i] * scale + (fq[i] - fk);
                     s = s + lam * u;
                     const float p = valid ? fast_exp2(fmaf(s, LOG2E, -lq[i])) : 0.f;
-                    const float dsh = p * (dp[hb][i] - dh[i]);
+                    const float dsh = p * (dp[i] - dh[i]);
                     const float dsx = dsh - p * dd[i];
                     const float dso = strict ? dsx : 0.f;
                     dgu += dso * u;
                     dfs += dso;
-                    sc[hb][i] = p;
-                    dp[hb][i] = eye ? dsd : dso;
-                    cb[hb][i] = (eye ? dsd : (strict ? dsh : 0.f)) * (lam * dec);
+                    pv[hb][i] = p;
+                    kv[hb][i] = eye ? dsd : dso;
+                    bv[hb][i] = (eye ? dsd : (strict ? dsh : 0.f)) * (lam * dec);
                 }
             } else {
                 const f32x4 rq = lds4f(&rqm[i0]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float uc = cb[hb][i] * rq[i];
-                    float s = sc[hb][i] * scale + (fq[i] - fk);
+                    const float uc = cb[i] * rq[i];
+                    float s = sc[i] * scale + (fq[i] - fk);
                     s = s + rk * uc;
                     const float p = fast_exp2(fmaf(s, LOG2E, -lq[i]));
-                    const float dsh = p * (dp[hb][i] - dh[i]);
+                    const float dsh = p * (dp[i] - dh[i]);
                     const float dsx = dsh - p * dd[i];
                     dgu += dsx * uc;
                     dfs += dsx;
-                    sc[hb][i] = p;
-                    dp[hb][i] = dsx;
-                    cb[hb][i] = dsh * rq[i];
+                    pv[hb][i] = p;
+                    kv[hb][i] = dsx;
+                    bv[hb][i] = dsh * rq[i];
                 }
             }
         }
-        const frag8<T> pf = pack8<T>(sc[0], sc[1]);
-        const frag8<T> kfr = pack8<T>(dp[0], dp[1]);
-        const frag8<T> bf = pack8<T>(cb[0], cb[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        const frag8<T> pf = pack8<T>(pv[0], pv[1]);
+        const frag8<T> kfr = pack8<T>(kv[0], kv[1]);
+        const frag8<T> bf = pack8<T>(bv[0], bv[1]);
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
             dva[db] = mma(frag_tr<T, DH>(sm.ds, db * 16, st, lane), pf, dva[db]);
@@ -625,7 +615,7 @@ SISA_DEV void dkv_tile(const DkvLds<T>& sm, const float* rqm, int lane, int m0, 
 }
 
 template <class T>
-__global__ __launch_bounds__(NTH, 2) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a, float scale) {
+__global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a, float scale) {
     __shared__ DkvLds<T> sm;
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -653,13 +643,10 @@ __global__ __launch_bounds__(NTH, 2) void attn_bwd_dkv_kernel(sisa_attn_bwd_args
     const float* DELTA = WS + WS_DELTA * BHL + (int64_t)bh * L;
     const float* DDEL = WS + WS_DDEL * BHL + (int64_t)bh * L;
 
-    const int ktile0 = ktile * 128;
+    const int ktile0 = ktile * 64;                 // the workgroup's 64-key decay block
     const int k0 = ktile0 + 16 * w;
-    const int kblkw = w >> 2;                      // which of the workgroup's two key blocks
     const bool live = k0 < L;
-    const int kblk = k0 / BLK * BLK;
-    const float ge0 = G[(int64_t)(ktile0 + 63 < L ? ktile0 + 63 : L - 1) * sgl];
-    const float ge1 = G[(int64_t)(ktile0 + 127 < L ? ktile0 + 127 : L - 1) * sgl];
+    const float ge = G[(int64_t)(ktile0 + 63 < L ? ktile0 + 63 : L - 1) * sgl];   // anchor: g at the block end
 
     frag8<T> kf[2], vf[2], bfr;
     float fk, colf, rk, gk, dsd;
@@ -686,8 +673,8 @@ __global__ __launch_bounds__(NTH, 2) void attn_bwd_dkv_kernel(sisa_attn_bwd_args
     // column sums (diagonal excluded); off-block tiles accumulate dgu without the column factor colf
     float dgu = 0.f, dfs = 0.f;
 
-    TileStage<T, DH, NTH> stq, std_;
-    TileStage<T, DS, NTH> stc;
+    TileStage<T, DH, NTHB> stq, std_;
+    TileStage<T, DS, NTHB> stc;
     const int mlast = (L - 1) / 64 * 64;
     {
         const int nv = L - mlast;
@@ -695,6 +682,7 @@ __global__ __launch_bounds__(NTH, 2) void attn_bwd_dkv_kernel(sisa_attn_bwd_args
         std_.load(DO + (int64_t)mlast * sdl, sdl, nv, tid);
         stc.load(C + (int64_t)mlast * scl, scl, nv, tid);
     }
+    // query tiles after the block (all off-block, descending), then the block's own tile
     for (int m0 = mlast; m0 >= ktile0; m0 -= 64) {
         __syncthreads();
         stq.store(sm.qs, tid);
@@ -711,8 +699,7 @@ __global__ __launch_bounds__(NTH, 2) void attn_bwd_dkv_kernel(sisa_attn_bwd_args
             sm.gq[tid] = G[(int64_t)ic * sgl];
             const float rowf = ok ? ROWF[i] : 0.f;
             const float gm = G[(int64_t)m0 * sgl];   // start of the query block
-            sm.rq[0][tid] = rowf * exp2_le0((gm - ge0) * LOG2E);
-            sm.rq[1][tid] = rowf * exp2_le0((gm - ge1) * LOG2E);
+            sm.rq[tid] = rowf * exp2_le0((gm - ge) * LOG2E);
         }
         __syncthreads();
         const int m1 = m0 - 64;
@@ -721,18 +708,18 @@ __global__ __launch_bounds__(NTH, 2) void attn_bwd_dkv_kernel(sisa_attn_bwd_args
             std_.load(DO + (int64_t)m1 * sdl, sdl, 64, tid);
             stc.load(C + (int64_t)m1 * scl, scl, 64, tid);
         }
-        if (!live || m0 + 63 < k0) continue;      // every query of the tile is before every key of the wave
-        if (m0 == kblk) {
-            // the keys' own block is the wave's last tile: apply the off-block column factors once, in fp32
-            dgu *= colf;
-            dba[0] *= rk;
-            dba[1] *= rk;
-            dkv_tile<T, true>(sm, sm.rq[kblkw], lane, m0, k0, L, kf, vf, bfr, fk, rk, gk, dsd, lam, scale, dgu, dfs,
-                              dva, dka, dba);
-        } else {
-            dkv_tile<T, false>(sm, sm.rq[kblkw], lane, m0, k0, L, kf, vf, bfr, fk, rk, gk, dsd, lam, scale, dgu, dfs,
-                               dva, dka, dba);
-        }
+        if (!live) continue;
+        if (m0 > ktile0)
+            dkv_tile<T, false>(sm, sm.rq, lane, m0, k0, L, kf, vf, bfr, fk, rk, gk, dsd, lam, scale, dgu, dfs, dva,
+                               dka, dba);
+    }
+    if (live) {
+        // the block's own tile (still in LDS): apply the off-block column factors once, in fp32, then the pair path
+        dgu *= colf;
+        dba[0] *= rk;
+        dba[1] *= rk;
+        dkv_tile<T, true>(sm, sm.rq, lane, ktile0, k0, L, kf, vf, bfr, fk, rk, gk, dsd, lam, scale, dgu, dfs, dva,
+                          dka, dba);
     }
     if (!live) return;
     const float Dgu = group_sum(dgu), Dfs = group_sum(dfs);
@@ -793,11 +780,11 @@ int launch_fwd(const sisa_attn_fwd_args* a, hipStream_t st) {
 
 template <class T>
 int launch_bwd(const sisa_attn_bwd_args* a, hipStream_t st) {
-    dim3 grid((unsigned)sisa::cdiv(a->L, 128), (unsigned)(a->B * a->H));
-    attn_bwd_dq_kernel<T><<<grid, NTH, 0, st>>>(*a, 0.125f);
+    dim3 grid((unsigned)sisa::cdiv(a->L, 64), (unsigned)(a->B * a->H));
+    attn_bwd_dq_kernel<T><<<grid, NTHB, 0, st>>>(*a, 0.125f);
     int rc = sisa::launch_status("sisa_attn_bwd (dq)");
     if (rc) return rc;
-    attn_bwd_dkv_kernel<T><<<grid, NTH, 0, st>>>(*a, 0.125f);
+    attn_bwd_dkv_kernel<T><<<grid, NTHB, 0, st>>>(*a, 0.125f);
     rc = sisa::launch_status("sisa_attn_bwd (dkv)");
     if (rc) return rc;
     const int64_t BHL = (int64_t)a->B * a->H * a->L;
