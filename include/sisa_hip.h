@@ -160,41 +160,31 @@ int sisa_prep_bwd(const sisa_prep_bwd_args* a, void* stream);
 
 /* ------------------------------------------------------------------------------------------------ linear CE */
 
-/* Chunked linear + cross-entropy, one token chunk. logits = x W^T are never stored: the first call computes the
- * per-row log-sum-exp and loss row; the second recomputes each logits tile and accumulates dx = G W (token-owned)
- * and writes G = (softmax - onehot) * scale for the dW GEMM.
- * Replaces the chunk loop of `_LinearCrossEntropyFn.forward` (src/sisa/kernels/linear_ce.py:167-191) and
- * `_lmce_row_kernel` (linear_ce.py:60-96). */
+/* Row pass of the chunked linear cross-entropy over one chunk of low-precision logits (logits = x W_pad^T from the
+ * caller's GEMM, padded columns V..Vp-1 present but ignored on read):
+ *   lse_r   = log sum_{c<V} exp(logit[r,c])            (fp32; a NaN logit makes the row NaN)
+ *   loss_r  = lse_r - logit[r, label_r], or 0 when label_r == ignore_index (NaN for a label outside [0, V))
+ *   G[r,c]  = (exp(logit[r,c] - lse_r) - [c == label_r]) * (*inv_n) * gscale, 0 for ignored rows and for c >= V,
+ *             rounded once to the buffer dtype and written over the logits (when compute_grad != 0).
+ * Replaces `_lmce_row_kernel` + `_launch_rows` (src/sisa/kernels/linear_ce.py:60-104). Rows of up to 65,536 columns
+ * are read once (held in registers); longer rows are read twice. */
 typedef struct {
-    int32_t N;                 /* rows in this chunk */
-    int32_t D;                 /* hidden size (multiple of 32) */
-    int32_t V;                 /* real vocabulary rows */
-    int32_t Vp;                /* padded rows of w (multiple of 128, rows >= V are zero) */
-    int32_t dtype;             /* of x and w: SISA_BF16 or SISA_F16 */
-    const void* x;             /* (N, D) contiguous */
-    const void* w;             /* (Vp, D) contiguous */
-    const int64_t* labels;     /* (N,) */
+    int64_t T;                 /* rows of the chunk (0 is a no-op) */
+    int64_t V;                 /* real vocabulary columns, >= 1 */
+    int64_t Vp;                /* padded columns, >= V, multiple of 8 */
+    int64_t stride;            /* row stride of logits in elements, >= Vp, multiple of 8 */
+    int32_t dtype;             /* SISA_BF16 or SISA_F16 */
+    int32_t compute_grad;      /* nonzero: overwrite columns 0..Vp-1 of each row with G */
+    void* logits;              /* (T, stride), 16-byte aligned */
+    const int64_t* labels;     /* (T,) */
     int64_t ignore_index;
-    float* lse;                /* (N,) output, natural log */
-    float* loss_rows;          /* (N,) output: lse - logit[label], 0 if ignored */
-} sisa_lmce_fwd_args;
+    const float* inv_n;        /* device scalar 1 / N_valid (read only when compute_grad) */
+    float gscale;              /* extra multiplier of G (1, or the promised backward seed) */
+    float* loss_rows;          /* (T,) fp32 output */
+    float* lse;                /* (T,) fp32 output, natural log, or NULL */
+} sisa_lmce_rows_args;
 
-typedef struct {
-    int32_t N, D, V, Vp;
-    int32_t dtype;
-    const void* x;
-    const void* w;
-    const int64_t* labels;
-    int64_t ignore_index;
-    const float* lse;          /* from sisa_lmce_fwd */
-    const float* scale;        /* (1,) device scalar: 1/N_valid */
-    float gscale;              /* host multiplier (grad_scale promise or 1) */
-    float* dx;                 /* (N, D) fp32 output or NULL */
-    void* gbuf;                /* (N, Vp) dtype output G (for dW) or NULL */
-} sisa_lmce_bwd_args;
-
-int sisa_lmce_fwd(const sisa_lmce_fwd_args* a, void* stream);
-int sisa_lmce_bwd(const sisa_lmce_bwd_args* a, void* stream);
+int sisa_lmce_rows(const sisa_lmce_rows_args* a, void* stream);
 
 /* ------------------------------------------------------------------------------------------------ misc */
 

@@ -17,6 +17,8 @@ transposed operand fails it):
   factors                         rowf_i * mid * colf_j == exp(g_i - g_j) (closed form, fp64)
   lmce64                          == F.cross_entropy(fp64 logits); ignored rows get exactly zero gradient;
                                   == pure-Python scalar loops on a tiny case (golden fixture)
+  lmce_rows64                     loss rows == F.cross_entropy(reduction='none'); G == fp64 autograd of the
+                                  summed loss times inv_n; composed with the GEMMs == lmce64
 """
 from __future__ import annotations
 
@@ -306,6 +308,33 @@ def lmce64(h: torch.Tensor, w: torch.Tensor, labels: torch.Tensor, g: float = 1.
     return loss / n, dx.view(h.shape), dW
 
 
+def lmce_rows64(logits: torch.Tensor, labels: torch.Tensor, V: int, ignore_index: int = -100,
+                inv_n: float | None = None, gscale: float = 1.0):
+    """Row pass of the chunked linear cross-entropy in fp64 (src/sisa/kernels/linear_ce.py:60-96) on stored
+    (T, Vp) logits: lse over the V real columns, loss row (0 when ignored, NaN for a label outside [0, V)) and,
+    when ``inv_n`` is given, G = (softmax - onehot) * inv_n * gscale with zero rows for ignored labels and zero pad
+    columns. Returns (lse, loss_rows, G or None)."""
+    x = logits.double()
+    xr = x[:, :V]
+    lse = torch.logsumexp(xr, 1)
+    y = labels.to(torch.int64)
+    valid = y != ignore_index
+    inr = (y >= 0) & (y < V)
+    hot = valid & inr
+    ys = torch.where(hot, y, torch.zeros_like(y))
+    tgt = xr.gather(1, ys[:, None])[:, 0]
+    nan = torch.full_like(lse, float("nan"))
+    loss = torch.where(valid, torch.where(inr, lse - tgt, nan), torch.zeros_like(lse))
+    if inv_n is None:
+        return lse, loss, None
+    G = torch.zeros_like(x)
+    G[:, :V] = torch.exp(xr - lse[:, None])
+    rows = torch.nonzero(hot)[:, 0]
+    G[rows, ys[rows]] -= 1.0
+    G *= torch.where(valid, torch.full_like(lse, inv_n * gscale), torch.zeros_like(lse))[:, None]
+    return lse, loss, G
+
+
 # ============================================================================================ inputs
 G_KINDS = {"zero": None, "slow": (-7.0, 0.5), "model": (-2.5, 1.0), "med": (1.0, 1.0), "fast": (3.0, 1.0),
            "extreme": "extreme"}
@@ -390,7 +419,18 @@ def config_inputs(cfg: int, device="cpu", dtype=None) -> dict:
            z ~ N(4,0.5^2), lambda_raw = -1, upstream gradient ~ N(0,1)).
     cfg 1: B=4 T=2048 H=8; cfg 'ns': B=4 T=4096 H=8 -- the same distributions as proj columns (bf16) and z (fp32).
     cfg 2: B=1 T=16384 H=16, a ~ N(-7,1), z ~ N(4,1).
-    Returns dict(proj, z, lam_raw, dy, H) for the fused configs and the unfused tensors for cfg 0."""
+    cfg 3: linear cross-entropy, hidden [16384, 768] ~ N(0,1), W [50277, 768] ~ N(0, 0.02^2) fp32 master,
+           labels ~ U[0, 50277); hidden in ``dtype`` (default bf16).
+    Returns dict(proj, z, lam_raw, dy, H) for the fused configs, dict(hidden, weight, labels) for cfg 3 and the
+    unfused tensors for cfg 0."""
+    if cfg == 3:
+        gen = torch.Generator().manual_seed(3)
+        N, D, V = 16384, 768, 50277
+        hidden = torch.randn(N, D, generator=gen)
+        weight = 0.02 * torch.randn(V, D, generator=gen)
+        labels = torch.randint(0, V, (N,), generator=gen)
+        return dict(hidden=hidden.to(dtype or torch.bfloat16).to(device), weight=weight.to(device),
+                    labels=labels.to(device))
     shapes = {0: (1, 256, 4), 1: (4, 2048, 8), "ns": (4, 4096, 8), 2: (1, 16384, 16)}
     B, L, H = shapes[cfg]
     seed = {0: 0, 1: 1, "ns": 5, 2: 2}[cfg]

@@ -63,16 +63,10 @@ class PrepBwdArgs(Structure):
                 ("dz", c_void_p), ("s_dzb", c_int64), ("s_dzl", c_int64), ("workspace", c_void_p)]
 
 
-class LmceFwdArgs(Structure):
-    _fields_ = [("N", c_int32), ("D", c_int32), ("V", c_int32), ("Vp", c_int32), ("dtype", c_int32),
-                ("x", c_void_p), ("w", c_void_p), ("labels", c_void_p), ("ignore_index", c_int64),
-                ("lse", c_void_p), ("loss_rows", c_void_p)]
-
-
-class LmceBwdArgs(Structure):
-    _fields_ = [("N", c_int32), ("D", c_int32), ("V", c_int32), ("Vp", c_int32), ("dtype", c_int32),
-                ("x", c_void_p), ("w", c_void_p), ("labels", c_void_p), ("ignore_index", c_int64),
-                ("lse", c_void_p), ("scale", c_void_p), ("gscale", c_float), ("dx", c_void_p), ("gbuf", c_void_p)]
+class LmceRowsArgs(Structure):
+    _fields_ = [("T", c_int64), ("V", c_int64), ("Vp", c_int64), ("stride", c_int64), ("dtype", c_int32),
+                ("compute_grad", c_int32), ("logits", c_void_p), ("labels", c_void_p), ("ignore_index", c_int64),
+                ("inv_n", c_void_p), ("gscale", c_float), ("loss_rows", c_void_p), ("lse", c_void_p)]
 
 
 # exported symbol -> (argument types, return type); the same list the header declares
@@ -86,8 +80,7 @@ SIGNATURES = {
     "sisa_prep_fwd": ([POINTER(PrepFwdArgs), c_void_p], c_int),
     "sisa_prep_bwd_workspace_bytes": ([c_int32, c_int32, c_int32], c_int64),
     "sisa_prep_bwd": ([POINTER(PrepBwdArgs), c_void_p], c_int),
-    "sisa_lmce_fwd": ([POINTER(LmceFwdArgs), c_void_p], c_int),
-    "sisa_lmce_bwd": ([POINTER(LmceBwdArgs), c_void_p], c_int),
+    "sisa_lmce_rows": ([POINTER(LmceRowsArgs), c_void_p], c_int),
 }
 
 _LOCK = threading.Lock()
