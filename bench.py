@@ -11,6 +11,8 @@ Reported (one JSON line on rank 0):
   roofline   the attention kernels (forward + backward launches, the dominant work) against the bf16 dense MFMA
              peak: achieved = 1152 P / (their summed average duration, HIP events on the launch stream).
   roofline_prep  the prep forward against HBM peak: algorithmic bytes / its average duration.
+  lmce       the linear cross-entropy at config 3 (N=16384, d=768, V=50277): step time, TFLOP/s of its three GEMMs
+             (6 N V d), hipBLASLt GEMM roofline and the HIP row pass against HBM peak.
   cpu_baseline   the reference's pure-PyTorch path (oracle restatement of src/sisa/functional.py:106-155 plus the
              modeling.py glue) on the host cores, on a bounded sample of the same workload (one batch row, all 8
              heads, T=4096, fp32 forward + backward).
@@ -30,6 +32,12 @@ if ROOT not in sys.path:
 
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
+# HBM bytes per step measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, each scaled by what the same counter
+# reads for a plain 1 GiB copy (fetch x2.0, write x1.0); per-kernel figures in profiles/hbm_traffic_ns_ce.txt.
+# They belong to the kernels of this build: re-measure after a kernel change.
+TRAFFIC_ATTN_NS = 1437.1e6       # attn_fwd + attn_bwd_dq + attn_bwd_dkv + dlam, north-star shape
+TRAFFIC_PREP_FWD_NS = 51.0e6     # prep_sums + prep_fwd
+TRAFFIC_LMCE_ROWS_C3 = 3299.8e6  # lmce_rows on the 16384 x 50304 chunk
 
 
 def parse():
@@ -40,7 +48,88 @@ def parse():
     p.add_argument("--config", default="ns", choices=["ns", "1", "2"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-reps", type=int, default=8)
+    p.add_argument("--no-ce", action="store_true", help="skip the linear cross-entropy leg (config 3)")
+    p.add_argument("--copy-mib", type=int, default=0,
+                   help="run one plain device copy of this many MiB first (calibrates HBM byte counters)")
     return p.parse_args()
+
+
+def bench_ce(steps: int, warmup: int) -> dict:
+    """Linear cross-entropy at config 3 (N=16,384 tokens, d=768, V=50,277, bf16): one step = the work of
+    linear_cross_entropy forward with both gradients (logits GEMM, HIP row pass, dx GEMM, dW GEMM), inputs resident
+    in HBM, timed per phase with HIP events on the current stream."""
+    import torch
+
+    from oracle.reference import config_inputs
+    from sisa_amd.kernels import linear_ce as LC
+
+    dev = torch.device("cuda:0")
+    c = config_inputs(3, device=dev)
+    x, w, lab = c["hidden"], c["weight"], c["labels"]
+    N, D = x.shape
+    V = w.shape[0]
+    wp = LC._padded_lowp_weight(w, torch.bfloat16)
+    Vp = wp.shape[0]
+    rows = LC._pick_chunk(N, Vp, None, 2)
+    buf = torch.empty((rows, Vp), dtype=torch.bfloat16, device=dev)
+    loss_rows = torch.empty(N, device=dev)
+    dx = torch.empty((N, D), device=dev)
+    dw = torch.empty((Vp, D), device=dev)
+    ev = lambda: torch.cuda.Event(enable_timing=True)   # noqa: E731
+    marks = {k: [] for k in ("logits_gemm", "rows", "dx_gemm", "dw_gemm")}
+
+    def step(record):
+        n_valid = (lab != -100).sum()
+        inv_n = torch.reciprocal(n_valid.to(torch.float32)).reshape(1)
+        for s in range(0, N, rows):
+            e = [ev() for _ in range(5)] if record else None
+            lg = buf[:min(N, s + rows) - s]
+            xc = x[s:s + lg.shape[0]]
+            if record:
+                e[0].record()
+            torch.mm(xc, wp.t(), out=lg)
+            if record:
+                e[1].record()
+            LC.lmce_rows(lg, lab[s:s + lg.shape[0]], loss_rows[s:s + lg.shape[0]], V, -100, inv_n, 1.0)
+            if record:
+                e[2].record()
+            torch.mm(lg, wp, out_dtype=torch.float32, out=dx[s:s + lg.shape[0]])
+            if record:
+                e[3].record()
+            if s == 0:
+                torch.mm(lg.t(), xc, out_dtype=torch.float32, out=dw)
+            else:
+                torch.addmm(dw, lg.t(), xc, out_dtype=torch.float32, out=dw)
+            if record:
+                e[4].record()
+                for i, k_ in enumerate(marks):
+                    marks[k_].append((e[i], e[i + 1]))
+        return loss_rows.sum() / n_valid
+
+    for _ in range(warmup):
+        step(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(True)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    ph = {k: sum(a.elapsed_time(b_) for a, b_ in v) / steps for k, v in marks.items()}
+    fl = LC.flops(N, V, D)
+    gemm_ms = ph["logits_gemm"] + ph["dx_gemm"] + ph["dw_gemm"]
+    row_bytes = N * Vp * 2 * 2 + N * 12
+    return {"workload": "linear cross-entropy fwd with dx, dW (config 3)", "N": N, "d": D, "V": V, "Vp": Vp,
+            "chunk_rows": rows, "ms_per_step": round(ms, 4), "tflops": round(fl["total"] / (ms * 1e-3) / 1e12, 2),
+            "tokens_per_s": round(N / (ms * 1e-3), 1), "phases_ms": {k: round(v, 4) for k, v in ph.items()},
+            "roofline_gemm": {"bound": "mfma", "achieved": round(fl["total"] / (gemm_ms * 1e-3) / 1e12, 1),
+                              "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                              "frac": round(fl["total"] / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                              "algorithmic": "3 GEMMs x 2*N*V*d flop"},
+            "roofline_rows": {"bound": "hbm", "achieved": round(row_bytes / (ph["rows"] * 1e-3) / 1e9, 1),
+                              "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                              "frac": round(row_bytes / (ph["rows"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                              "traffic": TRAFFIC_LMCE_ROWS_C3,
+                              "algorithmic": "N*Vp*2 B read + N*Vp*2 B written (+12 B per row)"}}
 
 
 def cpu_baseline(reps: int) -> dict:
@@ -137,6 +226,11 @@ def main():
             for i, k_ in enumerate(marks):
                 marks[k_].append((e[i], e[i + 1]))
 
+    if args.copy_mib > 0:
+        src = torch.ones(args.copy_mib << 18, device=dev)       # MiB of fp32
+        torch.empty_like(src).copy_(src)
+        torch.cuda.synchronize()
+        del src
     for _ in range(args.warmup):
         step(False)
     torch.cuda.synchronize()
@@ -175,13 +269,17 @@ def main():
         "mfma_util_pct": round(100 * value / PEAK_BF16_TFLOPS, 2),
         "phases_ms": {k: round(v, 4) for k, v in phases.items()},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": TRAFFIC_ATTN_NS if cfg == "ns" else None,
                      "kernel": "attention fwd + bwd launches (attn_fwd, attn_bwd_dq, attn_bwd_dkv, dlam)",
                      "algorithmic": f"1152 flop per causal pair x {fl['pairs']:.4g} pairs per step"},
         "roofline_prep": {"bound": "hbm", "achieved": round(prep_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": round(prep_gbs / PEAK_HBM_GBS, 4),
+                          "traffic": TRAFFIC_PREP_FWD_NS if cfg == "ns" else None,
                           "algorithmic": f"{pb['total'] / 1e6:.1f} MB per prep forward (310 B per token-head)"},
     }
+    if not args.no_ce:
+        out["lmce"] = bench_ce(max(3, args.steps // 2), 2)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_reps)
     print(json.dumps(out), flush=True)
