@@ -45,9 +45,11 @@ __all__ = [
 IMPLS = ("auto", "torch", "hip", "hip_fused")
 SUPPORTED_ARCHS = ("gfx950",)
 
-# Launch configuration of the attention kernels (fixed, no autotuning): 128 queries (keys) per workgroup of 4 waves,
-# 64-position key (query) tiles staged in LDS, decay factors over 64-row blocks (T).
-_ATTN_CFG_ALL = dict(T=64, rows_per_wg=128, rows_per_wave=32, tile=64, waves=4)
+# Launch configuration of the attention kernels (fixed, no autotuning): the forward runs 128 queries per workgroup of
+# 8 waves (16 query rows per wave), the backward kernels 64 queries (dq) or keys (dk/dv/db) per workgroup of 4 waves;
+# 64-position tiles staged in LDS; decay factors over 64-row blocks (T).
+_ATTN_CFG_ALL = dict(T=64, tile=64, rows_per_wave=16, fwd_rows_per_wg=128, fwd_waves=8, bwd_rows_per_wg=64,
+                     bwd_waves=4)
 
 _CHECK_MODES = ("async", "sync", "off")
 _STATE = {"check": "async"}
