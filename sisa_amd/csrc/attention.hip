@@ -10,13 +10,16 @@
 // before log2e, the self-normalised fp32 o'' for the exact delta, and the delta-free diagonal dS_tt. The kernel
 // structure (tiles, wave ownership, MFMA layouts, LDS staging) is this library's own.
 //
-// Work decomposition (512 threads = 8 waves per workgroup, two workgroups per CU):
-//   forward, dq kernel: a workgroup owns 128 consecutive queries, each wave 16 of them; key tiles of 64 positions
-//     are staged row-major in LDS (the next tile's global loads are in flight during the current tile's math).
-//   dkv kernel: a workgroup owns 128 consecutive keys, each wave 16; query tiles of 64 positions are staged.
+// Work decomposition (16 rows per wave: one column group of the 16x16 MFMA blocks; no atomics):
+//   forward: a workgroup of 8 waves owns 128 consecutive queries; key tiles of 64 positions are staged row-major in
+//     LDS while the next tile's global loads are in flight; at most 128 VGPRs, so 4 waves per SIMD.
+//   dq kernel: a workgroup of 4 waves owns one 64-query decay block; every key tile before the block is an
+//     off-block tile for all four waves and the block's own tile comes last, in its own code region.
+//   dkv kernel: a workgroup of 4 waves owns one 64-key block; query tiles are visited from the last one down to the
+//     block's own tile. Both backward kernels run 3 waves per SIMD.
 //   Operands of the sequence-contracted products (P V, dS K, ...) are read from the row-major tiles with the gfx950
 //   LDS transpose read, so no transposed copy is ever stored.
-//   Ownership is exclusive (no atomics): dq/dc by query tiles, dk/dv/db/dg/dF by key tiles.
+//   Ownership is exclusive: dq/dc by query blocks, dk/dv/db/dg/dF by key blocks.
 #include "common.h"
 #include "host.h"
 
@@ -26,8 +29,8 @@ constexpr int DH = 64;   // d_head
 constexpr int DS = 32;   // d_state
 constexpr int BLK = 64;  // decay-factor block (rowf/colf anchors)
 
-// Every attention kernel: 8 waves per workgroup, 16 rows (one column group of the MFMA block) per wave, 128 rows per
-// workgroup, 64-position tiles of the other operand staged row-major in LDS; two workgroups fit on a CU.
+// Forward: 8 waves per workgroup, 16 rows (one column group of the MFMA block) per wave, 128 rows per workgroup,
+// 64-position tiles of the other operand staged row-major in LDS.
 constexpr int NW = 8;
 constexpr int NTH = 64 * NW;
 // Backward kernels: 4 waves x 16 rows = one 64-row decay block per workgroup, so that every tile before the block is
