@@ -14,9 +14,12 @@
 // bit for bit and g is non-increasing across chunk boundaries. The backward runs the same scheme in reverse with
 // fp64 accumulators.
 //
-// Decomposition: one workgroup per (64-row chunk, batch row, group of HG heads); 256 threads. The chunk's theta,
-// alpha and z slab is staged in LDS with coalesced loads; the rotation reads/writes the C and B columns of the head
-// group (contiguous in a proj row) directly.
+// Decomposition: one 256-thread workgroup per (64-row chunk, batch row, group of HG = 4 heads). Every global access is
+// issued up front as 16-byte vectors (theta 8 vectors per row; C, B, dC~, dB~ 16 per row), element functions are
+// evaluated by all threads before the 72 scan lanes (head, component) run their sequential 64-row scans out of LDS,
+// and the totals of the preceding (following) chunks are staged through LDS with one parallel load before each lane
+// folds them in chunk order. The backward's first pass also applies the inverse rotation and keeps dPhi rows in the
+// workspace, so its second pass reads only dg, dF, dPhi, alpha and z.
 #include "common.h"
 #include "host.h"
 
@@ -58,322 +61,388 @@ SISA_DEV float logsigmoid_grad(float z) {
     return z < 0.f ? 1.f - r : r;
 }
 
+constexpr int NT = 512;              // threads per workgroup
+constexpr int NU = 1024 / NT;        // C/B vectors (units) per thread
+constexpr int HC = HG * NCOMP;       // (head, component) scan lanes of a workgroup
+
+// sin and cos of x: one fp32 reduction to revolutions in [-1/2, 1/2] and the hardware sine/cosine (input in
+// revolutions). The reduction error, |x| * 2^-24 radians, is about one unit in the last place of x itself; the
+// outputs are rounded to bf16/fp16 afterwards.
+SISA_DEV void sincos_rev(float x, float* s, float* c) {
+    const float r = x * 0.159154943091895336f;
+    const float f = r - __builtin_rintf(r);
+    *s = __builtin_amdgcn_sinf(f);
+    *c = __builtin_amdgcn_cosf(f);
+}
+
+// Column slabs of one 64-row chunk and HG heads: 16-byte vectors of 8 elements.
+//   theta: 8 vectors per row (head hl = part/2, pairs 8*(part%2)..+7)
+//   C, B : 16 vectors per row (head hl = part/4, elements 8*(part%4)..+7, i.e. pairs 4*(part%4)..+3)
+struct Unit {
+    int row, hl, q;
+};
+SISA_DEV Unit cb_unit(int v) { return Unit{v >> 4, (v >> 2) & 3, v & 3}; }
+
 template <class T>
-struct PrepLds {
-    float th[CH][HG * S2];   // theta, later Phi (forward) or dPhi (backward)
-    float al[CH][HG];        // alpha
-    float zz[CH][HG];        // z
-    float g[HG][CH];         // scan results of components 0 / 1
-    float f[HG][CH];
+SISA_DEV frag8<T> load8_if(const T* p, bool ok) { return ok ? load8<T>(p) : zero8<T>(); }
+
+// Scan lanes: x[hl*NCOMP + comp][r] holds the element values of chunk row r (0 beyond L), then the inclusive scan plus
+// the carry of the preceding chunks. Rows padded to 65 floats: the 72 scanning lanes read one row each without bank
+// conflicts.
+struct ScanLds {
+    float x[HC][CH + 1];
 };
 
-// Stage theta / alpha / z of rows [r0, r0+64) for heads [h0, h0+hn) (zero beyond L or without z).
+// Stage theta (comps 2..17) of the chunk into the scan lanes.
 template <class T>
-SISA_DEV void stage_slab(PrepLds<T>& sm, const T* P, int64_t s_pl, const float* Z, int64_t s_zl, int r0, int L,
-                         int h0, int hn, const Layout& off, int tid) {
-    for (int idx = tid; idx < CH * HG * S2; idx += 256) {
-        const int r = idx / (HG * S2), cc = idx % (HG * S2);
-        const int row = r0 + r;
-        float v = 0.f;
-        if (row < L && cc < hn * S2) v = (float)P[(int64_t)row * s_pl + off.TH + h0 * S2 + cc];
-        sm.th[r][cc] = v;
-    }
-    for (int idx = tid; idx < CH * HG; idx += 256) {
-        const int r = idx / HG, hl = idx % HG;
-        const int row = r0 + r;
-        const bool ok = row < L && hl < hn;
-        sm.al[r][hl] = ok ? (float)P[(int64_t)row * s_pl + off.A + h0 + hl] : 0.f;
-        sm.zz[r][hl] = (ok && Z) ? Z[(int64_t)row * s_zl + h0 + hl] : 0.f;
+SISA_DEV void stage_theta(ScanLds& sm, const T* P, int64_t s_pl, int nrows, int hn, const Layout& off, int h0,
+                          int tid) {
+#pragma unroll
+    for (int i = 0; i < 512 / NT; ++i) {
+        const int v = tid + NT * i;
+        const int row = v >> 3, hl = (v >> 1) & 3, half = v & 1;
+        const bool ok = row < nrows && hl < hn;
+        const frag8<T> t = load8_if<T>(P + (int64_t)row * s_pl + off.TH + (h0 + hl) * S2 + 8 * half, ok);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sm.x[hl * NCOMP + 2 + 8 * half + j][row] = (float)t[j];
     }
 }
 
-// Element value of component `comp` at chunk row r (0 for rows >= L).
+// Element functions of alpha and z into components 0 and 1 (one (row, head) per thread).
 template <class T>
-SISA_DEV float elem(const PrepLds<T>& sm, int comp, int hl, int r, bool valid) {
-    if (!valid) return 0.f;
-    if (comp == 0) return neg_softplus(sm.al[r][hl]);
-    if (comp == 1) return logsigmoid(sm.zz[r][hl]);
-    return sm.th[r][hl * S2 + comp - 2];
+SISA_DEV void stage_alpha_z(ScanLds& sm, const T* P, int64_t s_pl, const float* Z, int64_t s_zl, int nrows, int hn,
+                            const Layout& off, int h0, int tid) {
+    if (tid >= CH * HG) return;
+    const int row = tid >> 2, hl = tid & 3;
+    const bool ok = row < nrows && hl < hn;
+    const float al = ok ? (float)P[(int64_t)row * s_pl + off.A + h0 + hl] : 0.f;
+    const float zv = (ok && Z) ? Z[(int64_t)row * s_zl + h0 + hl] : 0.f;
+    sm.x[hl * NCOMP + 0][row] = ok ? neg_softplus(al) : 0.f;
+    sm.x[hl * NCOMP + 1][row] = (ok && Z) ? logsigmoid(zv) : 0.f;
 }
 
-// Pass 1: TOT[bh][c][comp] = sequential in-chunk sum.
+// Left fold, in chunk order, of the totals of chunks [c0, c1) of one scan lane (`col` points at the lane's component
+// of chunk 0; consecutive chunks are NCOMP apart). The loads of a batch are all issued before the first add.
+template <class Acc>
+SISA_DEV Acc fold_totals(const Acc* col, int c0, int c1, Acc acc) {
+    constexpr int NB = 16;
+    for (int cb = c0; cb < c1; cb += NB) {
+        Acc buf[NB];
+#pragma unroll
+        for (int k = 0; k < NB; ++k) buf[k] = (cb + k < c1) ? col[(int64_t)(cb + k) * NCOMP] : (Acc)0;
+#pragma unroll
+        for (int k = 0; k < NB; ++k)
+            if (cb + k < c1) acc += buf[k];
+    }
+    return acc;
+}
+
+// In-chunk inclusive scan of one lane with the carry added: x[r] = carry + sum_{i <= r} x[i] (sequential order).
+SISA_DEV void scan_lane(float* x, float carry) {
+    float v[CH];
+#pragma unroll
+    for (int r = 0; r < CH; ++r) v[r] = x[r];
+    float incl = 0.f;
+#pragma unroll
+    for (int r = 0; r < CH; ++r) {
+        incl += v[r];
+        x[r] = carry + incl;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ forward
+// Pass 1: TOT[bh][c][comp] = sequential sum of the chunk's element values (the same loop as the pass-2 scan, so the
+// total equals the chunk's last inclusive value bit for bit).
 template <class T>
-__global__ __launch_bounds__(256) void prep_sums_kernel(sisa_prep_fwd_args a) {
-    __shared__ PrepLds<T> sm;
+__global__ __launch_bounds__(NT) void prep_sums_kernel(sisa_prep_fwd_args a) {
+    __shared__ ScanLds sm;
     const int c = blockIdx.x, b = blockIdx.y, h0 = blockIdx.z * HG;
     const int H = a.H, L = a.L, NCH = gridDim.x;
     const int hn = (H - h0 < HG) ? H - h0 : HG;
+    const int nrows = (L - c * CH < CH) ? L - c * CH : CH;
     const Layout off = layout_of(H);
     const int tid = threadIdx.x;
-    const T* P = (const T*)a.proj + (int64_t)b * a.s_pb;
-    const float* Z = a.z ? a.z + (int64_t)b * a.s_zb : nullptr;
-    stage_slab<T>(sm, P, a.s_pl, Z, a.s_zl, c * CH, L, h0, hn, off, tid);
+    const T* P = (const T*)a.proj + (int64_t)b * a.s_pb + (int64_t)c * CH * a.s_pl;
+    const float* Z = a.z ? a.z + (int64_t)b * a.s_zb + (int64_t)c * CH * a.s_zl : nullptr;
+    stage_theta<T>(sm, P, a.s_pl, nrows, hn, off, h0, tid);
+    stage_alpha_z<T>(sm, P, a.s_pl, Z, a.s_zl, nrows, hn, off, h0, tid);
     __syncthreads();
-    if (tid < HG * NCOMP) {
-        const int hl = tid / NCOMP, comp = tid % NCOMP;
-        if (hl < hn) {
-            float incl = 0.f;
-            for (int r = 0; r < CH; ++r) incl += elem<T>(sm, comp, hl, r, c * CH + r < L && (comp != 1 || a.z));
-            a.tot[((int64_t)(b * H + h0 + hl) * NCH + c) * NCOMP + comp] = incl;
-        }
-    }
-}
-
-// Pass 2: scans, factors, rotation.
-template <class T>
-__global__ __launch_bounds__(256) void prep_fwd_kernel(sisa_prep_fwd_args a) {
-    __shared__ PrepLds<T> sm;
-    const int c = blockIdx.x, b = blockIdx.y, h0 = blockIdx.z * HG;
-    const int H = a.H, L = a.L, NCH = gridDim.x;
-    const int hn = (H - h0 < HG) ? H - h0 : HG;
-    const Layout off = layout_of(H);
-    const int tid = threadIdx.x;
-    const T* P = (const T*)a.proj + (int64_t)b * a.s_pb;
-    const float* Z = a.z ? a.z + (int64_t)b * a.s_zb : nullptr;
-    stage_slab<T>(sm, P, a.s_pl, Z, a.s_zl, c * CH, L, h0, hn, off, tid);
-    __syncthreads();
-    // one thread per (head, component); a theta column is read and overwritten with Phi by its own thread only
-    if (tid < HG * NCOMP && tid / NCOMP < hn) {
-        const int hl = tid / NCOMP, comp = tid % NCOMP;
-        const float* tb = a.tot + (int64_t)(b * H + h0 + hl) * NCH * NCOMP + comp;
-        float carry = 0.f;
-        for (int cc = 0; cc < c; ++cc) carry += tb[(int64_t)cc * NCOMP];
+    if (tid < HC && tid / NCOMP < hn) {
         float incl = 0.f;
-        for (int r = 0; r < CH; ++r) {
-            incl += elem<T>(sm, comp, hl, r, c * CH + r < L && (comp != 1 || a.z));
-            const float v = carry + incl;
-            if (comp == 0) sm.g[hl][r] = v;
-            else if (comp == 1) sm.f[hl][r] = v;
-            else sm.th[r][hl * S2 + comp - 2] = v;
+#pragma unroll 16
+        for (int r = 0; r < CH; ++r) incl += sm.x[tid][r];
+        a.tot[((int64_t)(b * H + h0 + tid / NCOMP) * NCH + c) * NCOMP + tid % NCOMP] = incl;
+    }
+}
+
+// Pass 2: scans (carry of the preceding chunks + in-chunk inclusive scan), g/F/rowf/colf, rotation of C and B.
+template <class T>
+__global__ __launch_bounds__(NT) void prep_fwd_kernel(sisa_prep_fwd_args a) {
+    __shared__ ScanLds sm;
+    const int c = blockIdx.x, b = blockIdx.y, h0 = blockIdx.z * HG;
+    const int H = a.H, L = a.L, NCH = gridDim.x;
+    const int hn = (H - h0 < HG) ? H - h0 : HG;
+    const int nrows = (L - c * CH < CH) ? L - c * CH : CH;
+    const Layout off = layout_of(H);
+    const int tid = threadIdx.x;
+    const T* P = (const T*)a.proj + (int64_t)b * a.s_pb + (int64_t)c * CH * a.s_pl;
+    const float* Z = a.z ? a.z + (int64_t)b * a.s_zb + (int64_t)c * CH * a.s_zl : nullptr;
+    // the C and B vectors this thread rotates: loads issued first, consumed last
+    frag8<T> cv[NU], bv[NU];
+#pragma unroll
+    for (int i = 0; i < NU; ++i) {
+        const Unit u = cb_unit(tid + NT * i);
+        const bool ok = u.row < nrows && u.hl < hn;
+        const T* prow = P + (int64_t)u.row * a.s_pl + (h0 + u.hl) * DS + 8 * u.q;
+        cv[i] = load8_if<T>(prow + off.C, ok);
+        bv[i] = load8_if<T>(prow + off.B, ok);
+    }
+    const bool lane = tid < HC && tid / NCOMP < hn;
+    const float carry =
+        lane ? fold_totals<float>(a.tot + ((int64_t)(b * H + h0 + tid / NCOMP) * NCH) * NCOMP + tid % NCOMP, 0, c, 0.f)
+             : 0.f;
+    stage_theta<T>(sm, P, a.s_pl, nrows, hn, off, h0, tid);
+    stage_alpha_z<T>(sm, P, a.s_pl, Z, a.s_zl, nrows, hn, off, h0, tid);
+    __syncthreads();
+    if (lane) scan_lane(sm.x[tid], carry);
+    __syncthreads();
+    // g, F, rowf, colf: (B,H,L) rows, one (head, row) per thread, coalesced along L
+    {
+        const int hh = tid >> 6, r = tid & 63;
+        if (hh < hn && r < nrows) {   // hh >= HG for the upper half of the workgroup
+            const int64_t o = ((int64_t)(b * H + h0 + hh)) * L + c * CH + r;
+            const float* gx = sm.x[hh * NCOMP];
+            const float g = gx[r];
+            a.g[o] = g;
+            a.rowf[o] = exp2_le0((g - gx[0]) * LOG2E);
+            a.colf[o] = exp2_le0((gx[CH - 1] - g) * LOG2E);   // rows >= L added 0: the last valid g
+            if (a.z) a.f[o] = sm.x[hh * NCOMP + 1][r];
         }
     }
-    __syncthreads();
-    // g, F, rowf, colf: (B,H,L) rows, coalesced along L
-    for (int idx = tid; idx < hn * CH; idx += 256) {
-        const int hh = idx / CH, r = idx % CH;
-        const int row = c * CH + r;
-        if (row >= L) continue;
-        const int64_t o = ((int64_t)(b * H + h0 + hh)) * L + row;
-        const float g = sm.g[hh][r];
-        a.g[o] = g;
-        a.rowf[o] = exp2_le0((g - sm.g[hh][0]) * LOG2E);
-        a.colf[o] = exp2_le0((sm.g[hh][CH - 1] - g) * LOG2E);   // rows >= L add 0: the last valid g
-        if (a.z) a.f[o] = sm.f[hh][r];
-    }
-    // rotation of C and B by Phi (fp32, one rounding to T)
+    // rotation of C and B by Phi (fp32, one rounding to T); 4 pairs per vector
     T* CR = (T*)a.cr;
     T* BR = (T*)a.br;
-    for (int idx = tid; idx < CH * hn * S2; idx += 256) {
-        const int r = idx / (hn * S2), rem = idx % (hn * S2);
-        const int hh = rem / S2, pr = rem % S2;
-        const int row = c * CH + r;
-        if (row >= L) continue;
-        float sn, cs;
-        sincosf(sm.th[r][hh * S2 + pr], &sn, &cs);
-        const T* prow = P + (int64_t)row * a.s_pl;
-        const int h = h0 + hh;
-        const typename Vec<T>::x2 cv = *reinterpret_cast<const typename Vec<T>::x2*>(prow + off.C + h * DS + 2 * pr);
-        const typename Vec<T>::x2 bv = *reinterpret_cast<const typename Vec<T>::x2*>(prow + off.B + h * DS + 2 * pr);
-        const int64_t o = (((int64_t)b * L + row) * H + h) * DS + 2 * pr;
-        {
-            const float ze = (float)cv[0], zo = (float)cv[1];
-            f32x2 out = {ze * cs - zo * sn, ze * sn + zo * cs};
-            *reinterpret_cast<typename Vec<T>::x2*>(CR + o) = __builtin_convertvector(out, typename Vec<T>::x2);
+#pragma unroll
+    for (int i = 0; i < NU; ++i) {
+        const Unit u = cb_unit(tid + NT * i);
+        if (u.row >= nrows || u.hl >= hn) continue;
+        f32x4 clo, chi, blo, bhi;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            float sn, cs;
+            sincos_rev(sm.x[u.hl * NCOMP + 2 + 4 * u.q + p][u.row], &sn, &cs);
+            const float ce = (float)cv[i][2 * p], co = (float)cv[i][2 * p + 1];
+            const float be = (float)bv[i][2 * p], bo = (float)bv[i][2 * p + 1];
+            const float c0 = ce * cs - co * sn, c1 = ce * sn + co * cs;
+            const float b0 = be * cs - bo * sn, b1 = be * sn + bo * cs;
+            if (p < 2) {
+                clo[2 * p] = c0; clo[2 * p + 1] = c1; blo[2 * p] = b0; blo[2 * p + 1] = b1;
+            } else {
+                chi[2 * p - 4] = c0; chi[2 * p - 3] = c1; bhi[2 * p - 4] = b0; bhi[2 * p - 3] = b1;
+            }
         }
-        {
-            const float ze = (float)bv[0], zo = (float)bv[1];
-            f32x2 out = {ze * cs - zo * sn, ze * sn + zo * cs};
-            *reinterpret_cast<typename Vec<T>::x2*>(BR + o) = __builtin_convertvector(out, typename Vec<T>::x2);
-        }
+        const int64_t o = (((int64_t)b * L + c * CH + u.row) * H + h0 + u.hl) * DS + 8 * u.q;
+        *reinterpret_cast<frag8<T>*>(CR + o) = pack8<T>(clo, chi);
+        *reinterpret_cast<frag8<T>*>(BR + o) = pack8<T>(blo, bhi);
     }
 }
 
 // ------------------------------------------------------------------------------------------------ backward
-struct BwdLds {
-    float th[CH][HG * S2];   // theta -> Phi -> dPhi
-    float al[CH][HG];
-    float zz[CH][HG];
-    float dg[HG][CH];
-    float df[HG][CH];
-};
-
-// Recompute Phi for the chunk (identical code to the forward scan) into sm.th, then replace it with
-// dPhi = sum over {C, B} of (dout_odd * out_even - dout_even * out_odd), optionally writing the inverse-rotated
-// gradients dC, dB into dproj.
-template <class T, bool WRITE>
-SISA_DEV void phi_and_dphi(BwdLds& sm, const sisa_prep_bwd_args& a, const T* P, int b, int c, int h0, int hn,
-                           int NCH, const Layout& off, int tid) {
-    const int H = a.H, L = a.L;
-    if (tid < hn * S2) {
-        const int hl = tid / S2, pr = tid % S2;
-        const float* tb = a.tot + (int64_t)(b * H + h0 + hl) * NCH * NCOMP + 2 + pr;
-        float carry = 0.f;
-        for (int cc = 0; cc < c; ++cc) carry += tb[(int64_t)cc * NCOMP];
-        float incl = 0.f;
-        for (int r = 0; r < CH; ++r) {
-            incl += (c * CH + r < L) ? sm.th[r][hl * S2 + pr] : 0.f;
-            sm.th[r][hl * S2 + pr] = carry + incl;
-        }
-    }
-    __syncthreads();
-    T* DP = (T*)a.dproj + (int64_t)b * a.s_db;
-    for (int idx = tid; idx < CH * hn * S2; idx += 256) {
-        const int r = idx / (hn * S2), rem = idx % (hn * S2);
-        const int hh = rem / S2, p2 = rem % S2;
-        const int row = c * CH + r;
-        float dphi = 0.f;
-        if (row < L) {
-            float sn, cs;
-            sincosf(sm.th[r][hh * S2 + p2], &sn, &cs);
-            const T* prow = P + (int64_t)row * a.s_pl;
-            const int h = h0 + hh;
-            const int64_t o = (((int64_t)b * L + row) * H + h) * DS + 2 * p2;
-            const f32x2 dcv = *reinterpret_cast<const f32x2*>(a.dcr + o);
-            const f32x2 dbv = *reinterpret_cast<const f32x2*>(a.dbr + o);
-            const typename Vec<T>::x2 cv =
-                *reinterpret_cast<const typename Vec<T>::x2*>(prow + off.C + h * DS + 2 * p2);
-            const typename Vec<T>::x2 bv =
-                *reinterpret_cast<const typename Vec<T>::x2*>(prow + off.B + h * DS + 2 * p2);
-            float d1, d2;
-            {
-                const float ze = (float)cv[0], zo = (float)cv[1];
-                const float oe = ze * cs - zo * sn, oo = ze * sn + zo * cs;
-                d1 = dcv[1] * oe - dcv[0] * oo;
-                if (WRITE) {
-                    f32x2 dz = {dcv[0] * cs + dcv[1] * sn, dcv[1] * cs - dcv[0] * sn};
-                    *reinterpret_cast<typename Vec<T>::x2*>(DP + (int64_t)row * a.s_dl + off.C + h * DS + 2 * p2) =
-                        __builtin_convertvector(dz, typename Vec<T>::x2);
-                }
-            }
-            {
-                const float ze = (float)bv[0], zo = (float)bv[1];
-                const float oe = ze * cs - zo * sn, oo = ze * sn + zo * cs;
-                d2 = dbv[1] * oe - dbv[0] * oo;
-                if (WRITE) {
-                    f32x2 dz = {dbv[0] * cs + dbv[1] * sn, dbv[1] * cs - dbv[0] * sn};
-                    *reinterpret_cast<typename Vec<T>::x2*>(DP + (int64_t)row * a.s_dl + off.B + h * DS + 2 * p2) =
-                        __builtin_convertvector(dz, typename Vec<T>::x2);
-                }
-            }
-            dphi = d1 + d2;
-        }
-        sm.th[r][hh * S2 + p2] = dphi;   // each element is read and replaced by its own thread
-    }
+// Workspace: fp64 chunk totals BT (B*H, NCH, 18), then dPhi rows (B, L, H, 16) fp32 written by pass 1.
+__host__ __device__ inline int64_t bt_bytes(int B, int L, int H) {
+    return ((int64_t)B * H * ((L + CH - 1) / CH) * NCOMP * (int64_t)sizeof(double) + 255) / 256 * 256;
 }
 
+// Pass 1: recompute Phi (the forward scan of theta), then per (row, head, 4 pairs): dPhi = sum over {C, B} of
+// dout_odd * out_even - dout_even * out_odd, the inverse rotation dC = R(-Phi) dC~, dB = R(-Phi) dB~ into dproj, dPhi
+// rows into the workspace, and the fp64 chunk totals of (dg, dF, dPhi[16]).
 template <class T>
-SISA_DEV void stage_bwd(BwdLds& sm, const sisa_prep_bwd_args& a, const T* P, int b, int c, int h0, int hn,
-                        const Layout& off, int tid) {
-    const int H = a.H, L = a.L;
-    const float* Z = a.z ? a.z + (int64_t)b * a.s_zb : nullptr;
-    for (int idx = tid; idx < CH * HG * S2; idx += 256) {
-        const int r = idx / (HG * S2), cc = idx % (HG * S2);
-        const int row = c * CH + r;
-        float v = 0.f;
-        if (row < L && cc < hn * S2) v = (float)P[(int64_t)row * a.s_pl + off.TH + h0 * S2 + cc];
-        sm.th[r][cc] = v;
-    }
-    for (int idx = tid; idx < CH * HG; idx += 256) {
-        const int r = idx / HG, hl = idx % HG;
-        const int row = c * CH + r;
-        const bool ok = row < L && hl < hn;
-        sm.al[r][hl] = ok ? (float)P[(int64_t)row * a.s_pl + off.A + h0 + hl] : 0.f;
-        sm.zz[r][hl] = (ok && Z) ? Z[(int64_t)row * a.s_zl + h0 + hl] : 0.f;
-    }
-    for (int idx = tid; idx < HG * CH; idx += 256) {
-        const int hl = idx / CH, r = idx % CH;
-        const int row = c * CH + r;
-        const bool ok = row < L && hl < hn;
-        const int64_t o = (int64_t)(b * H + h0 + hl) * L + row;
-        sm.dg[hl][r] = ok ? a.dg[o] : 0.f;
-        sm.df[hl][r] = (ok && a.df) ? a.df[o] : 0.f;
-    }
-}
-
-// Backward pass 1: fp64 chunk totals BT[bh][c] = (sum dg, sum dF, sum dPhi[16]).
-template <class T>
-__global__ __launch_bounds__(256) void prep_bsums_kernel(sisa_prep_bwd_args a) {
-    __shared__ BwdLds sm;
-    const int c = blockIdx.x, b = blockIdx.y, h0 = blockIdx.z * HG;
-    const int H = a.H, NCH = gridDim.x;
-    const int hn = (H - h0 < HG) ? H - h0 : HG;
-    const Layout off = layout_of(H);
-    const int tid = threadIdx.x;
-    const T* P = (const T*)a.proj + (int64_t)b * a.s_pb;
-    stage_bwd<T>(sm, a, P, b, c, h0, hn, off, tid);
-    __syncthreads();
-    phi_and_dphi<T, false>(sm, a, P, b, c, h0, hn, NCH, off, tid);
-    __syncthreads();
-    double* BT = (double*)a.workspace;
-    if (tid < hn * NCOMP) {
-        const int hl = tid / NCOMP, comp = tid % NCOMP;
-        double s = 0.0;
-        for (int r = 0; r < CH; ++r) {
-            const float v = comp == 0 ? sm.dg[hl][r] : (comp == 1 ? sm.df[hl][r] : sm.th[r][hl * S2 + comp - 2]);
-            s += (double)v;
-        }
-        BT[((int64_t)(b * H + h0 + hl) * NCH + c) * NCOMP + comp] = s;
-    }
-}
-
-// Backward pass 2: reverse scans (fp64 carries of the following chunks + sequential in-chunk reverse sums).
-template <class T>
-__global__ __launch_bounds__(256) void prep_bwd_kernel(sisa_prep_bwd_args a) {
-    __shared__ BwdLds sm;
-    __shared__ float outv[CH][HG * NCOMP];
+__global__ __launch_bounds__(NT) void prep_bsums_kernel(sisa_prep_bwd_args a) {
+    __shared__ ScanLds sm;
     const int c = blockIdx.x, b = blockIdx.y, h0 = blockIdx.z * HG;
     const int H = a.H, L = a.L, NCH = gridDim.x;
     const int hn = (H - h0 < HG) ? H - h0 : HG;
+    const int nrows = (L - c * CH < CH) ? L - c * CH : CH;
     const Layout off = layout_of(H);
     const int tid = threadIdx.x;
-    const T* P = (const T*)a.proj + (int64_t)b * a.s_pb;
-    stage_bwd<T>(sm, a, P, b, c, h0, hn, off, tid);
+    const T* P = (const T*)a.proj + (int64_t)b * a.s_pb + (int64_t)c * CH * a.s_pl;
+    frag8<T> cv[NU], bv[NU];
+    f32x4 dc[NU][2], db[NU][2];
+#pragma unroll
+    for (int i = 0; i < NU; ++i) {
+        const Unit u = cb_unit(tid + NT * i);
+        const bool ok = u.row < nrows && u.hl < hn;
+        const T* prow = P + (int64_t)u.row * a.s_pl + (h0 + u.hl) * DS + 8 * u.q;
+        cv[i] = load8_if<T>(prow + off.C, ok);
+        bv[i] = load8_if<T>(prow + off.B, ok);
+        const int64_t o = (((int64_t)b * L + c * CH + u.row) * H + h0 + u.hl) * DS + 8 * u.q;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            dc[i][k] = ok ? *reinterpret_cast<const f32x4*>(a.dcr + o + 4 * k) : zero4();
+            db[i][k] = ok ? *reinterpret_cast<const f32x4*>(a.dbr + o + 4 * k) : zero4();
+        }
+    }
+    // dg and dF of the chunk into components 0 and 1 (one (head, row) per thread)
+    if (tid < CH * HG) {
+        const int hh = tid >> 6, r = tid & 63;
+        const bool ok = hh < hn && r < nrows;
+        const int64_t o = (int64_t)(b * H + h0 + hh) * L + c * CH + r;
+        const float dgv = ok ? a.dg[o] : 0.f;
+        const float dfv = (ok && a.df) ? a.df[o] : 0.f;
+        sm.x[(hh & 3) * NCOMP + 0][r] = dgv;
+        sm.x[(hh & 3) * NCOMP + 1][r] = dfv;
+    }
+    const bool lane = tid < HC && tid / NCOMP < hn && tid % NCOMP >= 2;   // Phi lanes (components 2..17)
+    const float carry =
+        lane ? fold_totals<float>(a.tot + ((int64_t)(b * H + h0 + tid / NCOMP) * NCH) * NCOMP + tid % NCOMP, 0, c, 0.f)
+             : 0.f;
+    stage_theta<T>(sm, P, a.s_pl, nrows, hn, off, h0, tid);
     __syncthreads();
-    phi_and_dphi<T, true>(sm, a, P, b, c, h0, hn, NCH, off, tid);
+    if (lane) scan_lane(sm.x[tid], carry);   // Phi: the forward scan of theta
     __syncthreads();
-    const double* BT = (const double*)a.workspace;
-    if (tid < hn * NCOMP) {
+    T* DP = (T*)a.dproj + (int64_t)b * a.s_db + (int64_t)c * CH * a.s_dl;
+    float* DPHI = (float*)((char*)a.workspace + bt_bytes(a.B, L, H));
+    float dphi[NU][4];
+#pragma unroll
+    for (int i = 0; i < NU; ++i) {
+        const Unit u = cb_unit(tid + NT * i);
+        const bool ok = u.row < nrows && u.hl < hn;
+        f32x4 xlo, xhi, ylo, yhi;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            float sn, cs;
+            sincos_rev(ok ? sm.x[u.hl * NCOMP + 2 + 4 * u.q + p][u.row] : 0.f, &sn, &cs);
+            const float dc0 = dc[i][p >> 1][2 * (p & 1)], dc1 = dc[i][p >> 1][2 * (p & 1) + 1];
+            const float db0 = db[i][p >> 1][2 * (p & 1)], db1 = db[i][p >> 1][2 * (p & 1) + 1];
+            const float ce = (float)cv[i][2 * p], co = (float)cv[i][2 * p + 1];
+            const float be = (float)bv[i][2 * p], bo = (float)bv[i][2 * p + 1];
+            const float coe = ce * cs - co * sn, coo = ce * sn + co * cs;
+            const float boe = be * cs - bo * sn, boo = be * sn + bo * cs;
+            const float d1 = dc1 * coe - dc0 * coo;
+            const float d2 = db1 * boe - db0 * boo;
+            dphi[i][p] = ok ? d1 + d2 : 0.f;
+            const float x0 = dc0 * cs + dc1 * sn, x1 = dc1 * cs - dc0 * sn;
+            const float y0 = db0 * cs + db1 * sn, y1 = db1 * cs - db0 * sn;
+            if (p < 2) {
+                xlo[2 * p] = x0; xlo[2 * p + 1] = x1; ylo[2 * p] = y0; ylo[2 * p + 1] = y1;
+            } else {
+                xhi[2 * p - 4] = x0; xhi[2 * p - 3] = x1; yhi[2 * p - 4] = y0; yhi[2 * p - 3] = y1;
+            }
+        }
+        if (ok) {
+            T* drow = DP + (int64_t)u.row * a.s_dl + (h0 + u.hl) * DS + 8 * u.q;
+            *reinterpret_cast<frag8<T>*>(drow + off.C) = pack8<T>(xlo, xhi);
+            *reinterpret_cast<frag8<T>*>(drow + off.B) = pack8<T>(ylo, yhi);
+            const int64_t o = (((int64_t)b * L + c * CH + u.row) * H + h0 + u.hl) * S2 + 4 * u.q;
+            *reinterpret_cast<f32x4*>(DPHI + o) = f32x4{dphi[i][0], dphi[i][1], dphi[i][2], dphi[i][3]};
+        }
+    }
+    __syncthreads();   // every Phi read is done before the lanes are overwritten with dPhi
+#pragma unroll
+    for (int i = 0; i < NU; ++i) {
+        const Unit u = cb_unit(tid + NT * i);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) sm.x[u.hl * NCOMP + 2 + 4 * u.q + p][u.row] = dphi[i][p];
+    }
+    __syncthreads();
+    double* BT = (double*)a.workspace;
+    if (tid < HC && tid / NCOMP < hn) {
+        double s = 0.0;
+#pragma unroll 16
+        for (int r = 0; r < CH; ++r) s += (double)sm.x[tid][r];
+        BT[((int64_t)(b * H + h0 + tid / NCOMP) * NCH + c) * NCOMP + tid % NCOMP] = s;
+    }
+}
+
+// Pass 2: reverse scans (fp64 carry of the following chunks + in-chunk reverse sums) into d alpha, dz, d theta; pad
+// columns set to zero.
+template <class T>
+__global__ __launch_bounds__(NT) void prep_bwd_kernel(sisa_prep_bwd_args a) {
+    __shared__ ScanLds sm;
+    __shared__ float dal[CH][HG], dzz[CH][HG];   // softplus'(alpha), logsigmoid'(z)
+    const int c = blockIdx.x, b = blockIdx.y, h0 = blockIdx.z * HG;
+    const int H = a.H, L = a.L, NCH = gridDim.x;
+    const int hn = (H - h0 < HG) ? H - h0 : HG;
+    const int nrows = (L - c * CH < CH) ? L - c * CH : CH;
+    const Layout off = layout_of(H);
+    const int tid = threadIdx.x;
+    const T* P = (const T*)a.proj + (int64_t)b * a.s_pb + (int64_t)c * CH * a.s_pl;
+    const float* DPHI = (const float*)((const char*)a.workspace + bt_bytes(a.B, L, H));
+    // dPhi rows (written by pass 1): one (row, head, 4 pairs) vector per thread and iteration
+#pragma unroll
+    for (int i = 0; i < NU; ++i) {
+        const Unit u = cb_unit(tid + NT * i);
+        const bool ok = u.row < nrows && u.hl < hn;
+        const int64_t o = (((int64_t)b * L + c * CH + u.row) * H + h0 + u.hl) * S2 + 4 * u.q;
+        const f32x4 d = ok ? *reinterpret_cast<const f32x4*>(DPHI + o) : zero4();
+#pragma unroll
+        for (int p = 0; p < 4; ++p) sm.x[u.hl * NCOMP + 2 + 4 * u.q + p][u.row] = d[p];
+    }
+    if (tid < CH * HG) {
+        const int hh = tid >> 6, r = tid & 63;
+        const bool ok = hh < hn && r < nrows;
+        const int64_t o = (int64_t)(b * H + h0 + hh) * L + c * CH + r;
+        sm.x[(hh & 3) * NCOMP + 0][r] = ok ? a.dg[o] : 0.f;
+        sm.x[(hh & 3) * NCOMP + 1][r] = (ok && a.df) ? a.df[o] : 0.f;
+    }
+    if (tid < CH * HG) {
+        const int row = tid >> 2, hl = tid & 3;
+        const bool ok = row < nrows && hl < hn;
+        const float al = ok ? (float)P[(int64_t)row * a.s_pl + off.A + h0 + hl] : 0.f;
+        const float zv = (ok && a.z) ? a.z[(int64_t)b * a.s_zb + (int64_t)(c * CH + row) * a.s_zl + h0 + hl] : 0.f;
+        dal[row][hl] = softplus_grad(al);
+        dzz[row][hl] = logsigmoid_grad(zv);
+    }
+    const bool lane = tid < HC && tid / NCOMP < hn;
+    const double sa =
+        lane ? fold_totals<double>((const double*)a.workspace + ((int64_t)(b * H + h0 + tid / NCOMP) * NCH) * NCOMP +
+                                       tid % NCOMP, c + 1, NCH, 0.0)
+             : 0.0;
+    __syncthreads();
+    if (lane) {
         const int hl = tid / NCOMP, comp = tid % NCOMP;
-        const double* tb = BT + (int64_t)(b * H + h0 + hl) * NCH * NCOMP + comp;
-        double sa = 0.0;
-        for (int cc = c + 1; cc < NCH; ++cc) sa += tb[(int64_t)cc * NCOMP];
+        float* x = sm.x[tid];
+        float v[CH];
+#pragma unroll
+        for (int r = 0; r < CH; ++r) v[r] = x[r];
         double rev = 0.0;
+#pragma unroll
         for (int r = CH - 1; r >= 0; --r) {
-            const float v = comp == 0 ? sm.dg[hl][r] : (comp == 1 ? sm.df[hl][r] : sm.th[r][hl * S2 + comp - 2]);
-            rev += (double)v;
+            rev += (double)v[r];
             const float tot = (float)(sa + rev);
-            float out;
-            if (comp == 0) out = -tot * softplus_grad(sm.al[r][hl]);
-            else if (comp == 1) out = tot * logsigmoid_grad(sm.zz[r][hl]);
-            else out = tot;
-            outv[r][hl * NCOMP + comp] = out;
+            x[r] = comp == 0 ? -tot * dal[r][hl] : (comp == 1 ? tot * dzz[r][hl] : tot);
         }
     }
     __syncthreads();
-    T* DP = (T*)a.dproj + (int64_t)b * a.s_db;
-    // d theta: contiguous HG*16 columns per row
-    for (int idx = tid; idx < CH * hn * S2; idx += 256) {
-        const int r = idx / (hn * S2), rem = idx % (hn * S2);
-        const int hh = rem / S2, pr = rem % S2;
-        const int row = c * CH + r;
-        if (row >= L) continue;
-        DP[(int64_t)row * a.s_dl + off.TH + (h0 + hh) * S2 + pr] = cvt<T>(outv[r][hh * NCOMP + 2 + pr]);
+    T* DP = (T*)a.dproj + (int64_t)b * a.s_db + (int64_t)c * CH * a.s_dl;
+    // d theta: 8 columns per vector
+#pragma unroll
+    for (int i = 0; i < 512 / NT; ++i) {
+        const int v = tid + NT * i;
+        const int row = v >> 3, hl = (v >> 1) & 3, half = v & 1;
+        if (row >= nrows || hl >= hn) continue;
+        f32x4 lo, hi;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            lo[j] = sm.x[hl * NCOMP + 2 + 8 * half + j][row];
+            hi[j] = sm.x[hl * NCOMP + 6 + 8 * half + j][row];
+        }
+        *reinterpret_cast<frag8<T>*>(DP + (int64_t)row * a.s_dl + off.TH + (h0 + hl) * S2 + 8 * half) =
+            pack8<T>(lo, hi);
     }
-    for (int idx = tid; idx < CH * hn; idx += 256) {
-        const int r = idx / hn, hh = idx % hn;
-        const int row = c * CH + r;
-        if (row >= L) continue;
-        DP[(int64_t)row * a.s_dl + off.A + h0 + hh] = cvt<T>(outv[r][hh * NCOMP + 0]);
-        if (a.dz) a.dz[(int64_t)b * a.s_dzb + (int64_t)row * a.s_dzl + h0 + hh] = outv[r][hh * NCOMP + 1];
+    if (tid < CH * HG) {
+        const int row = tid >> 2, hl = tid & 3;
+        if (row < nrows && hl < hn) {
+            DP[(int64_t)row * a.s_dl + off.A + h0 + hl] = cvt<T>(sm.x[hl * NCOMP + 0][row]);
+            if (a.dz) a.dz[(int64_t)b * a.s_dzb + (int64_t)(c * CH + row) * a.s_dzl + h0 + hl] = sm.x[hl * NCOMP + 1][row];
+        }
     }
     // zero padding columns (they multiply the zero rows of W_cat; keeps NaN out of dX)
     if (blockIdx.z == 0 && off.NPAD > off.NTOT) {
         const int npad = off.NPAD - off.NTOT;
-        for (int idx = tid; idx < CH * npad; idx += 256) {
+        for (int idx = tid; idx < CH * npad; idx += NT) {
             const int r = idx / npad, j = idx % npad;
-            const int row = c * CH + r;
-            if (row >= L) continue;
-            DP[(int64_t)row * a.s_dl + off.NTOT + j] = cvt<T>(0.f);
+            if (r < nrows) DP[(int64_t)r * a.s_dl + off.NTOT + j] = cvt<T>(0.f);
         }
     }
 }
@@ -381,20 +450,20 @@ __global__ __launch_bounds__(256) void prep_bwd_kernel(sisa_prep_bwd_args a) {
 template <class T>
 int launch_prep_fwd(const sisa_prep_fwd_args* a, hipStream_t st) {
     dim3 grid((unsigned)sisa::cdiv(a->L, CH), (unsigned)a->B, (unsigned)sisa::cdiv(a->H, HG));
-    prep_sums_kernel<T><<<grid, 256, 0, st>>>(*a);
+    prep_sums_kernel<T><<<grid, NT, 0, st>>>(*a);
     int rc = sisa::launch_status("sisa_prep_fwd (sums)");
     if (rc) return rc;
-    prep_fwd_kernel<T><<<grid, 256, 0, st>>>(*a);
+    prep_fwd_kernel<T><<<grid, NT, 0, st>>>(*a);
     return sisa::launch_status("sisa_prep_fwd");
 }
 
 template <class T>
 int launch_prep_bwd(const sisa_prep_bwd_args* a, hipStream_t st) {
     dim3 grid((unsigned)sisa::cdiv(a->L, CH), (unsigned)a->B, (unsigned)sisa::cdiv(a->H, HG));
-    prep_bsums_kernel<T><<<grid, 256, 0, st>>>(*a);
+    prep_bsums_kernel<T><<<grid, NT, 0, st>>>(*a);
     int rc = sisa::launch_status("sisa_prep_bwd (sums)");
     if (rc) return rc;
-    prep_bwd_kernel<T><<<grid, 256, 0, st>>>(*a);
+    prep_bwd_kernel<T><<<grid, NT, 0, st>>>(*a);
     return sisa::launch_status("sisa_prep_bwd");
 }
 
@@ -406,14 +475,16 @@ extern "C" int sisa_prep_fwd(const sisa_prep_fwd_args* a, void* stream) {
     SISA_REQUIRE(a->dtype == SISA_BF16 || a->dtype == SISA_F16, "sisa_prep_fwd: proj dtype must be bf16/fp16");
     SISA_REQUIRE(a->proj && a->cr && a->br && a->g && a->rowf && a->colf && a->tot, "sisa_prep_fwd: null pointer");
     SISA_REQUIRE(a->z == nullptr || a->f != nullptr, "sisa_prep_fwd: f is required with z");
-    SISA_REQUIRE(a->s_pl >= layout_of(a->H).NPAD && (a->s_pl % 2) == 0, "sisa_prep_fwd: proj row stride %lld",
-                 (long long)a->s_pl);
+    SISA_REQUIRE(a->s_pl >= layout_of(a->H).NPAD && a->s_pl % 8 == 0 && a->s_pb % 8 == 0 && sisa::aligned16(a->proj),
+                 "sisa_prep_fwd: proj must be 16-byte aligned with row and batch strides that are multiples of 8 "
+                 "(row stride %lld)", (long long)a->s_pl);
+    SISA_REQUIRE(sisa::aligned16(a->cr) && sisa::aligned16(a->br), "sisa_prep_fwd: cr/br must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     return a->dtype == SISA_BF16 ? launch_prep_fwd<__bf16>(a, st) : launch_prep_fwd<_Float16>(a, st);
 }
 
 extern "C" int64_t sisa_prep_bwd_workspace_bytes(int32_t B, int32_t L, int32_t H) {
-    return (int64_t)B * H * sisa::cdiv(L, CH) * NCOMP * (int64_t)sizeof(double);
+    return bt_bytes(B, L, H) + (int64_t)B * L * H * S2 * (int64_t)sizeof(float);
 }
 
 extern "C" int sisa_prep_bwd(const sisa_prep_bwd_args* a, void* stream) {
@@ -424,7 +495,12 @@ extern "C" int sisa_prep_bwd(const sisa_prep_bwd_args* a, void* stream) {
                  "sisa_prep_bwd: null pointer");
     SISA_REQUIRE((a->z == nullptr) == (a->df == nullptr) && (a->z == nullptr) == (a->dz == nullptr),
                  "sisa_prep_bwd: z, df and dz must all be given or all be null");
-    SISA_REQUIRE(a->s_pl >= layout_of(a->H).NPAD && a->s_dl >= layout_of(a->H).NPAD, "sisa_prep_bwd: row strides");
+    SISA_REQUIRE(a->s_pl >= layout_of(a->H).NPAD && a->s_dl >= layout_of(a->H).NPAD && a->s_pl % 8 == 0 &&
+                     a->s_pb % 8 == 0 && a->s_dl % 8 == 0 && a->s_db % 8 == 0,
+                 "sisa_prep_bwd: row strides must be >= NPAD and, like the batch strides, multiples of 8");
+    SISA_REQUIRE(sisa::aligned16(a->proj) && sisa::aligned16(a->dproj) && sisa::aligned16(a->dcr) &&
+                     sisa::aligned16(a->dbr) && sisa::aligned16(a->workspace),
+                 "sisa_prep_bwd: proj, dproj, dcr, dbr and workspace must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     return a->dtype == SISA_BF16 ? launch_prep_bwd<__bf16>(a, st) : launch_prep_bwd<_Float16>(a, st);
 }
