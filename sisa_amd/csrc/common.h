@@ -27,7 +27,7 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 static constexpr float LOG2E = 1.4426950408889634f;
-static constexpr int LDS_PAD = 8;   // elements of padding per LDS tile row
+static constexpr int LDS_PAD = 16;  // elements of padding per LDS tile row
 
 template <class T> struct Vec;
 template <> struct Vec<__bf16> { typedef bf16x8 x8; typedef bf16x4 x4; typedef bf16x2 x2; };
