@@ -75,6 +75,17 @@ SISA_DEV void store_row4(TO* p, f32x4 v) {
     store4<TO>(p, to_vec4<TO>(v));
 }
 
+// Workgroup i of a 1-D grid of nrank * BH workgroups -> (bh, rank). Workgroups are dispatched round-robin over the 8
+// XCDs (workgroup i runs on XCD i % 8), each with its own L2: the mapping gives every XCD a contiguous range of
+// (bh, rank) so that the workgroups sharing one head's K/V (or Q/dO) tiles run on one XCD and read them from HBM
+// once. Within an XCD's range the ranks of a head are dispatched in order.
+SISA_DEV void xcd_map(int i, int nrank, int BH, int& bh, int& rank) {
+    const int total = nrank * BH;
+    const int j = (total % 8 == 0) ? (i % 8) * (total / 8) + i / 8 : i;
+    bh = j / nrank;
+    rank = j % nrank;
+}
+
 // ------------------------------------------------------------------------------------------------ forward
 // Scores are computed transposed (S^T = K Q^T): a lane owns one query's softmax state and the 16x16 C blocks of S^T
 // are directly the B fragments of O^T += V^T P^T. Per tile and wave one of two code paths runs (uniform branch):
@@ -164,9 +175,10 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
     __shared__ FwdLds<T> sm;
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int NQT = gridDim.x;
-    const int tile = NQT - 1 - (int)blockIdx.x;   // heavy (late) query tiles first
-    const int bh = blockIdx.y;
+    const int NQT = (a.L + 127) / 128;
+    int bh, rank;
+    xcd_map(blockIdx.x, NQT, a.B * a.H, bh, rank);
+    const int tile = NQT - 1 - rank;               // heavy (late) query tiles first
     const int H = a.H, L = a.L;
     const int b = bh / H, h = bh % H;
     const bool has_f = a.f.ptr != nullptr;
@@ -362,9 +374,10 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
     __shared__ DqLds<T> sm;
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int NQT = gridDim.x;
-    const int tile = NQT - 1 - (int)blockIdx.x;
-    const int bh = blockIdx.y;
+    const int NQT = (a.L + 63) / 64;
+    int bh, rank;
+    xcd_map(blockIdx.x, NQT, a.B * a.H, bh, rank);
+    const int tile = NQT - 1 - rank;               // heavy (late) query blocks first
     const int H = a.H, L = a.L;
     const int b = bh / H, h = bh % H;
     const bool has_f = a.f.ptr != nullptr;
@@ -622,8 +635,8 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
     __shared__ DkvLds<T> sm;
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int ktile = blockIdx.x;                  // early key tiles carry the most queries: first
-    const int bh = blockIdx.y;
+    int bh, ktile;
+    xcd_map(blockIdx.x, (a.L + 63) / 64, a.B * a.H, bh, ktile);   // early key blocks carry the most queries: first
     const int H = a.H, L = a.L;
     const int b = bh / H, h = bh % H;
     const bool has_f = a.f.ptr != nullptr;
@@ -776,14 +789,14 @@ __global__ __launch_bounds__(1024) void dlam_kernel(const float* __restrict__ rl
 
 template <class T>
 int launch_fwd(const sisa_attn_fwd_args* a, hipStream_t st) {
-    dim3 grid((unsigned)sisa::cdiv(a->L, 128), (unsigned)(a->B * a->H));
+    const dim3 grid((unsigned)(sisa::cdiv(a->L, 128) * a->B * a->H));
     attn_fwd_kernel<T><<<grid, NTH, 0, st>>>(*a, 0.125f);
     return sisa::launch_status("sisa_attn_fwd");
 }
 
 template <class T>
 int launch_bwd(const sisa_attn_bwd_args* a, hipStream_t st) {
-    dim3 grid((unsigned)sisa::cdiv(a->L, 64), (unsigned)(a->B * a->H));
+    const dim3 grid((unsigned)(sisa::cdiv(a->L, 64) * a->B * a->H));
     attn_bwd_dq_kernel<T><<<grid, NTHB, 0, st>>>(*a, 0.125f);
     int rc = sisa::launch_status("sisa_attn_bwd (dq)");
     if (rc) return rc;
@@ -813,6 +826,8 @@ extern "C" int sisa_factors(const sisa_factors_args* a, void* stream) {
 extern "C" int sisa_attn_fwd(const sisa_attn_fwd_args* a, void* stream) {
     SISA_REQUIRE(a != nullptr, "sisa_attn_fwd: null args");
     SISA_REQUIRE(a->B >= 1 && a->H >= 1 && a->L >= 1, "sisa_attn_fwd: bad shape B=%d H=%d L=%d", a->B, a->H, a->L);
+    SISA_REQUIRE((int64_t)a->B * a->H * sisa::cdiv(a->L, 64) * 512 < ((int64_t)1 << 31),
+                 "sisa_attn_fwd: B*H*L too large for one launch");
     SISA_REQUIRE(a->dtype == SISA_BF16 || a->dtype == SISA_F16 || a->dtype == SISA_F32, "sisa_attn_fwd: dtype %d",
                  a->dtype);
     SISA_REQUIRE(sisa::view_ok(a->q, a->dtype) && sisa::view_ok(a->k, a->dtype) && sisa::view_ok(a->v, a->dtype) &&
@@ -838,6 +853,8 @@ extern "C" int64_t sisa_attn_bwd_workspace_bytes(int32_t B, int32_t H, int32_t L
 extern "C" int sisa_attn_bwd(const sisa_attn_bwd_args* a, void* stream) {
     SISA_REQUIRE(a != nullptr, "sisa_attn_bwd: null args");
     SISA_REQUIRE(a->B >= 1 && a->H >= 1 && a->L >= 1, "sisa_attn_bwd: bad shape B=%d H=%d L=%d", a->B, a->H, a->L);
+    SISA_REQUIRE((int64_t)a->B * a->H * sisa::cdiv(a->L, 64) * 512 < ((int64_t)1 << 31),
+                 "sisa_attn_bwd: B*H*L too large for one launch");
     SISA_REQUIRE(a->dtype == SISA_BF16 || a->dtype == SISA_F16 || a->dtype == SISA_F32, "sisa_attn_bwd: dtype %d",
                  a->dtype);
     SISA_REQUIRE(a->dcb_dtype == a->dtype || a->dcb_dtype == SISA_F32, "sisa_attn_bwd: dc/db dtype %d",
