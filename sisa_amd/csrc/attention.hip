@@ -172,7 +172,8 @@ SISA_DEV void fwd_tile(const FwdLds<T>& sm, const float* cfm, int lane, int n0, 
 
 template <class T>
 __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void attn_fwd_kernel(sisa_attn_fwd_args a, float scale) {
-    __shared__ FwdLds<T> sm;
+    constexpr int NBUF = sizeof(T) == 2 ? 2 : 1;
+    __shared__ FwdLds<T> smb[NBUF];
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int NQT = (a.L + 127) / 128;
@@ -221,40 +222,83 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
 #pragma unroll
     for (int db = 0; db < 5; ++db) acc[db] = zero4();
 
+    // Key tiles are staged through registers into LDS. 16-bit types double-buffer the LDS tiles: tile t+1 is stored
+    // into the idle buffer while tile t is computed, one barrier per tile. fp32 tiles do not fit twice and use one
+    // buffer with a barrier on each side of the store.
     TileStage<T, DH, NTH> stk, stv;
     TileStage<T, DS, NTH> stb;
     const int kend = (tile0 + 128 < L) ? tile0 + 128 : L;
-    stk.load(K, skl, L < 64 ? L : 64, tid);
-    stv.load(V, svl, L < 64 ? L : 64, tid);
-    stb.load(Bm, sbl, L < 64 ? L : 64, tid);
-    for (int n0 = 0; n0 < kend; n0 += 64) {
-        __syncthreads();
-        stk.store(sm.ks, tid);
-        stv.store(sm.vs, tid);
-        stb.store(sm.bs, tid);
+    auto load_tile = [&](int n0) {
+        const int nv = (L - n0 < 64) ? L - n0 : 64;
+        stk.load(K + (int64_t)n0 * skl, skl, nv, tid);
+        stv.load(V + (int64_t)n0 * svl, svl, nv, tid);
+        stb.load(Bm + (int64_t)n0 * sbl, sbl, nv, tid);
+    };
+    auto stage_tile = [&](FwdLds<T>& d, int n0) {
+        stk.store(d.ks, tid);
+        stv.store(d.vs, tid);
+        stb.store(d.bs, tid);
         if (tid < 64) {
             const int j = n0 + tid;
             const int jc = j < L ? j : L - 1;
-            sm.fk[tid] = (has_f && j < L) ? FF[(int64_t)j * sfl] : 0.f;
-            sm.gk[tid] = G[(int64_t)jc * sgl];
+            d.fk[tid] = (has_f && j < L) ? FF[(int64_t)j * sfl] : 0.f;
+            d.gk[tid] = G[(int64_t)jc * sgl];
             const float cf = j < L ? COLF[j] : 0.f;
             const float ge = G[(int64_t)(n0 + 63 < L ? n0 + 63 : L - 1) * sgl];   // end of the key block
-            sm.cfm[0][tid] = cf * exp2_le0((ga0 - ge) * LOG2E);
-            sm.cfm[1][tid] = cf * exp2_le0((ga1 - ge) * LOG2E);
+            d.cfm[0][tid] = cf * exp2_le0((ga0 - ge) * LOG2E);
+            d.cfm[1][tid] = cf * exp2_le0((ga1 - ge) * LOG2E);
         }
-        __syncthreads();
-        const int n1 = n0 + 64;
-        if (n1 < kend) {                           // next tile's loads are in flight during this tile's math
-            const int nv = (L - n1 < 64) ? L - n1 : 64;
-            stk.load(K + (int64_t)n1 * skl, skl, nv, tid);
-            stv.load(V + (int64_t)n1 * svl, svl, nv, tid);
-            stb.load(Bm + (int64_t)n1 * sbl, sbl, nv, tid);
+    };
+    // Advance to tile t (key offset 64 t): the tile is in LDS buffer t & (NBUF-1) afterwards; with two buffers the
+    // store of tile t+1 and the loads of tile t+2 are issued here too.
+    auto advance = [&](int t) {
+        const int n0 = 64 * t;
+        if (NBUF == 2) {
+            if (n0 + 64 < kend) {
+                stage_tile(smb[(t + 1) & (NBUF - 1)], n0 + 64);
+                if (n0 + 128 < kend) load_tile(n0 + 128);
+            }
+        } else {
+            if (t > 0) {
+                __syncthreads();
+                stage_tile(smb[0], n0);
+                __syncthreads();
+            }
+            if (n0 + 64 < kend) load_tile(n0 + 64);
         }
-        if (!live) continue;
-        if (n0 + 63 < q0)
-            fwd_tile<T, false>(sm, sm.cfm[qblk], lane, n0, q0, L, qf, cfr, onesf, fq, rs, gq, lam, scale, m, l, acc);
-        else if (n0 <= q0 + 15)
-            fwd_tile<T, true>(sm, sm.cfm[qblk], lane, n0, q0, L, qf, cfr, onesf, fq, rs, gq, lam, scale, m, l, acc);
+    };
+    load_tile(0);
+    stage_tile(smb[0], 0);
+    if (NBUF == 2 && 64 < kend) load_tile(64);
+    __syncthreads();
+    // tiles before the workgroup's first query block: off-block for every wave (one code path in the loop)
+    const int nfull = tile0 / 64;
+    for (int t = 0; t < nfull; ++t) {
+        advance(t);
+        if (live) {
+            const FwdLds<T>& sm = smb[t & (NBUF - 1)];
+            fwd_tile<T, false>(sm, sm.cfm[qblk], lane, 64 * t, q0, L, qf, cfr, onesf, fq, rs, gq, lam, scale, m, l,
+                               acc);
+        }
+        if (NBUF == 2) __syncthreads();
+    }
+    // the workgroup's own tiles: block 0's (off-block for block 1's waves), then block 1's
+    advance(nfull);
+    if (live) {
+        const FwdLds<T>& sm = smb[nfull & (NBUF - 1)];
+        if (qblk == 0)
+            fwd_tile<T, true>(sm, sm.cfm[0], lane, tile0, q0, L, qf, cfr, onesf, fq, rs, gq, lam, scale, m, l, acc);
+        else
+            fwd_tile<T, false>(sm, sm.cfm[1], lane, tile0, q0, L, qf, cfr, onesf, fq, rs, gq, lam, scale, m, l, acc);
+    }
+    if (tile0 + 64 < kend) {
+        if (NBUF == 2) __syncthreads();
+        advance(nfull + 1);
+        if (live && qblk == 1) {
+            const FwdLds<T>& sm = smb[(nfull + 1) & (NBUF - 1)];
+            fwd_tile<T, true>(sm, sm.cfm[1], lane, tile0 + 64, q0, L, qf, cfr, onesf, fq, rs, gq, lam, scale, m, l,
+                              acc);
+        }
     }
     if (!live) return;
     T* O = (T*)a.o.ptr + (int64_t)b * a.o.sb + (int64_t)h * a.o.sh;
