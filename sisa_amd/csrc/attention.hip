@@ -28,6 +28,8 @@ namespace {
 constexpr int DH = 64;   // d_head
 constexpr int DS = 32;   // d_state
 constexpr int BLK = 64;  // decay-factor block (rowf/colf anchors)
+constexpr float RESCALE_LOG2 = 8.f;   // forward: largest exponent of an unrescaled softmax weight (2^8)
+constexpr float M_FLOOR = -1e30f;     // forward: initial running maximum (finite, so exp2(-inf - m) = 0)
 
 // Forward: 8 waves per workgroup, 16 rows (one column group of the MFMA block) per wave, 128 rows per workgroup,
 // 64-position tiles of the other operand staged row-major in LDS.
@@ -144,23 +146,31 @@ SISA_DEV void fwd_tile(const FwdLds<T>& sm, const float* cfm, int lane, int n0, 
             }
         }
     }
-    // online softmax in log2 units; a NaN score reaches l through its exponential
-    const float mn = fmaxf(m, group_max(mloc) * LOG2E);
-    const float mu = (mn == -__builtin_inff()) ? 0.f : mn;
-    const float corr = fast_exp2(m - mu);
-    m = mu;
+    // Online softmax in log2 units with lazy rescaling: a query's running offset m moves (and its l, acc are
+    // rescaled) only when its tile maximum exceeds m by more than RESCALE_LOG2, so the exponentials stay below
+    // 2^RESCALE_LOG2. The decision is per query (a query's results never depend on its neighbours); the wave skips
+    // the rescale when no query needs it, and queries that do not need it multiply by exactly 1. m starts at a
+    // finite floor, so fully masked rows give exp2(-inf) = 0. A NaN score reaches l through its exponential.
+    const float mt = group_max(mloc) * LOG2E;
+    const bool need = mt > m + RESCALE_LOG2;
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+        const float mn = need ? fmaxf(m, mt) : m;
+        const float corr = fast_exp2(m - mn);
+        m = mn;
+        l *= corr;
+#pragma unroll
+        for (int db = 0; db < 5; ++db) acc[db] *= corr;
+    }
     float ls = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float pe = fast_exp2(fmaf(sc[kb][i], LOG2E, -mu));
+            const float pe = fast_exp2(fmaf(sc[kb][i], LOG2E, -m));
             sc[kb][i] = pe;
             ls += pe;
         }
-    l = l * corr + ls;
-#pragma unroll
-    for (int db = 0; db < 5; ++db) acc[db] *= corr;
+    l += ls;
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
         const frag8<T> pf = pack8<T>(sc[2 * st], sc[2 * st + 1]);
@@ -217,7 +227,7 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
     }
     const frag8<T> onesf = ones_row_frag<T>(lane);
 
-    float m = -__builtin_inff(), l = 0.f;
+    float m = M_FLOOR, l = 0.f;
     f32x4 acc[5];
 #pragma unroll
     for (int db = 0; db < 5; ++db) acc[db] = zero4();
@@ -225,14 +235,19 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
     // Key tiles are staged through registers into LDS. 16-bit types double-buffer the LDS tiles: tile t+1 is stored
     // into the idle buffer while tile t is computed, one barrier per tile. fp32 tiles do not fit twice and use one
     // buffer with a barrier on each side of the store.
-    TileStage<T, DH, NTH> stk, stv;
-    TileStage<T, DS, NTH> stb;
+    BufStage<T, DH, NTH> stk, stv;
+    BufStage<T, DS, NTH> stb;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(K, ((int64_t)(L - 1) * skl + DH) * (int64_t)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(V, ((int64_t)(L - 1) * svl + DH) * (int64_t)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bm, ((int64_t)(L - 1) * sbl + DS) * (int64_t)sizeof(T));
+    stk.init(skl, tid);
+    stv.init(svl, tid);
+    stb.init(sbl, tid);
     const int kend = (tile0 + 128 < L) ? tile0 + 128 : L;
     auto load_tile = [&](int n0) {
-        const int nv = (L - n0 < 64) ? L - n0 : 64;
-        stk.load(K + (int64_t)n0 * skl, skl, nv, tid);
-        stv.load(V + (int64_t)n0 * svl, svl, nv, tid);
-        stb.load(Bm + (int64_t)n0 * sbl, sbl, nv, tid);
+        stk.load(rk, (int)(n0 * skl * (int64_t)sizeof(T)), tid);
+        stv.load(rv, (int)(n0 * svl * (int64_t)sizeof(T)), tid);
+        stb.load(rb, (int)(n0 * sbl * (int64_t)sizeof(T)), tid);
     };
     auto stage_tile = [&](FwdLds<T>& d, int n0) {
         stk.store(d.ks, tid);
@@ -867,6 +882,11 @@ extern "C" int sisa_factors(const sisa_factors_args* a, void* stream) {
     return sisa::launch_status("sisa_factors");
 }
 
+// The sequence extent of one (batch, head) slice of a view, addressed through one buffer resource.
+static bool extent_ok(const sisa_view& v, int L, int C, int dtype) {
+    return v.sl >= 0 && ((int64_t)(L - 1) * v.sl + C) * sisa::elem_size(dtype) < ((int64_t)1 << 31);
+}
+
 extern "C" int sisa_attn_fwd(const sisa_attn_fwd_args* a, void* stream) {
     SISA_REQUIRE(a != nullptr, "sisa_attn_fwd: null args");
     SISA_REQUIRE(a->B >= 1 && a->H >= 1 && a->L >= 1, "sisa_attn_fwd: bad shape B=%d H=%d L=%d", a->B, a->H, a->L);
@@ -879,6 +899,9 @@ extern "C" int sisa_attn_fwd(const sisa_attn_fwd_args* a, void* stream) {
                  "sisa_attn_fwd: q/k/v/c/b/o must be non-null with 16-byte aligned rows");
     SISA_REQUIRE(g_view_ok(a->g) && a->lam && a->rowf && a->colf && a->lse, "sisa_attn_fwd: null pointer");
     SISA_REQUIRE(a->o32 == nullptr || sisa::aligned16(a->o32), "sisa_attn_fwd: o32 not aligned");
+    SISA_REQUIRE(extent_ok(a->k, a->L, DH, a->dtype) && extent_ok(a->v, a->L, DH, a->dtype) &&
+                     extent_ok(a->b, a->L, DS, a->dtype),
+                 "sisa_attn_fwd: a (batch, head) slice of k/v/b spans 2 GiB or more");
     hipStream_t st = (hipStream_t)stream;
     switch (a->dtype) {
         case SISA_BF16: return launch_fwd<__bf16>(a, st);

@@ -153,6 +153,55 @@ struct TileStage {
     }
 };
 
+// Buffer-resource staging of the same (64 x C) tiles: one resource per (batch, head) view covering rows 0..L-1, a
+// per-lane byte offset that does not change from tile to tile, and the tile's row offset as a wave-uniform scalar.
+// Rows at or beyond L fall outside the resource and read as zero (no per-row bounds test, no 64-bit address
+// arithmetic per tile). The view's extent must be below 2^31 bytes (checked by the host).
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+SISA_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+template <class T>
+SISA_DEV frag8<T> buf_load8(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    if constexpr (sizeof(T) == 2) {
+        return __builtin_bit_cast(frag8<T>, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+    } else {
+        const f32x4 lo = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+        const f32x4 hi = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, 0));
+        return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+}
+
+template <class T, int C, int NTH>
+struct BufStage {
+    static constexpr int NVEC = 64 * C / 8;
+    static constexpr int PER = (NVEC + NTH - 1) / NTH;
+    frag8<T> v[PER];
+    int voff[PER];
+
+    SISA_DEV void init(int64_t srow, int tid) {
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            const int idx = tid + p * NTH;
+            voff[p] = (int)(((idx / (C / 8)) * srow + (idx % (C / 8)) * 8) * (int64_t)sizeof(T));
+        }
+    }
+    // rows [row0, row0 + 64) of the view; soff = row0 * srow * sizeof(T)
+    SISA_DEV void load(__amdgpu_buffer_rsrc_t r, int soff, int tid) {
+#pragma unroll
+        for (int p = 0; p < PER; ++p)
+            v[p] = (tid + p * NTH < NVEC) ? buf_load8<T>(r, voff[p], soff) : zero8<T>();
+    }
+    SISA_DEV void store(T* __restrict__ X, int tid) const {
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            const int idx = tid + p * NTH;
+            const int row = idx / (C / 8), c8 = idx % (C / 8);
+            if (idx < NVEC) *reinterpret_cast<frag8<T>*>(X + row * (C + LDS_PAD) + c8 * 8) = v[p];
+        }
+    }
+};
+
 // Operand fragment of a row-major LDS tile X: row (position) r0 + lane%16, features 32*step + 8*grp + 0..7
 // (feature-contracted products: A/B operand whose row is a position).
 template <class T, int C>
