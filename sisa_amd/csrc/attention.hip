@@ -508,11 +508,17 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
     dca[0] = dca[1] = zero4();
     RowSums R{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 
-    TileStage<T, DH, NTHB> stk, stv;
-    TileStage<T, DS, NTHB> stb;
-    stk.load(K, skl, L < 64 ? L : 64, tid);
-    stv.load(V, svl, L < 64 ? L : 64, tid);
-    stb.load(Bm, sbl, L < 64 ? L : 64, tid);
+    BufStage<T, DH, NTHB> stk, stv;
+    BufStage<T, DS, NTHB> stb;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(K, ((int64_t)(L - 1) * skl + DH) * (int64_t)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(V, ((int64_t)(L - 1) * svl + DH) * (int64_t)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bm, ((int64_t)(L - 1) * sbl + DS) * (int64_t)sizeof(T));
+    stk.init(skl, tid);
+    stv.init(svl, tid);
+    stb.init(sbl, tid);
+    stk.load(rk, 0, tid);
+    stv.load(rv, 0, tid);
+    stb.load(rb, 0, tid);
     // key tiles before the block (all off-block), then the block's own tile
     for (int n0 = 0; n0 <= tile0; n0 += 64) {
         __syncthreads();
@@ -530,11 +536,10 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
         }
         __syncthreads();
         const int n1 = n0 + 64;
-        if (n1 <= tile0) {                         // next tile: full, or the block's own (ragged at the end)
-            const int nv = (L - n1 < 64) ? L - n1 : 64;
-            stk.load(K + (int64_t)n1 * skl, skl, nv, tid);
-            stv.load(V + (int64_t)n1 * svl, svl, nv, tid);
-            stb.load(Bm + (int64_t)n1 * sbl, sbl, nv, tid);
+        if (n1 <= tile0) {                         // next tile: full, or the block's own (rows >= L read as zero)
+            stk.load(rk, (int)(n1 * skl * (int64_t)sizeof(T)), tid);
+            stv.load(rv, (int)(n1 * svl * (int64_t)sizeof(T)), tid);
+            stb.load(rb, (int)(n1 * sbl * (int64_t)sizeof(T)), tid);
         }
         if (!live) continue;
         if (n0 < tile0)
@@ -748,14 +753,19 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
     // column sums (diagonal excluded); off-block tiles accumulate dgu without the column factor colf
     float dgu = 0.f, dfs = 0.f;
 
-    TileStage<T, DH, NTHB> stq, std_;
-    TileStage<T, DS, NTHB> stc;
+    BufStage<T, DH, NTHB> stq, std_;
+    BufStage<T, DS, NTHB> stc;
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(Q, ((int64_t)(L - 1) * sql + DH) * (int64_t)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rd = make_rsrc(DO, ((int64_t)(L - 1) * sdl + DH) * (int64_t)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(C, ((int64_t)(L - 1) * scl + DS) * (int64_t)sizeof(T));
+    stq.init(sql, tid);
+    std_.init(sdl, tid);
+    stc.init(scl, tid);
     const int mlast = (L - 1) / 64 * 64;
     {
-        const int nv = L - mlast;
-        stq.load(Q + (int64_t)mlast * sql, sql, nv, tid);
-        std_.load(DO + (int64_t)mlast * sdl, sdl, nv, tid);
-        stc.load(C + (int64_t)mlast * scl, scl, nv, tid);
+        stq.load(rq, (int)(mlast * sql * (int64_t)sizeof(T)), tid);
+        std_.load(rd, (int)(mlast * sdl * (int64_t)sizeof(T)), tid);
+        stc.load(rc, (int)(mlast * scl * (int64_t)sizeof(T)), tid);
     }
     // query tiles after the block (all off-block, descending), then the block's own tile
     for (int m0 = mlast; m0 >= ktile0; m0 -= 64) {
@@ -779,9 +789,9 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
         __syncthreads();
         const int m1 = m0 - 64;
         if (m1 >= ktile0) {                        // every tile below mlast is full
-            stq.load(Q + (int64_t)m1 * sql, sql, 64, tid);
-            std_.load(DO + (int64_t)m1 * sdl, sdl, 64, tid);
-            stc.load(C + (int64_t)m1 * scl, scl, 64, tid);
+            stq.load(rq, (int)(m1 * sql * (int64_t)sizeof(T)), tid);
+            std_.load(rd, (int)(m1 * sdl * (int64_t)sizeof(T)), tid);
+            stc.load(rc, (int)(m1 * scl * (int64_t)sizeof(T)), tid);
         }
         if (!live) continue;
         if (m0 > ktile0)
@@ -935,6 +945,10 @@ extern "C" int sisa_attn_bwd(const sisa_attn_bwd_args* a, void* stream) {
                  "sisa_attn_bwd: tensors must be non-null with 16-byte aligned rows");
     SISA_REQUIRE(g_view_ok(a->g) && a->lam && a->rowf && a->colf && a->lse && a->dg && a->dlam && a->workspace,
                  "sisa_attn_bwd: null pointer");
+    SISA_REQUIRE(extent_ok(a->q, a->L, DH, dt) && extent_ok(a->k, a->L, DH, dt) && extent_ok(a->v, a->L, DH, dt) &&
+                     extent_ok(a->dout, a->L, DH, dt) && extent_ok(a->c, a->L, DS, dt) &&
+                     extent_ok(a->b, a->L, DS, dt),
+                 "sisa_attn_bwd: a (batch, head) slice of q/k/v/do/c/b spans 2 GiB or more");
     SISA_REQUIRE((a->f.ptr == nullptr) == (a->df == nullptr), "sisa_attn_bwd: f and df must both be given or null");
     SISA_REQUIRE(a->o32 == nullptr || (sisa::aligned16(a->o32) && dt != SISA_F32), "sisa_attn_bwd: bad o32");
     hipStream_t st = (hipStream_t)stream;
