@@ -94,10 +94,10 @@ SISA_DEV void xcd_map(int i, int nrank, int BH, int& bh, int& rank) {
 // off-block tiles (every key in an earlier 64-block than the wave's queries; chunk-factored decay, no masks) or the
 // wave's own block (pairwise decay and the causal mask).
 template <class T>
-struct FwdLds {
-    T ks[64 * (DH + LDS_PAD)];   // K tile
-    T bs[64 * (DS + LDS_PAD)];   // B~ tile
-    T vs[64 * (DH + LDS_PAD)];   // V tile
+struct __attribute__((aligned(16))) FwdLds {
+    T ks[64 * DH];               // K tile
+    T bs[64 * DS];               // B~ tile
+    T vs[64 * DH];               // V tile
     float fk[64], gk[64];        // F and g at the tile's keys
     float cfm[2][64];            // colf * mid for the workgroup's two query blocks
 };
@@ -232,59 +232,60 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
 #pragma unroll
     for (int db = 0; db < 5; ++db) acc[db] = zero4();
 
-    // Key tiles are staged through registers into LDS. 16-bit types double-buffer the LDS tiles: tile t+1 is stored
-    // into the idle buffer while tile t is computed, one barrier per tile. fp32 tiles do not fit twice and use one
-    // buffer with a barrier on each side of the store.
-    BufStage<T, DH, NTH> stk, stv;
-    BufStage<T, DS, NTH> stb;
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(K, ((int64_t)(L - 1) * skl + DH) * (int64_t)sizeof(T));
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(V, ((int64_t)(L - 1) * svl + DH) * (int64_t)sizeof(T));
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bm, ((int64_t)(L - 1) * sbl + DS) * (int64_t)sizeof(T));
-    stk.init(skl, tid);
-    stv.init(svl, tid);
-    stb.init(sbl, tid);
+    // Key tiles go straight from global memory into LDS (DMA buffer loads). 16-bit types double-buffer the tiles:
+    // tile t+1 is issued into the idle buffer while tile t is computed, one barrier per tile. fp32 tiles do not fit
+    // twice and use one buffer with a barrier on each side of the issue. The per-key scalars of the next tile are
+    // fetched into registers by the first wave one tile ahead.
+    DmaStage<T, DH, NW> dk, dv;
+    DmaStage<T, DS, NW> dbt;
+    const int64_t xk = ((int64_t)(L - 1) * skl + DH) * (int64_t)sizeof(T);   // view extents (bytes)
+    const int64_t xv = ((int64_t)(L - 1) * svl + DH) * (int64_t)sizeof(T);
+    const int64_t xb = ((int64_t)(L - 1) * sbl + DS) * (int64_t)sizeof(T);
+    dk.init(skl, w, lane);
+    dv.init(svl, w, lane);
+    dbt.init(sbl, w, lane);
     const int kend = (tile0 + 128 < L) ? tile0 + 128 : L;
-    auto load_tile = [&](int n0) {
-        stk.load(rk, (int)(n0 * skl * (int64_t)sizeof(T)), tid);
-        stv.load(rv, (int)(n0 * svl * (int64_t)sizeof(T)), tid);
-        stb.load(rb, (int)(n0 * sbl * (int64_t)sizeof(T)), tid);
-    };
-    auto stage_tile = [&](FwdLds<T>& d, int n0) {
-        stk.store(d.ks, tid);
-        stv.store(d.vs, tid);
-        stb.store(d.bs, tid);
+    float pf_f = 0.f, pf_g = 0.f, pf_cf = 0.f, pf_ge = 0.f;
+    auto fetch_scalars = [&](int n0) {
         if (tid < 64) {
             const int j = n0 + tid;
             const int jc = j < L ? j : L - 1;
-            d.fk[tid] = (has_f && j < L) ? FF[(int64_t)j * sfl] : 0.f;
-            d.gk[tid] = G[(int64_t)jc * sgl];
-            const float cf = j < L ? COLF[j] : 0.f;
-            const float ge = G[(int64_t)(n0 + 63 < L ? n0 + 63 : L - 1) * sgl];   // end of the key block
-            d.cfm[0][tid] = cf * exp2_le0((ga0 - ge) * LOG2E);
-            d.cfm[1][tid] = cf * exp2_le0((ga1 - ge) * LOG2E);
+            pf_f = (has_f && j < L) ? FF[(int64_t)j * sfl] : 0.f;
+            pf_g = G[(int64_t)jc * sgl];
+            pf_cf = j < L ? COLF[j] : 0.f;
+            pf_ge = G[(int64_t)(n0 + 63 < L ? n0 + 63 : L - 1) * sgl];   // end of the key block
         }
     };
-    // Advance to tile t (key offset 64 t): the tile is in LDS buffer t & (NBUF-1) afterwards; with two buffers the
-    // store of tile t+1 and the loads of tile t+2 are issued here too.
+    auto issue_tile = [&](FwdLds<T>& d, int n0) {
+        dma_issue<0>(dk, K, xk, (int)(n0 * skl * (int64_t)sizeof(T)), d.ks, w);
+        dma_issue<0>(dv, V, xv, (int)(n0 * svl * (int64_t)sizeof(T)), d.vs, w);
+        dma_issue<0>(dbt, Bm, xb, (int)(n0 * sbl * (int64_t)sizeof(T)), d.bs, w);
+        if (tid < 64) {
+            d.fk[tid] = pf_f;
+            d.gk[tid] = pf_g;
+            d.cfm[0][tid] = pf_cf * exp2_le0((ga0 - pf_ge) * LOG2E);
+            d.cfm[1][tid] = pf_cf * exp2_le0((ga1 - pf_ge) * LOG2E);
+        }
+    };
+    // Advance to tile t (key offset 64 t): afterwards (and after the caller's barrier for two buffers) the tile is in
+    // LDS buffer t & (NBUF-1).
     auto advance = [&](int t) {
         const int n0 = 64 * t;
         if (NBUF == 2) {
             if (n0 + 64 < kend) {
-                stage_tile(smb[(t + 1) & (NBUF - 1)], n0 + 64);
-                if (n0 + 128 < kend) load_tile(n0 + 128);
+                issue_tile(smb[(t + 1) & (NBUF - 1)], n0 + 64);
+                if (n0 + 128 < kend) fetch_scalars(n0 + 128);
             }
-        } else {
-            if (t > 0) {
-                __syncthreads();
-                stage_tile(smb[0], n0);
-                __syncthreads();
-            }
-            if (n0 + 64 < kend) load_tile(n0 + 64);
+        } else if (t > 0) {
+            __syncthreads();
+            issue_tile(smb[0], n0);
+            __syncthreads();
+            if (n0 + 64 < kend) fetch_scalars(n0 + 64);
         }
     };
-    load_tile(0);
-    stage_tile(smb[0], 0);
-    if (NBUF == 2 && 64 < kend) load_tile(64);
+    fetch_scalars(0);
+    issue_tile(smb[0], 0);
+    if (64 < kend) fetch_scalars(64);
     __syncthreads();
     // tiles before the workgroup's first query block: off-block for every wave (one code path in the loop)
     const int nfull = tile0 / 64;
@@ -338,10 +339,10 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
 enum { WS_DELTA = 0, WS_DDEL, WS_DSD, WS_RG, WS_RL, WS_RF, WS_N };
 
 template <class T>
-struct DqLds {
-    T ks[64 * (DH + LDS_PAD)];   // K (scores; transposed reads for dq)
-    T vs[64 * (DH + LDS_PAD)];   // V (dP)
-    T bs[64 * (DS + LDS_PAD)];   // B~ (scores; transposed reads for dc)
+struct __attribute__((aligned(16))) DqLds {
+    T ks[64 * DH];               // K (scores; transposed reads for dq)
+    T vs[64 * DH];               // V (dP)
+    T bs[64 * DS];               // B~ (scores; transposed reads for dc)
     float fk[64], gk[64];
     float cfm[64];               // colf * mid for the workgroup's query block
 };
@@ -430,7 +431,8 @@ SISA_DEV void dq_tile(const DqLds<T>& sm, const float* cfm, int lane, int n0, in
 
 template <class T>
 __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void attn_bwd_dq_kernel(sisa_attn_bwd_args a, float scale) {
-    __shared__ DqLds<T> sm;
+    constexpr int NBUF = sizeof(T) == 2 ? 2 : 1;
+    __shared__ DqLds<T> smb[NBUF];
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int NQT = (a.L + 63) / 64;
@@ -508,46 +510,72 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
     dca[0] = dca[1] = zero4();
     RowSums R{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 
-    BufStage<T, DH, NTHB> stk, stv;
-    BufStage<T, DS, NTHB> stb;
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(K, ((int64_t)(L - 1) * skl + DH) * (int64_t)sizeof(T));
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(V, ((int64_t)(L - 1) * svl + DH) * (int64_t)sizeof(T));
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bm, ((int64_t)(L - 1) * sbl + DS) * (int64_t)sizeof(T));
-    stk.init(skl, tid);
-    stv.init(svl, tid);
-    stb.init(sbl, tid);
-    stk.load(rk, 0, tid);
-    stv.load(rv, 0, tid);
-    stb.load(rb, 0, tid);
-    // key tiles before the block (all off-block), then the block's own tile
-    for (int n0 = 0; n0 <= tile0; n0 += 64) {
-        __syncthreads();
-        stk.store(sm.ks, tid);
-        stv.store(sm.vs, tid);
-        stb.store(sm.bs, tid);
+    // Key tiles straight into LDS (DMA buffer loads); 16-bit types double-buffer them (one barrier per tile), fp32
+    // uses one buffer. The per-key scalars (F_j, g_j, colf_j, g at the tile's last key) are fetched into registers by
+    // the first wave one tile ahead.
+    DmaStage<T, DH, NWB> dk, dv;
+    DmaStage<T, DS, NWB> dbt;
+    const int64_t xk = ((int64_t)(L - 1) * skl + DH) * (int64_t)sizeof(T);   // view extents (bytes)
+    const int64_t xv = ((int64_t)(L - 1) * svl + DH) * (int64_t)sizeof(T);
+    const int64_t xb = ((int64_t)(L - 1) * sbl + DS) * (int64_t)sizeof(T);
+    dk.init(skl, w, lane);
+    dv.init(svl, w, lane);
+    dbt.init(sbl, w, lane);
+    float pf_f = 0.f, pf_g = 0.f, pf_cf = 0.f, pf_ge = 0.f;
+    auto fetch_scalars = [&](int n0) {
         if (tid < 64) {
             const int j = n0 + tid;
             const int jc = j < L ? j : L - 1;
-            sm.fk[tid] = (has_f && j < L) ? FF[(int64_t)j * sfl] : 0.f;
-            sm.gk[tid] = G[(int64_t)jc * sgl];
-            const float cf = j < L ? COLF[j] : 0.f;
-            const float ge = G[(int64_t)(n0 + 63 < L ? n0 + 63 : L - 1) * sgl];
-            sm.cfm[tid] = cf * exp2_le0((ga - ge) * LOG2E);
+            pf_f = (has_f && j < L) ? FF[(int64_t)j * sfl] : 0.f;
+            pf_g = G[(int64_t)jc * sgl];
+            pf_cf = j < L ? COLF[j] : 0.f;
+            pf_ge = G[(int64_t)(n0 + 63 < L ? n0 + 63 : L - 1) * sgl];
         }
-        __syncthreads();
-        const int n1 = n0 + 64;
-        if (n1 <= tile0) {                         // next tile: full, or the block's own (rows >= L read as zero)
-            stk.load(rk, (int)(n1 * skl * (int64_t)sizeof(T)), tid);
-            stv.load(rv, (int)(n1 * svl * (int64_t)sizeof(T)), tid);
-            stb.load(rb, (int)(n1 * sbl * (int64_t)sizeof(T)), tid);
+    };
+    auto issue_tile = [&](DqLds<T>& d, int n0) {   // rows >= L read as zero
+        dma_issue<1>(dk, K, xk, (int)(n0 * skl * (int64_t)sizeof(T)), d.ks, w);
+        dma_issue<1>(dv, V, xv, (int)(n0 * svl * (int64_t)sizeof(T)), d.vs, w);
+        dma_issue<1>(dbt, Bm, xb, (int)(n0 * sbl * (int64_t)sizeof(T)), d.bs, w);
+        if (tid < 64) {
+            d.fk[tid] = pf_f;
+            d.gk[tid] = pf_g;
+            d.cfm[tid] = pf_cf * exp2_le0((ga - pf_ge) * LOG2E);
         }
-        if (!live) continue;
-        if (n0 < tile0)
-            dq_tile<T, false>(sm, sm.cfm, lane, n0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, scale, R, dqa,
+    };
+    // tile t (keys 64 t ..) is in buffer t & (NBUF-1) after advance(t) (and, for two buffers, the barrier before it)
+    auto advance = [&](int t) {
+        const int n0 = 64 * t;
+        if (NBUF == 2) {
+            if (n0 + 64 <= tile0) {
+                issue_tile(smb[(t + 1) & (NBUF - 1)], n0 + 64);
+                if (n0 + 128 <= tile0) fetch_scalars(n0 + 128);
+            }
+        } else if (t > 0) {
+            __syncthreads();
+            issue_tile(smb[0], n0);
+            __syncthreads();
+            if (n0 + 64 <= tile0) fetch_scalars(n0 + 64);
+        }
+    };
+    fetch_scalars(0);
+    issue_tile(smb[0], 0);
+    if (64 <= tile0) fetch_scalars(64);
+    __syncthreads();
+    // key tiles before the block (all off-block), then the block's own tile
+    const int nt = tile0 / 64;
+    for (int t = 0; t < nt; ++t) {
+        advance(t);
+        if (live) {
+            const DqLds<T>& sm = smb[t & (NBUF - 1)];
+            dq_tile<T, false>(sm, sm.cfm, lane, 64 * t, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, scale, R, dqa,
                               dca);
+        }
+        if (NBUF == 2) __syncthreads();
     }
+    advance(nt);
     if (live) {
-        // the block's own tile (still in LDS): apply the off-block row factors once, in fp32, then the diagonal path
+        // the block's own tile: apply the off-block row factors once, in fp32, then the diagonal path
+        const DqLds<T>& sm = smb[nt & (NBUF - 1)];
         R.xa *= rowfq;
         R.ya *= rowfq;
         dca[0] *= rs;
@@ -611,10 +639,10 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
 // Scores are computed as S = Q K^T (a lane owns one key's column sums); query tiles are visited in descending order
 // so that the keys' own 64-block is every wave's last tile.
 template <class T>
-struct DkvLds {
-    T qs[64 * (DH + LDS_PAD)];   // Q (scores; transposed reads for dk)
-    T cs[64 * (DS + LDS_PAD)];   // C~ (scores; transposed reads for db)
-    T ds[64 * (DH + LDS_PAD)];   // dO (dP; transposed reads for dv)
+struct __attribute__((aligned(16))) DkvLds {
+    T qs[64 * DH];               // Q (scores; transposed reads for dk)
+    T cs[64 * DS];               // C~ (scores; transposed reads for db)
+    T ds[64 * DH];               // dO (dP; transposed reads for dv)
     float lse[64], dhat[64], ddel[64], fq[64], gq[64];
     float rq[64];                // rowf * mid for the query block against the workgroup's key block
 };
@@ -696,7 +724,8 @@ SISA_DEV void dkv_tile(const DkvLds<T>& sm, const float* rqm, int lane, int m0, 
 
 template <class T>
 __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a, float scale) {
-    __shared__ DkvLds<T> sm;
+    constexpr int NBUF = sizeof(T) == 2 ? 2 : 1;
+    __shared__ DkvLds<T> smb[NBUF];
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     int bh, ktile;
@@ -753,53 +782,78 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
     // column sums (diagonal excluded); off-block tiles accumulate dgu without the column factor colf
     float dgu = 0.f, dfs = 0.f;
 
-    BufStage<T, DH, NTHB> stq, std_;
-    BufStage<T, DS, NTHB> stc;
-    const __amdgpu_buffer_rsrc_t rq = make_rsrc(Q, ((int64_t)(L - 1) * sql + DH) * (int64_t)sizeof(T));
-    const __amdgpu_buffer_rsrc_t rd = make_rsrc(DO, ((int64_t)(L - 1) * sdl + DH) * (int64_t)sizeof(T));
-    const __amdgpu_buffer_rsrc_t rc = make_rsrc(C, ((int64_t)(L - 1) * scl + DS) * (int64_t)sizeof(T));
-    stq.init(sql, tid);
-    std_.init(sdl, tid);
-    stc.init(scl, tid);
+    // Query tiles straight into LDS (DMA buffer loads), from the last one down to the block's own tile; 16-bit types
+    // double-buffer them (one barrier per tile), fp32 uses one buffer. The per-query scalars are fetched into
+    // registers by the first wave one tile ahead.
+    DmaStage<T, DH, NWB> dmq, dmd;
+    DmaStage<T, DS, NWB> dmc;
+    const int64_t xq = ((int64_t)(L - 1) * sql + DH) * (int64_t)sizeof(T);   // view extents (bytes)
+    const int64_t xd = ((int64_t)(L - 1) * sdl + DH) * (int64_t)sizeof(T);
+    const int64_t xc = ((int64_t)(L - 1) * scl + DS) * (int64_t)sizeof(T);
+    dmq.init(sql, w, lane);
+    dmd.init(sdl, w, lane);
+    dmc.init(scl, w, lane);
     const int mlast = (L - 1) / 64 * 64;
-    {
-        stq.load(rq, (int)(mlast * sql * (int64_t)sizeof(T)), tid);
-        std_.load(rd, (int)(mlast * sdl * (int64_t)sizeof(T)), tid);
-        stc.load(rc, (int)(mlast * scl * (int64_t)sizeof(T)), tid);
-    }
-    // query tiles after the block (all off-block, descending), then the block's own tile
-    for (int m0 = mlast; m0 >= ktile0; m0 -= 64) {
-        __syncthreads();
-        stq.store(sm.qs, tid);
-        std_.store(sm.ds, tid);
-        stc.store(sm.cs, tid);
+    const int nt = (mlast - ktile0) / 64;         // query tiles after the block; tile t starts at mlast - 64 t
+    float pf_lse = 0.f, pf_dh = 0.f, pf_dd = 0.f, pf_f = 0.f, pf_g = 0.f, pf_rowf = 0.f, pf_gm = 0.f;
+    auto fetch_scalars = [&](int m0) {
         if (tid < 64) {
             const int i = m0 + tid;
             const bool ok = i < L;
             const int ic = ok ? i : L - 1;
-            sm.lse[tid] = ok ? LSE[i] : __builtin_inff();
-            sm.dhat[tid] = ok ? DELTA[i] : 0.f;
-            sm.ddel[tid] = ok ? DDEL[i] : 0.f;
-            sm.fq[tid] = (has_f && ok) ? FF[(int64_t)i * sfl] : 0.f;
-            sm.gq[tid] = G[(int64_t)ic * sgl];
-            const float rowf = ok ? ROWF[i] : 0.f;
-            const float gm = G[(int64_t)m0 * sgl];   // start of the query block
-            sm.rq[tid] = rowf * exp2_le0((gm - ge) * LOG2E);
+            pf_lse = ok ? LSE[i] : __builtin_inff();
+            pf_dh = ok ? DELTA[i] : 0.f;
+            pf_dd = ok ? DDEL[i] : 0.f;
+            pf_f = (has_f && ok) ? FF[(int64_t)i * sfl] : 0.f;
+            pf_g = G[(int64_t)ic * sgl];
+            pf_rowf = ok ? ROWF[i] : 0.f;
+            pf_gm = G[(int64_t)m0 * sgl];           // start of the query block
         }
-        __syncthreads();
-        const int m1 = m0 - 64;
-        if (m1 >= ktile0) {                        // every tile below mlast is full
-            stq.load(rq, (int)(m1 * sql * (int64_t)sizeof(T)), tid);
-            std_.load(rd, (int)(m1 * sdl * (int64_t)sizeof(T)), tid);
-            stc.load(rc, (int)(m1 * scl * (int64_t)sizeof(T)), tid);
+    };
+    auto issue_tile = [&](DkvLds<T>& d, int m0) {   // rows >= L read as zero
+        dma_issue<2>(dmq, Q, xq, (int)(m0 * sql * (int64_t)sizeof(T)), d.qs, w);
+        dma_issue<2>(dmd, DO, xd, (int)(m0 * sdl * (int64_t)sizeof(T)), d.ds, w);
+        dma_issue<2>(dmc, C, xc, (int)(m0 * scl * (int64_t)sizeof(T)), d.cs, w);
+        if (tid < 64) {
+            d.lse[tid] = pf_lse;
+            d.dhat[tid] = pf_dh;
+            d.ddel[tid] = pf_dd;
+            d.fq[tid] = pf_f;
+            d.gq[tid] = pf_g;
+            d.rq[tid] = pf_rowf * exp2_le0((pf_gm - ge) * LOG2E);
         }
-        if (!live) continue;
-        if (m0 > ktile0)
-            dkv_tile<T, false>(sm, sm.rq, lane, m0, k0, L, kf, vf, bfr, fk, rk, gk, dsd, lam, scale, dgu, dfs, dva,
-                               dka, dba);
+    };
+    auto advance = [&](int t) {
+        const int m0 = mlast - 64 * t;
+        if (NBUF == 2) {
+            if (t < nt) {
+                issue_tile(smb[(t + 1) & (NBUF - 1)], m0 - 64);
+                if (t + 1 < nt) fetch_scalars(m0 - 128);
+            }
+        } else if (t > 0) {
+            __syncthreads();
+            issue_tile(smb[0], m0);
+            __syncthreads();
+            if (t < nt) fetch_scalars(m0 - 64);
+        }
+    };
+    fetch_scalars(mlast);
+    issue_tile(smb[0], mlast);
+    if (nt > 0) fetch_scalars(mlast - 64);
+    __syncthreads();
+    for (int t = 0; t < nt; ++t) {
+        advance(t);
+        if (live) {
+            const DkvLds<T>& sm = smb[t & (NBUF - 1)];
+            dkv_tile<T, false>(sm, sm.rq, lane, mlast - 64 * t, k0, L, kf, vf, bfr, fk, rk, gk, dsd, lam, scale, dgu,
+                               dfs, dva, dka, dba);
+        }
+        if (NBUF == 2) __syncthreads();
     }
+    advance(nt);
     if (live) {
-        // the block's own tile (still in LDS): apply the off-block column factors once, in fp32, then the pair path
+        // the block's own tile: apply the off-block column factors once, in fp32, then the pair path
+        const DkvLds<T>& sm = smb[nt & (NBUF - 1)];
         dgu *= colf;
         dba[0] *= rk;
         dba[1] *= rk;

@@ -27,7 +27,6 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 static constexpr float LOG2E = 1.4426950408889634f;
-static constexpr int LDS_PAD = 16;  // elements of padding per LDS tile row
 
 template <class T> struct Vec;
 template <> struct Vec<__bf16> { typedef bf16x8 x8; typedef bf16x4 x4; typedef bf16x2 x2; };
@@ -123,99 +122,91 @@ SISA_DEV f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
 template <class T> SISA_DEV vec4<T> to_vec4(f32x4 x) { return __builtin_convertvector(x, vec4<T>); }
 
-// Cooperative staging of a (64 x C) tile of a sequence-major tensor (rows = positions, C in {32, 64} contiguous
-// features) into a row-major LDS tile X[r][f] (row stride C + LDS_PAD), in two phases so that the global loads of the
-// next tile are in flight while the current one is being used: load() issues 16-byte (8-element) vector loads into
-// registers, store() writes them to LDS. Rows >= nvalid are zero. Consecutive threads read consecutive 16-byte
-// pieces of a row (coalesced).
-template <class T, int C, int NTH>
-struct TileStage {
-    static constexpr int NVEC = 64 * C / 8;
-    static constexpr int PER = (NVEC + NTH - 1) / NTH;
-    frag8<T> v[PER];
+// ------------------------------------------------------------------------------------------------ LDS tiles
+// A tile is 64 rows (sequence positions) x C features stored densely row-major in LDS, in 16-byte chunks. For 16-bit
+// types the chunks of a row are XOR-swizzled so that both fragment reads below are free of bank conflicts:
+//   C = 64 (8 chunks per row): physical chunk = chunk ^ (row % 8);
+//   C = 32 (4 chunks per row): physical chunk = chunk ^ 2 * ((row / 4) % 2).
+// (8 consecutive rows of one chunk column, and the 4-row x 32-byte footprint of a transpose read, then fall on
+// distinct banks.) fp32 tiles (the accuracy path) are not swizzled.
+template <class T, int C>
+SISA_DEV int swz(int row) {
+    if constexpr (sizeof(T) != 2) return 0;
+    else if constexpr (C == 64) return row & 7;
+    else return ((row >> 2) & 1) << 1;
+}
+// element offset of (row, 16-byte chunk) in a tile
+template <class T, int C>
+SISA_DEV int toff(int row, int chunk) {
+    return row * C + (16 / (int)sizeof(T)) * (chunk ^ swz<T, C>(row));
+}
 
-    SISA_DEV void load(const T* __restrict__ src, int64_t srow, int nvalid, int tid) {
-#pragma unroll
-        for (int p = 0; p < PER; ++p) {
-            const int idx = tid + p * NTH;
-            const int row = idx / (C / 8), c8 = idx % (C / 8);
-            if (idx < NVEC && row < nvalid) v[p] = load8<T>(src + (int64_t)row * srow + c8 * 8);
-            else v[p] = zero8<T>();
-        }
-    }
-    SISA_DEV void store(T* __restrict__ X, int tid) const {
-#pragma unroll
-        for (int p = 0; p < PER; ++p) {
-            const int idx = tid + p * NTH;
-            const int row = idx / (C / 8), c8 = idx % (C / 8);
-            if (idx < NVEC) *reinterpret_cast<frag8<T>*>(X + row * (C + LDS_PAD) + c8 * 8) = v[p];
-        }
-    }
-};
-
-// Buffer-resource staging of the same (64 x C) tiles: one resource per (batch, head) view covering rows 0..L-1, a
-// per-lane byte offset that does not change from tile to tile, and the tile's row offset as a wave-uniform scalar.
-// Rows at or beyond L fall outside the resource and read as zero (no per-row bounds test, no 64-bit address
-// arithmetic per tile). The view's extent must be below 2^31 bytes (checked by the host).
+// Buffer resource over one (batch, head) view: rows 0..L-1 of `bytes` total extent; rows at or beyond L read as zero.
+// The extent must be below 2^31 bytes (checked by the host).
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 SISA_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
-template <class T>
-SISA_DEV frag8<T> buf_load8(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    if constexpr (sizeof(T) == 2) {
-        return __builtin_bit_cast(frag8<T>, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-    } else {
-        const f32x4 lo = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-        const f32x4 hi = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, 0));
-        return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    }
-}
 
-template <class T, int C, int NTH>
-struct BufStage {
-    static constexpr int NVEC = 64 * C / 8;
-    static constexpr int PER = (NVEC + NTH - 1) / NTH;
-    frag8<T> v[PER];
+// Staging of a tile straight from global memory into LDS (buffer loads with the LDS destination, no registers):
+// wave instruction k of a tile fills tile bytes [1024 k, 1024 k + 1024), lane i the 16-byte chunk 64 k + i, so a
+// tile of CPR chunks per row takes CPR instructions, spread over the NW waves of the workgroup. The per-lane global
+// offsets do not change from tile to tile; the tile's first row enters as a scalar offset. The loads complete
+// asynchronously: a workgroup barrier after them (the compiler waits for the loads before it) publishes the tile.
+template <class T, int C, int NW>
+struct DmaStage {
+    static constexpr int CPR = C * (int)sizeof(T) / 16;   // chunks per row = wave instructions per tile
+    static constexpr int PER = (CPR + NW - 1) / NW;
     int voff[PER];
 
-    SISA_DEV void init(int64_t srow, int tid) {
+    SISA_DEV void init(int64_t srow, int w, int lane) {
 #pragma unroll
         for (int p = 0; p < PER; ++p) {
-            const int idx = tid + p * NTH;
-            voff[p] = (int)(((idx / (C / 8)) * srow + (idx % (C / 8)) * 8) * (int64_t)sizeof(T));
-        }
-    }
-    // rows [row0, row0 + 64) of the view; soff = row0 * srow * sizeof(T)
-    SISA_DEV void load(__amdgpu_buffer_rsrc_t r, int soff, int tid) {
-#pragma unroll
-        for (int p = 0; p < PER; ++p)
-            v[p] = (tid + p * NTH < NVEC) ? buf_load8<T>(r, voff[p], soff) : zero8<T>();
-    }
-    SISA_DEV void store(T* __restrict__ X, int tid) const {
-#pragma unroll
-        for (int p = 0; p < PER; ++p) {
-            const int idx = tid + p * NTH;
-            const int row = idx / (C / 8), c8 = idx % (C / 8);
-            if (idx < NVEC) *reinterpret_cast<frag8<T>*>(X + row * (C + LDS_PAD) + c8 * 8) = v[p];
+            const int ci = 64 * (w + NW * p) + lane;
+            const int row = ci / CPR, phys = ci % CPR;
+            voff[p] = (int)(row * srow * (int64_t)sizeof(T) + 16 * (phys ^ swz<T, C>(row)));
         }
     }
 };
 
-// Operand fragment of a row-major LDS tile X: row (position) r0 + lane%16, features 32*step + 8*grp + 0..7
-// (feature-contracted products: A/B operand whose row is a position).
-template <class T, int C>
-SISA_DEV frag8<T> frag_rows(const T* X, int r0, int step, int lane) {
-    return load8<T>(X + (r0 + (lane & 15)) * (C + LDS_PAD) + 32 * step + 8 * (lane >> 4));
+// Issue the staging of rows [row0, row0 + 64) of a view (base pointer, extent in bytes) into tile X
+// (soff = row0 * srow * sizeof(T)). The buffer resource is formed here: the resource type is device-only, and kernel
+// code that the host compilation pass also analyses must not pass it around. KERNEL gives each kernel its own
+// specialization: the host pass of this compiler rejects a second kernel's use of a specialization already used by
+// another kernel (and silently drops that kernel's launch stub when the call is a member function).
+template <int KERNEL, class T, int C, int NW>
+SISA_DEV void dma_issue(const DmaStage<T, C, NW>& st, const void* base, int64_t bytes, int soff, T* X, int w) {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(base, bytes);
+#pragma unroll
+    for (int p = 0; p < DmaStage<T, C, NW>::PER; ++p) {
+        const int k = w + NW * p;
+        if (k < DmaStage<T, C, NW>::CPR)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                r, (__attribute__((address_space(3))) void*)(X + k * (1024 / (int)sizeof(T))), 16, st.voff[p], soff, 0,
+                0);
+    }
 }
 
-// Operand fragment of the transpose of a row-major LDS tile X (rows = positions): row (feature) f0 + lane%16,
-// K = the positions of the sequence map for `step` (positions 32*step .. 32*step+31 of the tile).
+// Operand fragment of a tile X: row (position) r0 + lane%16, features 32*step + 8*grp + 0..7 (feature-contracted
+// products: A/B operand whose row is a position).
+template <class T, int C>
+SISA_DEV frag8<T> frag_rows(const T* X, int r0, int step, int lane) {
+    const int row = r0 + (lane & 15);
+    if constexpr (sizeof(T) == 2) {
+        return load8<T>(X + toff<T, C>(row, 4 * step + (lane >> 4)));
+    } else {
+        const int c0 = (32 * step + 8 * (lane >> 4)) / 4;
+        return join<T>(load4<T>(X + toff<T, C>(row, c0)), load4<T>(X + toff<T, C>(row, c0 + 1)));
+    }
+}
+
+// Operand fragment of the transpose of a tile X (rows = positions): row (feature) f0 + lane%16, K = the positions of
+// the sequence map for `step` (positions 32*step .. 32*step+31 of the tile).
 // 16-bit types use the gfx950 LDS transpose read ds_read_b64_tr_b16: within each block of 16 lanes, destination
 // lane d receives, as element j, element d%4 of the 8 bytes addressed by source lane 4j + d/4. Source lane
 // s = 4j + q of lane group grp therefore addresses position 16*blk + 4*grp + j, features f0 + 4q .. f0 + 4q + 3, and
 // destination lane d gets feature f0 + d at positions 16*blk + 4*grp + 0..3 -- slots j (blk = 2*step) and j + 4
-// (blk = 2*step + 1) of the sequence map.
+// (blk = 2*step + 1) of the sequence map. The swizzle of a row equals that of the row 16 below it.
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 template <class T>
 SISA_DEV vec4<T> lds_tr4(const T* p) {
@@ -226,17 +217,19 @@ SISA_DEV vec4<T> lds_tr4(const T* p) {
 template <class T, int C>
 SISA_DEV frag8<T> frag_tr(const T* X, int f0, int step, int lane) {
     const int s = lane & 15, grp = lane >> 4;
-    const T* p0 = X + ((2 * step) * 16 + 4 * grp + (s >> 2)) * (C + LDS_PAD) + f0 + 4 * (s & 3);
-    return join<T>(lds_tr4<T>(p0), lds_tr4<T>(p0 + 16 * (C + LDS_PAD)));
+    const int row = 32 * step + 4 * grp + (s >> 2);
+    const int f = f0 + 4 * (s & 3);
+    const T* p0 = X + toff<T, C>(row, f >> 3) + (f & 4);
+    return join<T>(lds_tr4<T>(p0), lds_tr4<T>(p0 + 16 * C));
 }
 
-// fp32 tiles: plain element gathers (the fp32 path exists for correctness, not speed).
+// fp32 tiles: plain element gathers (the fp32 path exists for accuracy, not speed).
 template <>
 SISA_DEV frag8<float> frag_tr<float, 64>(const float* X, int f0, int step, int lane) {
     const int m = lane & 15, grp = lane >> 4;
     frag8<float> r;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] = X[((2 * step + j / 4) * 16 + 4 * grp + j % 4) * (64 + LDS_PAD) + f0 + m];
+    for (int j = 0; j < 8; ++j) r[j] = X[((2 * step + j / 4) * 16 + 4 * grp + j % 4) * 64 + f0 + m];
     return r;
 }
 template <>
@@ -244,7 +237,7 @@ SISA_DEV frag8<float> frag_tr<float, 32>(const float* X, int f0, int step, int l
     const int m = lane & 15, grp = lane >> 4;
     frag8<float> r;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] = X[((2 * step + j / 4) * 16 + 4 * grp + j % 4) * (32 + LDS_PAD) + f0 + m];
+    for (int j = 0; j < 8; ++j) r[j] = X[((2 * step + j / 4) * 16 + 4 * grp + j % 4) * 32 + f0 + m];
     return r;
 }
 
