@@ -77,11 +77,21 @@ SISA_DEV void store_row4(TO* p, f32x4 v) {
     store4<TO>(p, to_vec4<TO>(v));
 }
 
-// Workgroup i of a 1-D grid of nrank * BH workgroups -> (bh, rank). Workgroups are dispatched round-robin over the 8
-// XCDs (workgroup i runs on XCD i % 8), each with its own L2: the mapping gives every XCD a contiguous range of
-// (bh, rank) so that the workgroups sharing one head's K/V (or Q/dO) tiles run on one XCD and read them from HBM
-// once. Within an XCD's range the ranks of a head are dispatched in order.
+// Workgroup i of a 1-D grid of nrank * BH workgroups -> (bh, rank); rank 0 is the heaviest workgroup of a head.
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup i runs on XCD i % 8), each with its own L2, so
+// every XCD gets whole heads: the workgroups sharing one head's K/V (or Q/dO) tiles run on one XCD and read them
+// from HBM once. When BH is a multiple of 8, XCD x owns heads [x BH/8, (x+1) BH/8) and dispatches them rank-major
+// (rank 0 of each of its heads, then rank 1, ...): the XCD's queue is heaviest-first, which a greedy in-order
+// dispatcher packs with a short tail (head after head, the last head's heavy workgroups would start late).
+// Otherwise each XCD gets a contiguous range of (bh, rank), or the plain order when the grid does not split in 8.
 SISA_DEV void xcd_map(int i, int nrank, int BH, int& bh, int& rank) {
+    if (BH % 8 == 0) {
+        const int hp = BH / 8;
+        const int s = i / 8;
+        bh = (i % 8) * hp + s % hp;
+        rank = s / hp;
+        return;
+    }
     const int total = nrank * BH;
     const int j = (total % 8 == 0) ? (i % 8) * (total / 8) + i / 8 : i;
     bh = j / nrank;
