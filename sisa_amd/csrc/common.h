@@ -209,7 +209,7 @@ SISA_DEV frag8<T> frag_rows(const T* X, int r0, int step, int lane) {
 // (blk = 2*step + 1) of the sequence map. The swizzle of a row equals that of the row 16 below it.
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 template <class T>
-SISA_DEV vec4<T> lds_tr4(const T* p) {
+SISA_DEV vec4<T> lds_tr4(const T* __restrict__ p) {
     const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
     return __builtin_bit_cast(vec4<T>, r);
 }
