@@ -103,35 +103,78 @@ SISA_DEV void xcd_map(int i, int nrank, int BH, int& bh, int& rank) {
 // are directly the B fragments of O^T += V^T P^T. Per tile and wave one of two code paths runs (uniform branch):
 // off-block tiles (every key in an earlier 64-block than the wave's queries; chunk-factored decay, no masks) or the
 // wave's own block (pairwise decay and the causal mask).
+//
+// Score arithmetic (16-bit inputs). Off-block tiles use the key block's last F as an anchor: with F_e = F at the
+// tile's last key, s_ij = s''_ij + (F_i - F_e), where s''_ij = q.k/8 + (F_e - F_j) + decay term and F_i - F_e is one
+// scalar per (query, tile) that goes into the exponent offset and the tile maximum. Both parts are differences of
+// F values no farther apart than F_i - F_j, so errors keep scaling with F differences, never with |F| (shift
+// invariance); the diagonal tile, where F_i - F_e can exceed F_i - F_j, uses the reference's per-element F_i - F_j.
+// Then
+//   * q is pre-scaled by 1/8 = 1/sqrt(d_head) (a power of two: exact), and the per-key F_e - F_j enters the q.k MFMA
+//     as its accumulator input, so that product block is already q.k/8 + F_e - F_j;
+//   * off-block tiles: for bf16 the query factor lam*rowf_i is folded into the c~ operand as an unevaluated bf16 pair
+//     hi + lo = lam*rowf_i*c~_i (relative error <= 2^-17, two MFMAs), for fp32 as one fp32 operand; the decayed
+//     side term is then one FMA with the per-key colf_j*mid. fp16 (too little exponent range for the split) keeps
+//     the fp32 products lam*rowf_i * (cb_ij * colf_j*mid).
+// Per off-block score element that leaves one FMA (two for fp16) before the softmax. fp32 (the accuracy path) keeps
+// the reference's per-element F_i - F_j everywhere.
+constexpr float QSCALE = 0.125f;   // 1/sqrt(DH), exact in every input type
+template <class T> struct FoldC { static constexpr bool on = sizeof(T) != 2 || __is_same(T, __bf16); };
+template <class T> struct SplitC { static constexpr bool on = __is_same(T, __bf16); };
+template <class T> struct Anchor { static constexpr bool on = sizeof(T) == 2; };
+
 template <class T>
 struct __attribute__((aligned(16))) FwdLds {
     T ks[64 * DH];               // K tile
     T bs[64 * DS];               // B~ tile
     T vs[64 * DH];               // V tile
     float fk[64], gk[64];        // F and g at the tile's keys
+    float nfe[64];               // F_e - F_j (F_e = F at the tile's last key)
     float cfm[2][64];            // colf * mid for the workgroup's two query blocks
 };
 
+// The 8 values of a fragment multiplied by s (fp32) and rounded back to T.
+template <class T> SISA_DEV frag8<T> scale_frag(const frag8<T>& f, float s) {
+    return __builtin_convertvector(__builtin_convertvector(f, f32x8) * s, frag8<T>);
+}
+// hi + lo = s * f with hi, lo in T (lo = 0 where the split is off).
+template <class T> SISA_DEV void split_frag(const frag8<T>& f, float s, frag8<T>& hi, frag8<T>& lo) {
+    const f32x8 x = __builtin_convertvector(f, f32x8) * s;
+    hi = __builtin_convertvector(x, frag8<T>);
+    if constexpr (SplitC<T>::on) lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x8), frag8<T>);
+    else lo = zero8<T>();
+}
+
+// One 64-key tile for a wave's 16 queries. cx0/cx1: for off-block tiles the folded c~ operand (hi, lo; FoldC types)
+// or the plain c~ (fp16, cx1 unused); for the diagonal tile the plain c~ (cx1 unused).
 template <class T, bool DIAG>
-SISA_DEV void fwd_tile(const FwdLds<T>& sm, const float* cfm, int lane, int n0, int q0, int L, const frag8<T> (&qf)[2],
-                       const frag8<T>& cfr, const frag8<T>& onesf, float fq, float rs, float gq, float lam, float scale,
-                       float& m, float& l, f32x4 (&acc)[5]) {
+SISA_DEV void fwd_tile(const FwdLds<T>& sm, int qblk, int lane, int n0, int q0, int L, const frag8<T> (&qf)[2],
+                       const frag8<T>& cx0, const frag8<T>& cx1, const frag8<T>& onesf, float fq, float rs, float gq,
+                       float lam, float& m, float& l, f32x4 (&acc)[5]) {
+    constexpr bool ANCH = Anchor<T>::on && !DIAG;
     const int grp = lane >> 4, lc = lane & 15;
     const int qq = q0 + lc;
+    const float* cfm = sm.cfm[qblk];
     f32x4 sc[4], cb[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
         const frag8<T> k0 = frag_rows<T, DH>(sm.ks, kb * 16, 0, lane);
         const frag8<T> k1 = frag_rows<T, DH>(sm.ks, kb * 16, 1, lane);
         const frag8<T> bf = frag_rows<T, DS>(sm.bs, kb * 16, 0, lane);
-        sc[kb] = mma(k1, qf[1], mma(k0, qf[0], zero4()));
-        cb[kb] = mma(bf, cfr, zero4());
+        if constexpr (ANCH) sc[kb] = mma(k1, qf[1], mma(k0, qf[0], lds4f(&sm.nfe[kb * 16 + 4 * grp])));
+        else sc[kb] = mma(k1, qf[1], mma(k0, qf[0], zero4()));
+        if constexpr (!DIAG && SplitC<T>::on) cb[kb] = mma(bf, cx1, mma(bf, cx0, zero4()));
+        else cb[kb] = mma(bf, cx0, zero4());
     }
     float mloc = -__builtin_inff();
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
         const int j0 = kb * 16 + 4 * grp;
-        const f32x4 fk = lds4f(&sm.fk[j0]);
+        if constexpr (!ANCH) {   // the reference's difference F_i - F_j per element
+            const f32x4 fk = lds4f(&sm.fk[j0]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[kb][i] = sc[kb][i] + (fq - fk[i]);
+        }
         if (DIAG) {
             const f32x4 gk = lds4f(&sm.gk[j0]);
 #pragma unroll
@@ -139,8 +182,7 @@ SISA_DEV void fwd_tile(const FwdLds<T>& sm, const float* cfm, int lane, int n0, 
                 const int jj = n0 + j0 + i;
                 const bool valid = jj <= qq && jj < L;
                 const float dec = valid ? exp2_le0((gq - gk[i]) * LOG2E) : 0.f;
-                float s = sc[kb][i] * scale + (fq - fk[i]);
-                s = s + lam * (dec * cb[kb][i]);
+                float s = sc[kb][i] + lam * (dec * cb[kb][i]);
                 s = valid ? s : -__builtin_inff();
                 sc[kb][i] = s;
                 mloc = fmaxf(mloc, s);
@@ -149,19 +191,22 @@ SISA_DEV void fwd_tile(const FwdLds<T>& sm, const float* cfm, int lane, int n0, 
             const f32x4 cf = lds4f(&cfm[j0]);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                float s = sc[kb][i] * scale + (fq - fk[i]);
-                s = s + rs * (cb[kb][i] * cf[i]);
+                float s;
+                if constexpr (FoldC<T>::on) s = fmaf(cb[kb][i], cf[i], sc[kb][i]);
+                else s = sc[kb][i] + rs * (cb[kb][i] * cf[i]);
                 sc[kb][i] = s;
                 mloc = fmaxf(mloc, s);
             }
         }
     }
+    // anchored tiles: sc holds s'' = s - (F_i - F_e); ft = (F_i - F_e) * log2e restores s in the exponent and max
+    const float ft = ANCH ? (fq - sm.fk[63]) * LOG2E : 0.f;
     // Online softmax in log2 units with lazy rescaling: a query's running offset m moves (and its l, acc are
     // rescaled) only when its tile maximum exceeds m by more than RESCALE_LOG2, so the exponentials stay below
     // 2^RESCALE_LOG2. The decision is per query (a query's results never depend on its neighbours); the wave skips
     // the rescale when no query needs it, and queries that do not need it multiply by exactly 1. m starts at a
     // finite floor, so fully masked rows give exp2(-inf) = 0. A NaN score reaches l through its exponential.
-    const float mt = group_max(mloc) * LOG2E;
+    const float mt = ANCH ? fmaf(group_max(mloc), LOG2E, ft) : group_max(mloc) * LOG2E;
     const bool need = mt > m + RESCALE_LOG2;
     if (__builtin_amdgcn_ballot_w64(need) != 0) {
         const float mn = need ? fmaxf(m, mt) : m;
@@ -172,11 +217,12 @@ SISA_DEV void fwd_tile(const FwdLds<T>& sm, const float* cfm, int lane, int n0, 
         for (int db = 0; db < 5; ++db) acc[db] *= corr;
     }
     float ls = 0.f;
+    const float off = ANCH ? ft - m : -m;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float pe = fast_exp2(fmaf(sc[kb][i], LOG2E, -m));
+            const float pe = fast_exp2(fmaf(sc[kb][i], LOG2E, off));
             sc[kb][i] = pe;
             ls += pe;
         }
@@ -191,7 +237,7 @@ SISA_DEV void fwd_tile(const FwdLds<T>& sm, const float* cfm, int lane, int n0, 
 }
 
 template <class T>
-__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void attn_fwd_kernel(sisa_attn_fwd_args a, float scale) {
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void attn_fwd_kernel(sisa_attn_fwd_args a) {
     constexpr int NBUF = sizeof(T) == 2 ? 2 : 1;
     __shared__ FwdLds<T> smb[NBUF];
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
@@ -220,21 +266,30 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
     const int q0 = tile0 + 16 * w;
     const int qblk = w >> 2;                       // which of the workgroup's two query blocks
     const bool live = q0 < L;
-    const float ga0 = G[(int64_t)(tile0 < L ? tile0 : L - 1) * sgl];
-    const float ga1 = G[(int64_t)(tile0 + 64 < L ? tile0 + 64 : L - 1) * sgl];
+    const int ta0 = tile0 < L ? tile0 : L - 1, ta1 = tile0 + 64 < L ? tile0 + 64 : L - 1;   // block anchors
+    const float ga0 = G[(int64_t)ta0 * sgl];
+    const float ga1 = G[(int64_t)ta1 * sgl];
 
-    frag8<T> qf[2], cfr;
+    // qf: q/8 (exact). cx0/cx1: the c~ operand of off-block tiles (folded with lam*rowf_i where FoldC).
+    frag8<T> qf[2], cx0, cx1;
     float fq, rs, gq;
     {
         const int qq = q0 + lc;
         const bool ok = qq < L;
-        qf[0] = ok ? load8<T>(Q + (int64_t)qq * sql + 8 * grp) : zero8<T>();
-        qf[1] = ok ? load8<T>(Q + (int64_t)qq * sql + 32 + 8 * grp) : zero8<T>();
-        cfr = ok ? load8<T>(C + (int64_t)qq * scl + 8 * grp) : zero8<T>();
+        qf[0] = ok ? scale_frag<T>(load8<T>(Q + (int64_t)qq * sql + 8 * grp), QSCALE) : zero8<T>();
+        qf[1] = ok ? scale_frag<T>(load8<T>(Q + (int64_t)qq * sql + 32 + 8 * grp), QSCALE) : zero8<T>();
+        const frag8<T> cfr = ok ? load8<T>(C + (int64_t)qq * scl + 8 * grp) : zero8<T>();
         fq = (has_f && ok) ? FF[(int64_t)qq * sfl] : 0.f;
         rs = lam * (ok ? ROWF[qq] : 0.f);
         gq = G[(int64_t)(ok ? qq : L - 1) * sgl];
+        if constexpr (FoldC<T>::on) split_frag<T>(cfr, rs, cx0, cx1);
+        else { cx0 = cfr; cx1 = zero8<T>(); }
     }
+    // the plain c~ operand of the diagonal tile (loaded there: the loop does not keep it in registers)
+    auto diag_c = [&]() -> frag8<T> {
+        const int qq = q0 + lc;
+        return qq < L ? load8<T>(C + (int64_t)qq * scl + 8 * grp) : zero8<T>();
+    };
     const frag8<T> onesf = ones_row_frag<T>(lane);
 
     float m = M_FLOOR, l = 0.f;
@@ -255,15 +310,17 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
     dv.init(svl, w, lane);
     dbt.init(sbl, w, lane);
     const int kend = (tile0 + 128 < L) ? tile0 + 128 : L;
-    float pf_f = 0.f, pf_g = 0.f, pf_cf = 0.f, pf_ge = 0.f;
+    float pf_f = 0.f, pf_g = 0.f, pf_cf = 0.f, pf_ge = 0.f, pf_fe = 0.f;
     auto fetch_scalars = [&](int n0) {
         if (tid < 64) {
             const int j = n0 + tid;
             const int jc = j < L ? j : L - 1;
+            const int je = n0 + 63 < L ? n0 + 63 : L - 1;   // end of the key block
             pf_f = (has_f && j < L) ? FF[(int64_t)j * sfl] : 0.f;
             pf_g = G[(int64_t)jc * sgl];
             pf_cf = j < L ? COLF[j] : 0.f;
-            pf_ge = G[(int64_t)(n0 + 63 < L ? n0 + 63 : L - 1) * sgl];   // end of the key block
+            pf_ge = G[(int64_t)je * sgl];
+            pf_fe = has_f ? FF[(int64_t)je * sfl] : 0.f;
         }
     };
     auto issue_tile = [&](FwdLds<T>& d, int n0) {
@@ -272,6 +329,7 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
         dma_issue<0>(dbt, Bm, xb, (int)(n0 * sbl * (int64_t)sizeof(T)), d.bs, w);
         if (tid < 64) {
             d.fk[tid] = pf_f;
+            d.nfe[tid] = pf_fe - pf_f;
             d.gk[tid] = pf_g;
             d.cfm[0][tid] = pf_cf * exp2_le0((ga0 - pf_ge) * LOG2E);
             d.cfm[1][tid] = pf_cf * exp2_le0((ga1 - pf_ge) * LOG2E);
@@ -303,8 +361,7 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
         advance(t);
         if (live) {
             const FwdLds<T>& sm = smb[t & (NBUF - 1)];
-            fwd_tile<T, false>(sm, sm.cfm[qblk], lane, 64 * t, q0, L, qf, cfr, onesf, fq, rs, gq, lam, scale, m, l,
-                               acc);
+            fwd_tile<T, false>(sm, qblk, lane, 64 * t, q0, L, qf, cx0, cx1, onesf, fq, rs, gq, lam, m, l, acc);
         }
         if (NBUF == 2) __syncthreads();
     }
@@ -313,17 +370,16 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
     if (live) {
         const FwdLds<T>& sm = smb[nfull & (NBUF - 1)];
         if (qblk == 0)
-            fwd_tile<T, true>(sm, sm.cfm[0], lane, tile0, q0, L, qf, cfr, onesf, fq, rs, gq, lam, scale, m, l, acc);
+            fwd_tile<T, true>(sm, 0, lane, tile0, q0, L, qf, diag_c(), cx1, onesf, fq, rs, gq, lam, m, l, acc);
         else
-            fwd_tile<T, false>(sm, sm.cfm[1], lane, tile0, q0, L, qf, cfr, onesf, fq, rs, gq, lam, scale, m, l, acc);
+            fwd_tile<T, false>(sm, 1, lane, tile0, q0, L, qf, cx0, cx1, onesf, fq, rs, gq, lam, m, l, acc);
     }
     if (tile0 + 64 < kend) {
         if (NBUF == 2) __syncthreads();
         advance(nfull + 1);
         if (live && qblk == 1) {
             const FwdLds<T>& sm = smb[(nfull + 1) & (NBUF - 1)];
-            fwd_tile<T, true>(sm, sm.cfm[1], lane, tile0 + 64, q0, L, qf, cfr, onesf, fq, rs, gq, lam, scale, m, l,
-                              acc);
+            fwd_tile<T, true>(sm, 1, lane, tile0 + 64, q0, L, qf, diag_c(), cx1, onesf, fq, rs, gq, lam, m, l, acc);
         }
     }
     if (!live) return;
@@ -341,6 +397,7 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
 #pragma unroll
         for (int db = 0; db < 4; ++db) *reinterpret_cast<f32x4*>(O32 + db * 16 + 4 * grp) = acc[db] / lbs;
     }
+    // lse of the true scores s = s' + (F_i - F_a), in log2 units
     if (grp == 0) a.lse[(int64_t)bh * L + qq] = m + __builtin_amdgcn_logf(ls);
 }
 
@@ -923,7 +980,7 @@ __global__ __launch_bounds__(1024) void dlam_kernel(const float* __restrict__ rl
 template <class T>
 int launch_fwd(const sisa_attn_fwd_args* a, hipStream_t st) {
     const dim3 grid((unsigned)(sisa::cdiv(a->L, 128) * a->B * a->H));
-    attn_fwd_kernel<T><<<grid, NTH, 0, st>>>(*a, 0.125f);
+    attn_fwd_kernel<T><<<grid, NTH, 0, st>>>(*a);
     return sisa::launch_status("sisa_attn_fwd");
 }
 
