@@ -411,6 +411,7 @@ struct __attribute__((aligned(16))) DqLds {
     T vs[64 * DH];               // V (dP)
     T bs[64 * DS];               // B~ (scores; transposed reads for dc)
     float fk[64], gk[64];
+    float nfe[64];               // F_e - F_j (F_e = F at the tile's last key; anchored off-block scores)
     float cfm[64];               // colf * mid for the workgroup's query block
 };
 
@@ -421,12 +422,21 @@ struct RowSums {
     float xa, ya, wa, za, ptt, dptt, xd;
 };
 
+// Score arithmetic as in the forward: q is pre-scaled by 1/8; for 16-bit inputs off-block tiles are anchored at the
+// key tile's last F (F_e - F_j enters the q.k MFMA as its accumulator input, (F_i - F_e) log2e - lse is one offset
+// per query and tile) and dP - Delta comes out of the dO.V MFMA (-Delta as its accumulator input). The dkv kernel
+// evaluates the same pairs with the same anchors and the same accumulator inputs.
 template <class T, bool DIAG>
-SISA_DEV void dq_tile(const DqLds<T>& sm, const float* cfm, int lane, int n0, int q0, int L, const frag8<T> (&qf)[2],
+SISA_DEV void dq_tile(const DqLds<T>& sm, int lane, int n0, int q0, int L, const frag8<T> (&qf)[2],
                       const frag8<T>& cfr, const frag8<T> (&dof)[2], float fq, float rs, float gq, float lse,
-                      float dhat, float lam, float scale, RowSums& R, f32x4 (&dqa)[4], f32x4 (&dca)[2]) {
+                      float dhat, float lam, RowSums& R, f32x4 (&dqa)[4], f32x4 (&dca)[2]) {
+    constexpr bool F16 = Anchor<T>::on;
+    constexpr bool ANCH = F16 && !DIAG;
     const int grp = lane >> 4, lc = lane & 15;
     const int qq = q0 + lc;
+    const float* cfm = sm.cfm;
+    const float ftl = ANCH ? fmaf(fq - sm.fk[63], LOG2E, -lse) : -lse;
+    const f32x4 ndh = F16 ? f32x4{-dhat, -dhat, -dhat, -dhat} : zero4();
 #pragma unroll
     for (int st = 0; st < 2; ++st) {           // 32 keys (one K-step of the dq/dc products) at a time
         f32x4 dsv[2], wv[2];                   // dq and dc operands of the two 16-key blocks (before rounding)
@@ -434,12 +444,13 @@ SISA_DEV void dq_tile(const DqLds<T>& sm, const float* cfm, int lane, int n0, in
         for (int hb = 0; hb < 2; ++hb) {       // one 16-key block at a time keeps the live set small
             __builtin_amdgcn_sched_barrier(0);
             const int kb = 2 * st + hb;
+            const int j0 = kb * 16 + 4 * grp;
             const f32x4 sc = mma(frag_rows<T, DH>(sm.ks, kb * 16, 1, lane), qf[1],
-                                 mma(frag_rows<T, DH>(sm.ks, kb * 16, 0, lane), qf[0], zero4()));
+                                 mma(frag_rows<T, DH>(sm.ks, kb * 16, 0, lane), qf[0],
+                                     ANCH ? lds4f(&sm.nfe[j0]) : zero4()));
             const f32x4 cb = mma(frag_rows<T, DS>(sm.bs, kb * 16, 0, lane), cfr, zero4());
             const f32x4 dp = mma(frag_rows<T, DH>(sm.vs, kb * 16, 1, lane), dof[1],
-                                 mma(frag_rows<T, DH>(sm.vs, kb * 16, 0, lane), dof[0], zero4()));
-            const int j0 = kb * 16 + 4 * grp;
+                                 mma(frag_rows<T, DH>(sm.vs, kb * 16, 0, lane), dof[0], ndh));
             const f32x4 fk = lds4f(&sm.fk[j0]);
             if (DIAG) {
                 const f32x4 gk = lds4f(&sm.gk[j0]);
@@ -451,14 +462,14 @@ SISA_DEV void dq_tile(const DqLds<T>& sm, const float* cfm, int lane, int n0, in
                     const float dec = valid ? exp2_le0((gq - gk[i]) * LOG2E) : 0.f;
                     const float cbv = cb[i];
                     const float u = dec * cbv;
-                    float s = sc[i] * scale + (fq - fk[i]);
+                    float s = sc[i] + (fq - fk[i]);
                     s = s + lam * u;
                     const float pr = valid ? fast_exp2(fmaf(s, LOG2E, -lse)) : 0.f;
-                    const float dpv = dp[i];
-                    const float ds = pr * (dpv - dhat);
+                    const float dpd = F16 ? dp[i] : dp[i] - dhat;   // dP - Delta
+                    const float ds = pr * dpd;
                     const float dso = eye ? 0.f : ds;
                     R.ptt += eye ? pr : 0.f;
-                    R.dptt += eye ? dpv : 0.f;
+                    R.dptt += eye ? dpd : 0.f;
                     R.xd += eye ? cbv : 0.f;
                     const float po = eye ? 0.f : pr;
                     R.za += po;
@@ -473,10 +484,11 @@ SISA_DEV void dq_tile(const DqLds<T>& sm, const float* cfm, int lane, int n0, in
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float uc = cb[i] * cf[i];
-                    float s = sc[i] * scale + (fq - fk[i]);
-                    s = s + rs * uc;
-                    const float pr = fast_exp2(fmaf(s, LOG2E, -lse));
-                    const float ds = pr * (dp[i] - dhat);
+                    float s;
+                    if constexpr (ANCH) s = fmaf(rs, uc, sc[i]);
+                    else s = (sc[i] + (fq - fk[i])) + rs * uc;
+                    const float pr = fast_exp2(fmaf(s, LOG2E, ftl));
+                    const float ds = pr * (F16 ? dp[i] : dp[i] - dhat);
                     R.xa += ds * uc;
                     R.ya += pr * uc;
                     R.za += pr;
@@ -497,7 +509,7 @@ SISA_DEV void dq_tile(const DqLds<T>& sm, const float* cfm, int lane, int n0, in
 }
 
 template <class T>
-__global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void attn_bwd_dq_kernel(sisa_attn_bwd_args a, float scale) {
+__global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void attn_bwd_dq_kernel(sisa_attn_bwd_args a) {
     constexpr int NBUF = sizeof(T) == 2 ? 2 : 1;
     __shared__ DqLds<T> smb[NBUF];
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
@@ -540,7 +552,7 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
         float part = 0.f;
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
-            qf[st] = ok ? load8<T>(Q + (int64_t)qq * a.q.sl + 32 * st + 8 * grp) : zero8<T>();
+            qf[st] = ok ? scale_frag<T>(load8<T>(Q + (int64_t)qq * a.q.sl + 32 * st + 8 * grp), QSCALE) : zero8<T>();
             dof[st] = ok ? load8<T>(DO + (int64_t)qq * a.dout.sl + 32 * st + 8 * grp) : zero8<T>();
             if (ok) {
                 const frag8<T> ov = load8<T>(O + (int64_t)qq * a.o.sl + 32 * st + 8 * grp);
@@ -588,15 +600,17 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
     dk.init(skl, w, lane);
     dv.init(svl, w, lane);
     dbt.init(sbl, w, lane);
-    float pf_f = 0.f, pf_g = 0.f, pf_cf = 0.f, pf_ge = 0.f;
+    float pf_f = 0.f, pf_g = 0.f, pf_cf = 0.f, pf_ge = 0.f, pf_fe = 0.f;
     auto fetch_scalars = [&](int n0) {
         if (tid < 64) {
             const int j = n0 + tid;
             const int jc = j < L ? j : L - 1;
+            const int je = n0 + 63 < L ? n0 + 63 : L - 1;   // end of the key block
             pf_f = (has_f && j < L) ? FF[(int64_t)j * sfl] : 0.f;
             pf_g = G[(int64_t)jc * sgl];
             pf_cf = j < L ? COLF[j] : 0.f;
-            pf_ge = G[(int64_t)(n0 + 63 < L ? n0 + 63 : L - 1) * sgl];
+            pf_ge = G[(int64_t)je * sgl];
+            pf_fe = has_f ? FF[(int64_t)je * sfl] : 0.f;
         }
     };
     auto issue_tile = [&](DqLds<T>& d, int n0) {   // rows >= L read as zero
@@ -605,6 +619,7 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
         dma_issue<1>(dbt, Bm, xb, (int)(n0 * sbl * (int64_t)sizeof(T)), d.bs, w);
         if (tid < 64) {
             d.fk[tid] = pf_f;
+            d.nfe[tid] = pf_fe - pf_f;
             d.gk[tid] = pf_g;
             d.cfm[tid] = pf_cf * exp2_le0((ga - pf_ge) * LOG2E);
         }
@@ -634,8 +649,7 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
         advance(t);
         if (live) {
             const DqLds<T>& sm = smb[t & (NBUF - 1)];
-            dq_tile<T, false>(sm, sm.cfm, lane, 64 * t, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, scale, R, dqa,
-                              dca);
+            dq_tile<T, false>(sm, lane, 64 * t, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, R, dqa, dca);
         }
         if (NBUF == 2) __syncthreads();
     }
@@ -647,8 +661,7 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
         R.ya *= rowfq;
         dca[0] *= rs;
         dca[1] *= rs;
-        dq_tile<T, true>(sm, sm.cfm, lane, tile0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, scale, R, dqa,
-                         dca);
+        dq_tile<T, true>(sm, lane, tile0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, R, dqa, dca);
     }
     if (!live) return;
     const float xat = group_sum(R.xa), yat = group_sum(R.ya), Wa = group_sum(R.wa), Za = group_sum(R.za);
@@ -658,7 +671,7 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
     // self-normalised exact delta and the delta-free diagonal (attention.py:453-463)
     float ssum = Ptt + Za;
     ssum = ssum > 0.f ? ssum : 1.f;
-    const float x0 = Dptt - dhat;
+    const float x0 = Dptt;   // dP_tt - Delta
     const float tt = dhat + (Ptt * x0 + Wa) / ssum;
     const float dstt = Ptt * (Za * x0 - Wa) / ssum;
     const float dl_row = xat + (dhat - tt) * yat;
@@ -674,7 +687,7 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
         f32x4 r = dqa[db];
 #pragma unroll
         for (int i = 0; i < 4; ++i) r[i] = fmaf(dsq, (float)kv[i], r[i]);
-        store_row4<T, T>(dqp + d, r * scale);
+        store_row4<T, T>(dqp + d, r * QSCALE);
     }
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
@@ -712,14 +725,23 @@ struct __attribute__((aligned(16))) DkvLds {
     T ds[64 * DH];               // dO (dP; transposed reads for dv)
     float lse[64], dhat[64], ddel[64], fq[64], gq[64];
     float rq[64];                // rowf * mid for the query block against the workgroup's key block
+    float ftl[64];               // (F_i - F_e) log2e - lse_i (16-bit: anchored off-block scores)
+    float ndh[64];               // -Delta_i (16-bit: the dO.V MFMA's accumulator input)
 };
 
+// kf holds k/8 (the same exact products as the dq kernel's q/8); for 16-bit inputs off-block tiles use the dq kernel's
+// anchor (nfe = F_e - F_j of the workgroup's key block as the q.k accumulator input, ftl per query) and -Delta as the
+// dO.V accumulator input, so both kernels evaluate every pair with the same operations.
 template <class T, bool PAIR>
-SISA_DEV void dkv_tile(const DkvLds<T>& sm, const float* rqm, int lane, int m0, int k0, int L, const frag8<T> (&kf)[2],
-                       const frag8<T> (&vf)[2], const frag8<T>& bfr, float fk, float rk, float gk, float dsd, float lam,
-                       float scale, float& dgu, float& dfs, f32x4 (&dva)[4], f32x4 (&dka)[4], f32x4 (&dba)[2]) {
+SISA_DEV void dkv_tile(const DkvLds<T>& sm, int lane, int m0, int k0, int L, const frag8<T> (&kf)[2],
+                       const frag8<T> (&vf)[2], const frag8<T>& bfr, float fk, float nfe, float rk, float gk, float dsd,
+                       float lam, float& dgu, float& dfs, f32x4 (&dva)[4], f32x4 (&dka)[4], f32x4 (&dba)[2]) {
+    constexpr bool F16 = Anchor<T>::on;
+    constexpr bool ANCH = F16 && !PAIR;
     const int grp = lane >> 4, lc = lane & 15;
     const int kk = k0 + lc;
+    const float* rqm = sm.rq;
+    const f32x4 nfe4 = ANCH ? f32x4{nfe, nfe, nfe, nfe} : zero4();
 #pragma unroll
     for (int st = 0; st < 2; ++st) {           // 32 queries (one K-step of the dk/dv/db products) at a time
         f32x4 pv[2], kv[2], bv[2];             // dv, dk and db operands of the two 16-query blocks (before rounding)
@@ -727,16 +749,18 @@ SISA_DEV void dkv_tile(const DkvLds<T>& sm, const float* rqm, int lane, int m0, 
         for (int hb = 0; hb < 2; ++hb) {       // one 16-query block at a time keeps the live set small
             __builtin_amdgcn_sched_barrier(0);
             const int qb = 2 * st + hb;
+            const int i0 = qb * 16 + 4 * grp;
             const f32x4 sc = mma(frag_rows<T, DH>(sm.qs, qb * 16, 1, lane), kf[1],
-                                 mma(frag_rows<T, DH>(sm.qs, qb * 16, 0, lane), kf[0], zero4()));
+                                 mma(frag_rows<T, DH>(sm.qs, qb * 16, 0, lane), kf[0], nfe4));
             const f32x4 cb = mma(frag_rows<T, DS>(sm.cs, qb * 16, 0, lane), bfr, zero4());
             const f32x4 dp = mma(frag_rows<T, DH>(sm.ds, qb * 16, 1, lane), vf[1],
-                                 mma(frag_rows<T, DH>(sm.ds, qb * 16, 0, lane), vf[0], zero4()));
-            const int i0 = qb * 16 + 4 * grp;
-            const f32x4 lq = lds4f(&sm.lse[i0]), dh = lds4f(&sm.dhat[i0]), dd = lds4f(&sm.ddel[i0]);
-            const f32x4 fq = lds4f(&sm.fq[i0]);
+                                 mma(frag_rows<T, DH>(sm.ds, qb * 16, 0, lane), vf[0],
+                                     F16 ? lds4f(&sm.ndh[i0]) : zero4()));
+            const f32x4 dd = lds4f(&sm.ddel[i0]);
             if (PAIR) {
                 const f32x4 gq = lds4f(&sm.gq[i0]);
+                const f32x4 lq = lds4f(&sm.lse[i0]), fq = lds4f(&sm.fq[i0]);
+                const f32x4 dh = F16 ? zero4() : lds4f(&sm.dhat[i0]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int qq = m0 + i0 + i;
@@ -745,10 +769,10 @@ SISA_DEV void dkv_tile(const DkvLds<T>& sm, const float* rqm, int lane, int m0, 
                     const bool eye = valid && qq == kk;
                     const float dec = valid ? exp2_le0((gq[i] - gk) * LOG2E) : 0.f;
                     const float u = dec * cb[i];
-                    float s = sc[i] * scale + (fq[i] - fk);
+                    float s = sc[i] + (fq[i] - fk);
                     s = s + lam * u;
                     const float p = valid ? fast_exp2(fmaf(s, LOG2E, -lq[i])) : 0.f;
-                    const float dsh = p * (dp[i] - dh[i]);
+                    const float dsh = p * (F16 ? dp[i] : dp[i] - dh[i]);
                     const float dsx = dsh - p * dd[i];
                     const float dso = strict ? dsx : 0.f;
                     dgu += dso * u;
@@ -759,13 +783,18 @@ SISA_DEV void dkv_tile(const DkvLds<T>& sm, const float* rqm, int lane, int m0, 
                 }
             } else {
                 const f32x4 rq = lds4f(&rqm[i0]);
+                const f32x4 off = ANCH ? lds4f(&sm.ftl[i0]) : zero4();
+                const f32x4 lq = ANCH ? zero4() : lds4f(&sm.lse[i0]);
+                const f32x4 fq = ANCH ? zero4() : lds4f(&sm.fq[i0]);
+                const f32x4 dh = F16 ? zero4() : lds4f(&sm.dhat[i0]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float uc = cb[i] * rq[i];
-                    float s = sc[i] * scale + (fq[i] - fk);
-                    s = s + rk * uc;
-                    const float p = fast_exp2(fmaf(s, LOG2E, -lq[i]));
-                    const float dsh = p * (dp[i] - dh[i]);
+                    float s;
+                    if constexpr (ANCH) s = fmaf(rk, uc, sc[i]);
+                    else s = (sc[i] + (fq[i] - fk)) + rk * uc;
+                    const float p = fast_exp2(fmaf(s, LOG2E, ANCH ? off[i] : -lq[i]));
+                    const float dsh = p * (F16 ? dp[i] : dp[i] - dh[i]);
                     const float dsx = dsh - p * dd[i];
                     dgu += dsx * uc;
                     dfs += dsx;
@@ -790,7 +819,7 @@ SISA_DEV void dkv_tile(const DkvLds<T>& sm, const float* rqm, int lane, int m0, 
 }
 
 template <class T>
-__global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a, float scale) {
+__global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a) {
     constexpr int NBUF = sizeof(T) == 2 ? 2 : 1;
     __shared__ DkvLds<T> smb[NBUF];
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
@@ -822,20 +851,23 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
     const int ktile0 = ktile * 64;                 // the workgroup's 64-key decay block
     const int k0 = ktile0 + 16 * w;
     const bool live = k0 < L;
-    const float ge = G[(int64_t)(ktile0 + 63 < L ? ktile0 + 63 : L - 1) * sgl];   // anchor: g at the block end
+    const int kend = ktile0 + 63 < L ? ktile0 + 63 : L - 1;
+    const float ge = G[(int64_t)kend * sgl];       // anchors: g and F at the block end
+    const float fe = has_f ? FF[(int64_t)kend * sfl] : 0.f;
 
     frag8<T> kf[2], vf[2], bfr;
-    float fk, colf, rk, gk, dsd;
+    float fk, nfe, colf, rk, gk, dsd;
     {
         const int kk = k0 + lc;
         const bool ok = kk < L;
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
-            kf[st] = ok ? load8<T>(K + (int64_t)kk * a.k.sl + 32 * st + 8 * grp) : zero8<T>();
+            kf[st] = ok ? scale_frag<T>(load8<T>(K + (int64_t)kk * a.k.sl + 32 * st + 8 * grp), QSCALE) : zero8<T>();
             vf[st] = ok ? load8<T>(V + (int64_t)kk * a.v.sl + 32 * st + 8 * grp) : zero8<T>();
         }
         bfr = ok ? load8<T>(Bm + (int64_t)kk * a.b.sl + 8 * grp) : zero8<T>();
         fk = (has_f && ok) ? FF[(int64_t)kk * sfl] : 0.f;
+        nfe = fe - fk;
         colf = ok ? COLF[kk] : 0.f;
         rk = lam * colf;
         gk = G[(int64_t)(ok ? kk : L - 1) * sgl];
@@ -888,6 +920,8 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
             d.fq[tid] = pf_f;
             d.gq[tid] = pf_g;
             d.rq[tid] = pf_rowf * exp2_le0((pf_gm - ge) * LOG2E);
+            d.ftl[tid] = fmaf(pf_f - fe, LOG2E, -pf_lse);
+            d.ndh[tid] = -pf_dh;
         }
     };
     auto advance = [&](int t) {
@@ -912,8 +946,8 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
         advance(t);
         if (live) {
             const DkvLds<T>& sm = smb[t & (NBUF - 1)];
-            dkv_tile<T, false>(sm, sm.rq, lane, mlast - 64 * t, k0, L, kf, vf, bfr, fk, rk, gk, dsd, lam, scale, dgu,
-                               dfs, dva, dka, dba);
+            dkv_tile<T, false>(sm, lane, mlast - 64 * t, k0, L, kf, vf, bfr, fk, nfe, rk, gk, dsd, lam, dgu, dfs, dva,
+                               dka, dba);
         }
         if (NBUF == 2) __syncthreads();
     }
@@ -924,8 +958,7 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
         dgu *= colf;
         dba[0] *= rk;
         dba[1] *= rk;
-        dkv_tile<T, true>(sm, sm.rq, lane, ktile0, k0, L, kf, vf, bfr, fk, rk, gk, dsd, lam, scale, dgu, dfs, dva,
-                          dka, dba);
+        dkv_tile<T, true>(sm, lane, ktile0, k0, L, kf, vf, bfr, fk, nfe, rk, gk, dsd, lam, dgu, dfs, dva, dka, dba);
     }
     if (!live) return;
     const float Dgu = group_sum(dgu), Dfs = group_sum(dfs);
@@ -936,7 +969,7 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
         const int d = db * 16 + 4 * grp;
-        store_row4<T, T>(dkp + d, dka[db] * scale);
+        store_row4<T, T>(dkp + d, dka[db] * QSCALE);
         store_row4<T, T>(dvp + d, dva[db]);
     }
 #pragma unroll
@@ -987,10 +1020,10 @@ int launch_fwd(const sisa_attn_fwd_args* a, hipStream_t st) {
 template <class T>
 int launch_bwd(const sisa_attn_bwd_args* a, hipStream_t st) {
     const dim3 grid((unsigned)(sisa::cdiv(a->L, 64) * a->B * a->H));
-    attn_bwd_dq_kernel<T><<<grid, NTHB, 0, st>>>(*a, 0.125f);
+    attn_bwd_dq_kernel<T><<<grid, NTHB, 0, st>>>(*a);
     int rc = sisa::launch_status("sisa_attn_bwd (dq)");
     if (rc) return rc;
-    attn_bwd_dkv_kernel<T><<<grid, NTHB, 0, st>>>(*a, 0.125f);
+    attn_bwd_dkv_kernel<T><<<grid, NTHB, 0, st>>>(*a);
     rc = sisa::launch_status("sisa_attn_bwd (dkv)");
     if (rc) return rc;
     const int64_t BHL = (int64_t)a->B * a->H * a->L;
