@@ -35,7 +35,7 @@ PEAK_HBM_GBS = 8000.0
 # HBM bytes per step measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, each scaled by what the same counter
 # reads for a plain 1 GiB copy (fetch x2.0, write x1.0); per-kernel figures in profiles/hbm_traffic_ns_ce.txt.
 # They belong to the kernels of this build: re-measure after a kernel change.
-TRAFFIC_ATTN_NS = 549.0e6        # attn_fwd + attn_bwd_dq + attn_bwd_dkv + dlam, north-star shape
+TRAFFIC_ATTN_NS = 636.0e6        # attn_fwd + attn_bwd_dq + attn_bwd_dkv + dlam, north-star shape
 TRAFFIC_PREP_FWD_NS = 50.8e6     # prep_sums + prep_fwd
 TRAFFIC_LMCE_ROWS_C3 = 3299.8e6  # lmce_rows on the 16384 x 50304 chunk
 
