@@ -186,6 +186,72 @@ typedef struct {
 
 int sisa_lmce_rows(const sisa_lmce_rows_args* a, void* stream);
 
+/* ------------------------------------------------------------------------------------------------ decoder block */
+
+/* RMSNorm over the last axis: y = (x * rsqrt(mean(x^2) + eps)) * w in fp32, stored in the input dtype; rstd (N) fp32
+ * saved for the backward. Backward: dx = rstd * (dy*w - n * mean(dy*w*n)) with n = x*rstd, and dw = sum over rows of
+ * dy*n, reduced deterministically through dw_partial (sisa_rmsnorm_bwd_workspace_bytes). Replaces the eager float32
+ * `RMSNorm.forward` and its autograd (src/sisa/modeling.py:26-36). */
+typedef struct {
+    int64_t N;                 /* rows */
+    int32_t D;                 /* row length, multiple of 8, <= 4096 */
+    int32_t dtype;             /* of x, y, dy, dx: SISA_BF16, SISA_F16 or SISA_F32 */
+    float eps;
+    const void* x; int64_t sx;         /* (N, D), row stride sx */
+    const float* w;                    /* (D) fp32 */
+    void* y; int64_t sy;               /* forward output */
+    float* rstd;                       /* (N) fp32: written by the forward (may be NULL), read by the backward */
+    const void* dy; int64_t sdy;       /* backward: incoming gradient */
+    void* dx; int64_t sdx;             /* backward: gradient of x */
+    float* dw;                         /* backward: (D) fp32 gradient of w */
+    float* dw_partial;                 /* backward workspace */
+} sisa_rmsnorm_args;
+
+int64_t sisa_rmsnorm_bwd_workspace_bytes(int64_t N, int32_t D);
+int sisa_rmsnorm_fwd(const sisa_rmsnorm_args* a, void* stream);
+int sisa_rmsnorm_bwd(const sisa_rmsnorm_args* a, void* stream);
+
+/* SwiGLU activation h = silu(a) * b (fp32 arithmetic, one rounding) and its backward da = dh * b * silu'(a),
+ * db = dh * silu(a), over n contiguous elements (n a multiple of 8). Replaces `F.silu(self.w_gate(x)) * self.w_up(x)`
+ * and its autograd (src/sisa/modeling.py:48-49). */
+typedef struct {
+    int64_t n;
+    int32_t dtype;             /* SISA_BF16, SISA_F16 or SISA_F32 */
+    const void* a;             /* gate pre-activation */
+    const void* b;             /* up projection */
+    void* h;                   /* forward output */
+    const void* dh;            /* backward: incoming gradient */
+    void* da;                  /* backward outputs */
+    void* db;
+} sisa_swiglu_args;
+
+int sisa_swiglu_fwd(const sisa_swiglu_args* a, void* stream);
+int sisa_swiglu_bwd(const sisa_swiglu_args* a, void* stream);
+
+/* ------------------------------------------------------------------------------------------------ decoding */
+
+/* Attention of M new query rows (positions q_start .. q_start+M-1) against the N cached positions of a decode
+ * cache, exact fp32 score and softmax, fp32 output (B,H,M,64) contiguous:
+ *   s_mj = q_m.k_j/8 + lam_h * exp(g_m - g_j) * (c_m.b_j) + (F_m - F_j) for j <= q_start + m.
+ * Replaces `_attend_rows` (src/sisa/functional.py:69-93) in the decode step of `SISAAttention._forward_cached`
+ * (src/sisa/modeling.py:224-238). Split over 256-key chunks; workspace sisa_decode_workspace_bytes(B,H,M,N). */
+typedef struct {
+    int32_t B, H, M, N;
+    int32_t dtype;             /* of q, k, v, c, b: SISA_BF16, SISA_F16 or SISA_F32 */
+    int32_t q_start;           /* position of query row 0; q_start + M <= N */
+    sisa_view q, k, v;         /* (B,H,M,64), (B,H,N,64), (B,H,N,64) */
+    sisa_view c, b;            /* (B,H,M,32), (B,H,N,32) */
+    sisa_view gq, gk;          /* (B,H,M), (B,H,N) fp32 */
+    sisa_view fq, fk;          /* (B,H,M), (B,H,N) fp32, or both null */
+    const float* lam;          /* (H) fp32, element stride s_lam */
+    int64_t s_lam;
+    float* out;                /* (B,H,M,64) fp32 contiguous */
+    float* workspace;
+} sisa_decode_args;
+
+int64_t sisa_decode_workspace_bytes(int32_t B, int32_t H, int32_t M, int32_t N);
+int sisa_decode_attn(const sisa_decode_args* a, void* stream);
+
 /* ------------------------------------------------------------------------------------------------ misc */
 
 int sisa_abi_version(void);

@@ -1,4 +1,4 @@
-"""Configuration of the SISA attention layer (the fields the hot path and its callers use).
+"""Configuration of a SISA model (the attention layer, the blocks and the causal LM).
 
 Mirrors ``sisa.config`` (src/sisa/config.py:12-16, 19-139) for what the attention sublayer needs: the
 implementation names (the Triton names replaced by the HIP backend's ``"hip"`` and ``"hip_fused"``), the kernel shape
@@ -64,6 +64,18 @@ class SISAConfig:
     @property
     def d_head(self) -> int:
         return self.d_model // self.n_head
+
+    def num_parameters(self) -> int:
+        """Analytic parameter count; the tied LM head is counted once (config.py:100-113)."""
+        d, h, s, f = self.d_model, self.n_head, self.d_state, self.d_ff
+        per_layer = (4 * d * d              # W_Q, W_K, W_V, W_O
+                     + 2 * h * s * d        # W_B, W_C
+                     + h * (s // 2) * d     # theta_proj
+                     + 2 * (h * d + h)      # alpha_proj, forget_proj (weight + bias)
+                     + h                    # lambda_raw
+                     + 2 * d                # attn_norm, ffn_norm
+                     + 3 * d * f)           # SwiGLU
+        return self.n_layer * per_layer + self.vocab_size * d + d
 
     def to_dict(self) -> dict[str, Any]:
         return dataclasses.asdict(self)

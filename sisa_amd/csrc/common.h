@@ -104,6 +104,24 @@ template <class T> SISA_DEV frag8<T> load8(const T* p) { return *reinterpret_cas
 template <class T> SISA_DEV vec4<T> load4(const T* p) { return *reinterpret_cast<const vec4<T>*>(p); }
 template <class T> SISA_DEV void store4(T* p, vec4<T> v) { *reinterpret_cast<vec4<T>*>(p) = v; }
 
+// 8 consecutive elements of any type as fp32 (two 16-byte loads for fp32, one for 16-bit types), and back.
+template <class T> SISA_DEV f32x8 load_f32x8(const T* p) {
+    if constexpr (sizeof(T) == 4) {
+        const f32x4 lo = *reinterpret_cast<const f32x4*>(p), hi = *reinterpret_cast<const f32x4*>(p + 4);
+        return f32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    } else {
+        return __builtin_convertvector(load8<T>(p), f32x8);
+    }
+}
+template <class T> SISA_DEV void store_f32x8(T* p, const f32x8& v) {
+    if constexpr (sizeof(T) == 4) {
+        *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+    } else {
+        *reinterpret_cast<frag8<T>*>(p) = __builtin_convertvector(v, frag8<T>);
+    }
+}
+
 template <class T> SISA_DEV frag8<T> join(vec4<T> lo, vec4<T> hi) {
     frag8<T> r;
     r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];

@@ -69,6 +69,25 @@ class LmceRowsArgs(Structure):
                 ("inv_n", c_void_p), ("gscale", c_float), ("loss_rows", c_void_p), ("lse", c_void_p)]
 
 
+class RmsNormArgs(Structure):
+    _fields_ = [("N", c_int64), ("D", c_int32), ("dtype", c_int32), ("eps", c_float),
+                ("x", c_void_p), ("sx", c_int64), ("w", c_void_p), ("y", c_void_p), ("sy", c_int64),
+                ("rstd", c_void_p), ("dy", c_void_p), ("sdy", c_int64), ("dx", c_void_p), ("sdx", c_int64),
+                ("dw", c_void_p), ("dw_partial", c_void_p)]
+
+
+class SwigluArgs(Structure):
+    _fields_ = [("n", c_int64), ("dtype", c_int32), ("a", c_void_p), ("b", c_void_p), ("h", c_void_p),
+                ("dh", c_void_p), ("da", c_void_p), ("db", c_void_p)]
+
+
+class DecodeArgs(Structure):
+    _fields_ = [("B", c_int32), ("H", c_int32), ("M", c_int32), ("N", c_int32), ("dtype", c_int32),
+                ("q_start", c_int32), ("q", View), ("k", View), ("v", View), ("c", View), ("b", View),
+                ("gq", View), ("gk", View), ("fq", View), ("fk", View), ("lam", c_void_p), ("s_lam", c_int64),
+                ("out", c_void_p), ("workspace", c_void_p)]
+
+
 # exported symbol -> (argument types, return type); the same list the header declares
 SIGNATURES = {
     "sisa_abi_version": ([], c_int),
@@ -81,6 +100,13 @@ SIGNATURES = {
     "sisa_prep_bwd_workspace_bytes": ([c_int32, c_int32, c_int32], c_int64),
     "sisa_prep_bwd": ([POINTER(PrepBwdArgs), c_void_p], c_int),
     "sisa_lmce_rows": ([POINTER(LmceRowsArgs), c_void_p], c_int),
+    "sisa_rmsnorm_bwd_workspace_bytes": ([c_int64, c_int32], c_int64),
+    "sisa_rmsnorm_fwd": ([POINTER(RmsNormArgs), c_void_p], c_int),
+    "sisa_rmsnorm_bwd": ([POINTER(RmsNormArgs), c_void_p], c_int),
+    "sisa_swiglu_fwd": ([POINTER(SwigluArgs), c_void_p], c_int),
+    "sisa_swiglu_bwd": ([POINTER(SwigluArgs), c_void_p], c_int),
+    "sisa_decode_workspace_bytes": ([c_int32, c_int32, c_int32, c_int32], c_int64),
+    "sisa_decode_attn": ([POINTER(DecodeArgs), c_void_p], c_int),
 }
 
 _LOCK = threading.Lock()

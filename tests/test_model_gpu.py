@@ -1,0 +1,178 @@
+"""GPU tests of the model around the hot path: the decoder-block kernels (RMSNorm, SwiGLU activation), the decode
+kernel, and the whole causal LM through the three attention implementations against the dense fp64 oracle.
+
+Model-level gates follow the reference's integration judge (tests/test_model_cuda.py:1-8, 58-80 of tlstngud/sisa):
+under bf16 autocast the error against fp64 is dominated by bf16 rounding outside the attention and is the same for
+all implementations, so the HIP paths are judged against the torch glue under the same autocast: loss deviation
+<= max(2 d_torch, 2e-3) nats, logits e <= 2 e_torch + 1e-3 and, per parameter group, e <= 3 e_torch + 2e-3.
+Kernel gates: RMSNorm / SwiGLU against float32 torch (fp32 inputs 1e-6, bf16 inputs: no worse than torch's own bf16
+path + one bf16 rounding); decode rows against the float32 torch rows (1e-5).
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import model64 as M64
+
+from model_utils import rel_err, tiny_model, token_ids
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BF16_U = 2.0 ** -8
+
+
+@pytest.mark.parametrize("dtype,N,D", [(torch.float32, 1000, 768), (torch.bfloat16, 4099, 512),
+                                       (torch.float16, 33, 1024), (torch.float32, 5, 64), (torch.bfloat16, 1, 4096)])
+def test_rmsnorm_kernel(dtype, N, D):
+    from sisa_amd.kernels.norm import rms_norm_hip
+    gen = torch.Generator().manual_seed(N)
+    x = (3 * torch.randn(N, D, generator=gen)).to(dtype).to(DEV).requires_grad_(True)
+    w = (1 + 0.1 * torch.randn(D, generator=gen)).to(DEV).requires_grad_(True)
+    dy = torch.randn(N, D, generator=gen).to(dtype).to(DEV)
+    y = rms_norm_hip(x, w, 1e-6)
+    dx, dw = torch.autograd.grad(y, (x, w), dy)
+    x64, w64 = x.detach().double().requires_grad_(True), w.detach().double().requires_grad_(True)
+    y64 = (x64 * torch.rsqrt(x64.pow(2).mean(-1, keepdim=True) + 1e-6)) * w64
+    dx64, dw64 = torch.autograd.grad(y64, (x64, w64), dy.double())
+    tol = 1e-6 if dtype == torch.float32 else 2 * BF16_U
+    assert y.dtype == dtype and dx.dtype == dtype and dw.dtype == torch.float32
+    assert rel_err(y, y64) < tol and rel_err(dx, dx64) < tol and rel_err(dw, dw64) < 1e-5
+    again = torch.autograd.grad(rms_norm_hip(x, w, 1e-6), (x, w), dy)
+    assert torch.equal(again[0], dx) and torch.equal(again[1], dw)     # deterministic
+
+
+@pytest.mark.parametrize("dtype,shape", [(torch.bfloat16, (4, 77, 2744)), (torch.float32, (3, 40)),
+                                         (torch.float16, (8, 512))])
+def test_swiglu_kernel(dtype, shape):
+    from sisa_amd.kernels.norm import swiglu_hip
+    gen = torch.Generator().manual_seed(1)
+    a = (2 * torch.randn(shape, generator=gen)).to(dtype).to(DEV).requires_grad_(True)
+    b = torch.randn(shape, generator=gen).to(dtype).to(DEV).requires_grad_(True)
+    dh = torch.randn(shape, generator=gen).to(dtype).to(DEV)
+    h = swiglu_hip(a, b)
+    da, db = torch.autograd.grad(h, (a, b), dh)
+    a64, b64 = a.detach().double().requires_grad_(True), b.detach().double().requires_grad_(True)
+    h64 = F.silu(a64) * b64
+    da64, db64 = torch.autograd.grad(h64, (a64, b64), dh.double())
+    tol = 1e-6 if dtype == torch.float32 else 1.5 * BF16_U
+    for got, ref in ((h, h64), (da, da64), (db, db64)):
+        assert got.dtype == dtype and rel_err(got, ref) < tol
+
+
+def _decode_inputs(B, H, M, N, dtype, seed, has_f=True):
+    gen = torch.Generator().manual_seed(seed)
+    q, c = torch.randn(B, H, M, 64, generator=gen), 0.5 * torch.randn(B, H, M, 32, generator=gen)
+    k, v = torch.randn(B, H, N, 64, generator=gen), torch.randn(B, H, N, 64, generator=gen)
+    b = 0.5 * torch.randn(B, H, N, 32, generator=gen)
+    g = torch.cumsum(-F.softplus(torch.randn(B, H, N, generator=gen) - 3), -1)
+    f = torch.cumsum(F.logsigmoid(torch.randn(B, H, N, generator=gen) + 2), -1) if has_f else None
+    lam = F.softplus(torch.randn(H, generator=gen))
+    q_start = N - M
+    t = lambda x: None if x is None else x.to(DEV)                       # noqa: E731
+    return dict(q=t(q.to(dtype)), k=t(k.to(dtype)), v=t(v.to(dtype)), c=t(c.to(dtype)), b=t(b.to(dtype)),
+                g_q=t(g[..., q_start:]), g_k=t(g), lam=t(lam), f_q=t(None if f is None else f[..., q_start:]),
+                f_k=t(f), q_start=q_start)
+
+
+@pytest.mark.parametrize("B,H,M,N,dtype,has_f", [(1, 12, 1, 1, torch.bfloat16, True), (2, 3, 1, 257, torch.bfloat16, True),
+                                                 (1, 2, 5, 1000, torch.float32, True), (3, 2, 1, 4097, torch.float16, False),
+                                                 (1, 16, 2, 16384, torch.bfloat16, True)])
+def test_decode_kernel(B, H, M, N, dtype, has_f):
+    from sisa_amd.functional import _attend_rows
+    from sisa_amd.kernels.decode import sisa_decode_hip
+    d = _decode_inputs(B, H, M, N, dtype, seed=N + M, has_f=has_f)
+    got = sisa_decode_hip(d["q"], d["k"], d["v"], d["c"], d["b"], d["g_q"], d["g_k"], d["lam"], d["f_q"], d["f_k"],
+                          d["q_start"])
+    f = lambda x: None if x is None else x.double()                      # noqa: E731
+    ref = _attend_rows(f(d["q"]), f(d["k"]), f(d["v"]), f(d["c"]), f(d["b"]), f(d["g_q"]), f(d["g_k"]), f(d["lam"]),
+                       f(d["f_q"]), f(d["f_k"]), d["q_start"])
+    assert got.dtype == torch.float32 and got.shape == (B, H, M, 64)
+    assert rel_err(got, ref) < 1e-5
+    again = sisa_decode_hip(d["q"], d["k"], d["v"], d["c"], d["b"], d["g_q"], d["g_k"], d["lam"], d["f_q"], d["f_k"],
+                            d["q_start"])
+    assert torch.equal(got, again)
+
+
+_GROUPS = {"qkvo": ("W_Q", "W_K", "W_V", "W_O"), "bc": ("W_B", "W_C"), "alpha": ("alpha_proj",),
+           "theta": ("theta_proj",), "lambda": ("lambda_raw",), "forget": ("forget_proj",), "norms": ("norm",),
+           "ffn": ("ffn.",), "embed": ("embed",)}
+
+
+def _grouped(grads):
+    return {grp: torch.cat([g.flatten().double() for n, g in sorted(grads.items()) if any(k in n for k in keys)])
+            for grp, keys in _GROUPS.items()}
+
+
+def _run(model, ids, impl, autocast=True, fused_ce=False):
+    model.set_attn_impl(impl)
+    model.zero_grad(set_to_none=True)
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        out = model(ids, labels=ids, fused_ce=fused_ce)
+    out.loss.backward()
+    grads = {n: p.grad.detach().clone() for n, p in model.named_parameters()}
+    return out.loss.item(), (None if out.logits is None else out.logits.detach().float()), grads
+
+
+@pytest.mark.parametrize("seq_len", [2, 63, 200])
+def test_bf16_impls_vs_fp64(seq_len):
+    model = tiny_model(seed=seq_len, theta_scale=0.25).to(DEV)
+    ids = token_ids(2, seq_len, seed=seq_len).to(DEV)
+    loss64, logits64, grads64 = M64.loss_and_grads64(model, ids, ids)
+    res = {impl: _run(model, ids, impl) for impl in ("torch", "hip", "hip_fused")}
+    t_loss, t_logits, t_grads = res["torch"]
+    assert abs(t_loss - loss64) < 2e-2 and rel_err(t_logits, logits64) < 5e-2
+    ref_g, tor_g = _grouped(grads64), _grouped(t_grads)
+    for impl in ("hip", "hip_fused"):
+        loss, logits, grads = res[impl]
+        assert abs(loss - loss64) <= max(2.0 * abs(t_loss - loss64), 2e-3), impl
+        assert rel_err(logits, logits64) <= 2.0 * rel_err(t_logits, logits64) + 1e-3, impl
+        for n, g in grads.items():
+            assert g.dtype == torch.float32 and torch.isfinite(g).all(), (impl, n)
+        imp_g = _grouped(grads)
+        for grp in _GROUPS:
+            e_t = rel_err(tor_g[grp], ref_g[grp])
+            assert rel_err(imp_g[grp], ref_g[grp]) <= 3.0 * e_t + 2e-3, (impl, grp)
+
+
+def test_fp32_hip_close_to_fp64():
+    model = tiny_model(seed=3).to(DEV)
+    ids = token_ids(2, 130, seed=3).to(DEV)
+    loss64, _, grads64 = M64.loss_and_grads64(model, ids, ids)
+    loss, _, grads = _run(model, ids, "hip", autocast=False)
+    assert abs(loss - loss64) / loss64 < 1e-5
+    for n, g in grads.items():
+        assert rel_err(g, grads64[n]) < 1e-3, n
+
+
+def test_hip_determinism_and_fused_ce():
+    model = tiny_model(seed=4, theta_scale=0.25).to(DEV)
+    ids = token_ids(2, 150, seed=4).to(DEV)
+    for impl in ("hip", "hip_fused"):
+        a, b = _run(model, ids, impl), _run(model, ids, impl)
+        assert a[0] == b[0] and torch.equal(a[1], b[1]), impl
+        assert all(torch.equal(a[2][n], b[2][n]) for n in a[2]), impl
+    ref = _run(model, ids, "hip_fused")
+    fused = _run(model, ids, "hip_fused", fused_ce=True)
+    assert fused[1] is None and abs(fused[0] - ref[0]) < 1e-2
+    for grp, (g1, g2) in zip(_GROUPS, zip(_grouped(fused[2]).values(), _grouped(ref[2]).values())):
+        assert rel_err(g1, g2) < 2e-2, grp
+
+
+def test_gpu_decoding_matches_full_forward():
+    """Prefill + decode steps on the HIP paths (decode kernel) against the full forward, fp32 model."""
+    model = tiny_model(seed=5, attn_impl="hip").to(DEV).eval()
+    ids = token_ids(2, 90, seed=5).to(DEV)
+    from sisa_amd import SISACache
+    with torch.no_grad():
+        full = model(ids).logits
+        cache = SISACache()
+        parts = [model(ids[:, :70], cache=cache).logits]
+        parts += [model(ids[:, t:t + 1], cache=cache).logits for t in range(70, 88)]
+        parts.append(model(ids[:, 88:], cache=cache).logits)
+    assert rel_err(torch.cat(parts, 1), full) < 5e-5     # prefill kernel vs decode kernel, fp32 model
+    out = model.generate(ids[:, :20], 6)
+    with torch.no_grad():
+        check = model(out[:, :-1]).logits
+    assert torch.equal(check[:, 19:].argmax(-1), out[:, 20:])
