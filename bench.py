@@ -13,6 +13,8 @@ Reported (one JSON line on rank 0):
   roofline_prep  the prep forward against HBM peak: algorithmic bytes / its average duration.
   lmce       the linear cross-entropy at config 3 (N=16384, d=768, V=50277): step time, TFLOP/s of its three GEMMs
              (6 N V d), hipBLASLt GEMM roofline and the HIP row pass against HBM peak.
+  model_step the full decoder training step at config 4 (sisa-152m, B=8, T=2048, bf16 autocast, fused attention,
+             HIP RMSNorm/SwiGLU, fused linear CE, AdamW): tokens/s.
   cpu_baseline   the reference's pure-PyTorch path (oracle restatement of src/sisa/functional.py:106-155 plus the
              modeling.py glue) on the host cores, on a bounded sample of the same workload (one batch row, all 8
              heads, T=4096, fp32 forward + backward).
@@ -49,6 +51,7 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-reps", type=int, default=8)
     p.add_argument("--no-ce", action="store_true", help="skip the linear cross-entropy leg (config 3)")
+    p.add_argument("--no-model", action="store_true", help="skip the full decoder training step leg (config 4)")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="run one plain device copy of this many MiB first (calibrates HBM byte counters)")
     return p.parse_args()
@@ -130,6 +133,44 @@ def bench_ce(steps: int, warmup: int) -> dict:
                               "frac": round(row_bytes / (ph["rows"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                               "traffic": TRAFFIC_LMCE_ROWS_C3,
                               "algorithmic": "N*Vp*2 B read + N*Vp*2 B written (+12 B per row)"}}
+
+
+def bench_model(steps: int, warmup: int) -> dict:
+    """Full decoder training step at config 4: sisa-152m (12 layers, d=768, H=12, d_head=64, d_state=32, SwiGLU,
+    tied embedding, vocabulary 50277, README init), B=8 x T=2048 uniform random token ids, bf16 autocast; one step =
+    forward with the fused HIP attention path and the chunked HIP linear cross-entropy, backward, AdamW update."""
+    import torch
+
+    from sisa_amd import SISAConfig, SISAForCausalLM
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(4)
+    cfg = SISAConfig.preset("sisa-152m", attn_impl="hip_fused")
+    model = SISAForCausalLM(cfg).to(dev)
+    opt = torch.optim.AdamW(model.param_groups(3e-4, weight_decay=0.1), betas=(0.9, 0.95), fused=True)
+    B, T = 8, 2048
+    ids = torch.randint(0, cfg.vocab_size, (B, T), generator=torch.Generator().manual_seed(4)).to(dev)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            loss = model(ids, labels=ids, fused_ce=True).loss
+        loss.backward()
+        opt.step()
+        return loss
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    return {"workload": "full decoder training step (config 4): sisa-152m, B=8, T=2048, bf16 autocast, hip_fused "
+                        "attention + HIP RMSNorm/SwiGLU + fused linear CE + AdamW", "B": B, "T": T,
+            "params": model.num_parameters(), "steps": steps, "ms_per_step": round(ms, 3),
+            "tokens_per_s": round(B * T / (ms * 1e-3), 1), "loss": round(float(loss), 4)}
 
 
 def cpu_baseline(reps: int) -> dict:
@@ -280,6 +321,8 @@ def main():
     }
     if not args.no_ce:
         out["lmce"] = bench_ce(max(3, args.steps // 2), 2)
+    if not args.no_model:
+        out["model_step"] = bench_model(max(3, args.steps // 4), 2)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_reps)
     print(json.dumps(out), flush=True)
