@@ -15,6 +15,7 @@ Reported (one JSON line on rank 0):
              (6 N V d), hipBLASLt GEMM roofline and the HIP row pass against HBM peak.
   model_step the full decoder training step at config 4 (sisa-152m, B=8, T=2048, bf16 autocast, fused attention,
              HIP RMSNorm/SwiGLU, fused linear CE, AdamW): tokens/s.
+  block_kernels  RMSNorm, SwiGLU activation and decode-attention kernels against HBM peak (config-4 shapes).
   cpu_baseline   the reference's pure-PyTorch path (oracle restatement of src/sisa/functional.py:106-155 plus the
              modeling.py glue) on the host cores, on a bounded sample of the same workload (one batch row, all 8
              heads, T=4096, fp32 forward + backward).
@@ -173,6 +174,65 @@ def bench_model(steps: int, warmup: int) -> dict:
             "tokens_per_s": round(B * T / (ms * 1e-3), 1), "loss": round(float(loss), 4)}
 
 
+def bench_block_kernels(reps: int = 20) -> dict:
+    """The decoder-block and decode kernels at config-4 shapes, each against the HBM roofline (HIP events on the
+    current stream, mean over reps): RMSNorm forward + backward on the fp32 residual stream (16384 x 768), the SwiGLU
+    activation forward + backward (16384 x 2744 bf16), and one decode step of 8 sequences x 12 heads against a
+    16,384-position bf16 cache (algorithmic bytes: k, v, b~ rows and g, F per cached position and head)."""
+    import torch
+    import torch.nn.functional as F
+
+    from sisa_amd.kernels.decode import sisa_decode_hip
+    from sisa_amd.kernels.norm import rms_norm_hip, swiglu_hip
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(5)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e-3
+
+    def line(name, nbytes, sec):
+        gbs = nbytes / sec / 1e9
+        return {"us": round(sec * 1e6, 2), "bytes": int(nbytes), "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4)}
+
+    N, D, FF = 16384, 768, 2744
+    x = torch.randn(N, D, generator=gen).to(dev).requires_grad_(True)
+    w = torch.ones(D, device=dev, requires_grad=True)
+    dy = torch.randn(N, D, generator=gen).to(dev)
+    t_rms_f = timed(lambda: rms_norm_hip(x.detach(), w.detach(), 1e-6))
+    t_rms_fb = timed(lambda: torch.autograd.grad(rms_norm_hip(x, w, 1e-6), (x, w), dy))
+    a = torch.randn(N, FF, generator=gen).to(torch.bfloat16).to(dev).requires_grad_(True)
+    b = torch.randn(N, FF, generator=gen).to(torch.bfloat16).to(dev).requires_grad_(True)
+    dh = torch.randn(N, FF, generator=gen).to(torch.bfloat16).to(dev)
+    t_sw_f = timed(lambda: swiglu_hip(a.detach(), b.detach()))
+    t_sw_fb = timed(lambda: torch.autograd.grad(swiglu_hip(a, b), (a, b), dh))
+    Bd, H, T = 8, 12, 16384
+    k, v = (torch.randn(Bd, H, T, 64, generator=gen).to(torch.bfloat16).to(dev) for _ in range(2))
+    bb = torch.randn(Bd, H, T, 32, generator=gen).to(torch.bfloat16).to(dev)
+    q = torch.randn(Bd, H, 1, 64, generator=gen).to(torch.bfloat16).to(dev)
+    c = torch.randn(Bd, H, 1, 32, generator=gen).to(torch.bfloat16).to(dev)
+    g = torch.cumsum(-F.softplus(torch.randn(Bd, H, T, generator=gen) - 5), -1).to(dev)
+    f = torch.cumsum(F.logsigmoid(torch.randn(Bd, H, T, generator=gen) + 4), -1).to(dev)
+    lam = torch.full((H,), 0.31, device=dev)
+    t_dec = timed(lambda: sisa_decode_hip(q, k, v, c, bb, g[..., -1:], g, lam, f[..., -1:], f, T - 1))
+    return {"workload": "decoder-block and decode kernels at config-4 shapes",
+            "rmsnorm_fwd": line("rmsnorm_fwd", 2 * N * D * 4 + N * 4, t_rms_f),
+            "rmsnorm_fwd_bwd": line("rmsnorm_fwd_bwd", 5 * N * D * 4 + 2 * N * 4, t_rms_fb),
+            "swiglu_fwd": line("swiglu_fwd", 3 * N * FF * 2, t_sw_f),
+            "swiglu_fwd_bwd": line("swiglu_fwd_bwd", 8 * N * FF * 2, t_sw_fb),
+            "decode_step": dict(line("decode_step", Bd * H * T * (160 * 2 + 8), t_dec),
+                                cache_positions=T, sequences=Bd, heads=H)}
+
+
 def cpu_baseline(reps: int) -> dict:
     """A bounded sample of the benchmark workload on the host cores: one batch row (all heads) of the north-star
     shape (T=4096, d_h=64, d_s=32, BASELINE.json config-0 distributions) in fp32, glue + blocked attention forward +
@@ -323,6 +383,7 @@ def main():
         out["lmce"] = bench_ce(max(3, args.steps // 2), 2)
     if not args.no_model:
         out["model_step"] = bench_model(max(3, args.steps // 4), 2)
+        out["block_kernels"] = bench_block_kernels()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_reps)
     print(json.dumps(out), flush=True)

@@ -11,9 +11,9 @@
 //
 // Work decomposition: one workgroup of 4 waves per (query row, chunk of 256 keys); each wave owns 64 keys, one per
 // lane (the lane reads its key's k and b~ rows with 16-byte loads and forms the score); the wave's weighted sum of V
-// runs lane = feature over its 64 keys (coalesced 128-byte rows of v). Each workgroup writes its chunk's (max, sum,
-// unnormalised output) in fixed wave order; a second kernel combines the chunks of a row in chunk order. No atomics:
-// bitwise reproducible.
+// reads the 64 v rows with 16-byte loads (8 per lane) and reduces over keys with shuffles. Each workgroup writes its
+// chunk's (max, sum, unnormalised output) in fixed wave order; a second kernel combines the chunks of a row in chunk
+// order. No atomics: bitwise reproducible.
 #include "common.h"
 #include "host.h"
 
@@ -78,20 +78,37 @@ __global__ __launch_bounds__(64 * DW) void decode_chunk_kernel(sisa_decode_args 
     float l = p;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
-    // weighted sum of V: lane = feature, over the wave's 64 keys
-    float acc = 0.f;
+    // weighted sum of V over the wave's 64 keys: lane l covers features 8 (l%8) .. +7 of keys l/8 + 8 i (i < 8),
+    // one 16-byte load each; the 8 lanes of a feature group are then summed with xor shuffles (fixed order). Keys at
+    // or beyond N are not read; masked keys have weight 0 (as in the reference's weights @ v).
     const int jw = chunk * KCH + w * 64;
     const T* vbase = (const T*)a.v.ptr + (int64_t)b * a.v.sb + (int64_t)h * a.v.sh;
-    const int nk = (a.N - jw < 64) ? a.N - jw : 64;
-    for (int i = 0; i < nk; ++i) {
-        const float pi = __shfl(p, i);
-        if (pi != 0.f) acc = fmaf(pi, (float)vbase[(int64_t)(jw + i) * a.v.sl + lane], acc);
+    const int fg = lane & 7, kq = lane >> 3;
+    f32x8 acc;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int kk = kq + 8 * i;                     // key within the wave's 64
+        const float pk = __shfl(p, kk);
+        if (jw + kk < a.N) {
+            const f32x8 vv = load_f32x8<T>(vbase + (int64_t)(jw + kk) * a.v.sl + 8 * fg);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] = fmaf(pk, vv[e], acc[e]);
+        }
     }
+#pragma unroll
+    for (int o = 8; o < 64; o <<= 1)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o);
     if (lane == 0) {
         wm[w] = mx;
         wl[w] = l;
     }
-    wo[w][lane] = acc;
+    if (kq == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wo[w][8 * fg + e] = acc[e];
+    }
     __syncthreads();
     if (w != 0) return;
     // combine the 4 waves in order into the chunk partial
