@@ -175,46 +175,67 @@ def bench_model(steps: int, warmup: int) -> dict:
 
 
 def bench_block_kernels(reps: int = 20) -> dict:
-    """The decoder-block and decode kernels at config-4 shapes, each against the HBM roofline (HIP events on the
-    current stream, mean over reps): RMSNorm forward + backward on the fp32 residual stream (16384 x 768), the SwiGLU
-    activation forward + backward (16384 x 2744 bf16), and one decode step of 8 sequences x 12 heads against a
-    16,384-position bf16 cache (algorithmic bytes: k, v, b~ rows and g, F per cached position and head)."""
+    """The decoder-block and decode kernels at config-4 shapes, each against the HBM roofline: RMSNorm forward and
+    backward (three launches: rows, two dw reduction levels) on the fp32 residual stream (16384 x 768), the SwiGLU
+    activation forward and backward (16384 x 2744 bf16), and one decode step (chunk + combine launches) of 8
+    sequences x 12 heads against a 16,384-position bf16 cache. Each entry point is called through the C-ABI with
+    prepared arguments, reps times back to back behind a GPU spin so that host overhead is not timed; HIP events on
+    the launch stream. Algorithmic bytes: RMSNorm forward x read + y written (+ rstd), backward x, dy read + dx written
+    (+ rstd, dw); SwiGLU forward a, b read + h written, backward a, b, dh read + da, db written; decode the k, v, b~
+    rows and g, F of every cached position and head."""
+    import ctypes
+
     import torch
     import torch.nn.functional as F
 
-    from sisa_amd.kernels.decode import sisa_decode_hip
-    from sisa_amd.kernels.norm import rms_norm_hip, swiglu_hip
+    from sisa_amd.kernels import _lib
 
     dev = torch.device("cuda:0")
     gen = torch.Generator().manual_seed(5)
+    lib = _lib.load()
 
-    def timed(fn):
-        fn()
+    def timed(name, args, anchor):
+        fn, ref, st = getattr(lib, name), ctypes.byref(args), _lib.stream_of(anchor)
+        if fn(ref, st) != 0:
+            raise RuntimeError(f"{name}: {lib.sisa_last_error().decode()}")
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(20_000_000)          # the GPU spins while the host queues the timed launches
         e0.record()
-        for _ in range(reps):
-            fn()
+        rcs = [fn(ref, st) for _ in range(reps)]
         e1.record()
         torch.cuda.synchronize()
+        if any(rcs):
+            raise RuntimeError(f"{name}: {lib.sisa_last_error().decode()}")
         return e0.elapsed_time(e1) / reps * 1e-3
 
-    def line(name, nbytes, sec):
+    def line(nbytes, sec, **extra):
         gbs = nbytes / sec / 1e9
-        return {"us": round(sec * 1e6, 2), "bytes": int(nbytes), "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4)}
+        return dict({"us": round(sec * 1e6, 2), "bytes": int(nbytes), "achieved": round(gbs, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4)}, **extra)
 
     N, D, FF = 16384, 768, 2744
-    x = torch.randn(N, D, generator=gen).to(dev).requires_grad_(True)
-    w = torch.ones(D, device=dev, requires_grad=True)
+    x = torch.randn(N, D, generator=gen).to(dev)
+    w = (1 + 0.1 * torch.randn(D, generator=gen)).to(dev)
     dy = torch.randn(N, D, generator=gen).to(dev)
-    t_rms_f = timed(lambda: rms_norm_hip(x.detach(), w.detach(), 1e-6))
-    t_rms_fb = timed(lambda: torch.autograd.grad(rms_norm_hip(x, w, 1e-6), (x, w), dy))
-    a = torch.randn(N, FF, generator=gen).to(torch.bfloat16).to(dev).requires_grad_(True)
-    b = torch.randn(N, FF, generator=gen).to(torch.bfloat16).to(dev).requires_grad_(True)
-    dh = torch.randn(N, FF, generator=gen).to(torch.bfloat16).to(dev)
-    t_sw_f = timed(lambda: swiglu_hip(a.detach(), b.detach()))
-    t_sw_fb = timed(lambda: torch.autograd.grad(swiglu_hip(a, b), (a, b), dh))
+    y, dx = torch.empty_like(x), torch.empty_like(x)
+    rstd, dw = torch.empty(N, device=dev), torch.empty(D, device=dev)
+    ws = torch.empty(_lib.workspace_bytes("sisa_rmsnorm_bwd_workspace_bytes", N, D) // 4, device=dev)
+    f32 = _lib.dtype_code(torch.float32)
+    rf = _lib.RmsNormArgs(N, D, f32, 1e-6, x.data_ptr(), D, w.data_ptr(), y.data_ptr(), D, rstd.data_ptr(), None, 0,
+                          None, 0, None, None)
+    rb = _lib.RmsNormArgs(N, D, f32, 1e-6, x.data_ptr(), D, w.data_ptr(), None, 0, rstd.data_ptr(), dy.data_ptr(), D,
+                          dx.data_ptr(), D, dw.data_ptr(), ws.data_ptr())
+    t_rms_f = timed("sisa_rmsnorm_fwd", rf, x)
+    t_rms_b = timed("sisa_rmsnorm_bwd", rb, x)
+    a, b, dh = (torch.randn(N, FF, generator=gen).to(torch.bfloat16).to(dev) for _ in range(3))
+    h, da, db = torch.empty_like(a), torch.empty_like(a), torch.empty_like(a)
+    bf = _lib.dtype_code(torch.bfloat16)
+    sf = _lib.SwigluArgs(N * FF, bf, a.data_ptr(), b.data_ptr(), h.data_ptr(), None, None, None)
+    sb = _lib.SwigluArgs(N * FF, bf, a.data_ptr(), b.data_ptr(), None, dh.data_ptr(), da.data_ptr(), db.data_ptr())
+    t_sw_f = timed("sisa_swiglu_fwd", sf, a)
+    t_sw_b = timed("sisa_swiglu_bwd", sb, a)
+    del a, b, dh, h, da, db
     Bd, H, T = 8, 12, 16384
     k, v = (torch.randn(Bd, H, T, 64, generator=gen).to(torch.bfloat16).to(dev) for _ in range(2))
     bb = torch.randn(Bd, H, T, 32, generator=gen).to(torch.bfloat16).to(dev)
@@ -222,15 +243,20 @@ def bench_block_kernels(reps: int = 20) -> dict:
     c = torch.randn(Bd, H, 1, 32, generator=gen).to(torch.bfloat16).to(dev)
     g = torch.cumsum(-F.softplus(torch.randn(Bd, H, T, generator=gen) - 5), -1).to(dev)
     f = torch.cumsum(F.logsigmoid(torch.randn(Bd, H, T, generator=gen) + 4), -1).to(dev)
+    gq, fq = g[..., -1:].contiguous(), f[..., -1:].contiguous()
     lam = torch.full((H,), 0.31, device=dev)
-    t_dec = timed(lambda: sisa_decode_hip(q, k, v, c, bb, g[..., -1:], g, lam, f[..., -1:], f, T - 1))
-    return {"workload": "decoder-block and decode kernels at config-4 shapes",
-            "rmsnorm_fwd": line("rmsnorm_fwd", 2 * N * D * 4 + N * 4, t_rms_f),
-            "rmsnorm_fwd_bwd": line("rmsnorm_fwd_bwd", 5 * N * D * 4 + 2 * N * 4, t_rms_fb),
-            "swiglu_fwd": line("swiglu_fwd", 3 * N * FF * 2, t_sw_f),
-            "swiglu_fwd_bwd": line("swiglu_fwd_bwd", 8 * N * FF * 2, t_sw_fb),
-            "decode_step": dict(line("decode_step", Bd * H * T * (160 * 2 + 8), t_dec),
-                                cache_positions=T, sequences=Bd, heads=H)}
+    out = torch.empty(Bd, H, 1, 64, device=dev)
+    dws = torch.empty(_lib.workspace_bytes("sisa_decode_workspace_bytes", Bd, H, 1, T) // 4, device=dev)
+    da_ = _lib.DecodeArgs(Bd, H, 1, T, bf, T - 1, _lib.view(q), _lib.view(k), _lib.view(v), _lib.view(c),
+                          _lib.view(bb), _lib.view(gq), _lib.view(g), _lib.view(fq), _lib.view(f), lam.data_ptr(), 1,
+                          out.data_ptr(), dws.data_ptr())
+    t_dec = timed("sisa_decode_attn", da_, q)
+    return {"workload": "decoder-block and decode kernels at config-4 shapes (C-ABI calls, host overhead excluded)",
+            "rmsnorm_fwd": line(2 * N * D * 4 + N * 4, t_rms_f),
+            "rmsnorm_bwd": line(3 * N * D * 4 + N * 4 + 2 * D * 4, t_rms_b),
+            "swiglu_fwd": line(3 * N * FF * 2, t_sw_f),
+            "swiglu_bwd": line(5 * N * FF * 2, t_sw_b),
+            "decode_step": line(Bd * H * T * (160 * 2 + 8), t_dec, cache_positions=T, sequences=Bd, heads=H)}
 
 
 def cpu_baseline(reps: int) -> dict:

@@ -9,11 +9,12 @@
 // exponential, softmax over the valid keys. The reference materialises the (M, N) score matrix with torch GEMMs; here
 // the cache is read once: the work is memory-bound (328 bytes per cached bf16 key and head: k, v, b~, g, F).
 //
-// Work decomposition: one workgroup of 4 waves per (query row, chunk of 256 keys); each wave owns 64 keys, one per
-// lane (the lane reads its key's k and b~ rows with 16-byte loads and forms the score); the wave's weighted sum of V
-// reads the 64 v rows with 16-byte loads (8 per lane) and reduces over keys with shuffles. Each workgroup writes its
-// chunk's (max, sum, unnormalised output) in fixed wave order; a second kernel combines the chunks of a row in chunk
-// order. No atomics: bitwise reproducible.
+// Work decomposition: one workgroup of 4 waves per (query row, chunk of 256 keys); each wave owns 64 keys. Within a
+// wave, 8 consecutive lanes share a key: lane (slot kq, group fg) reads features 8 fg .. 8 fg + 7 of the k, v (and b~)
+// rows of keys kq + 8 i, i < 8, so every load instruction covers whole 128-byte rows. The lane's partial score is
+// summed over the 8 lanes of its key; the weighted sum of V over the key slots. Each workgroup writes its chunk's
+// (max, sum, unnormalised output) in fixed wave order; a second kernel combines the chunks of a row in chunk order.
+// No atomics: bitwise reproducible.
 #include "common.h"
 #include "host.h"
 
@@ -24,77 +25,116 @@ constexpr int DW = 4;                 // waves per workgroup
 constexpr int KCH = 64 * DW;          // keys per chunk (workgroup)
 constexpr int PART = DH + 2;          // chunk partial: max, sum, out[64]
 
+SISA_DEV float wave_max(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+    return x;
+}
+
+SISA_DEV float wave_sum(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+}
+
 template <class T>
 __global__ __launch_bounds__(64 * DW) void decode_chunk_kernel(sisa_decode_args a) {
-    __shared__ float qs[DH], cs[DS];
     __shared__ float wm[DW], wl[DW], wo[DW][DH];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int fg = lane & 7, kq = lane >> 3;           // feature group (8 features), key slot within a group of 8
     const int chunk = blockIdx.x;
     const int row = blockIdx.y;                        // (b, h, m) flattened
     const int M = a.M, H = a.H;
     const int m = row % M, bh = row / M, h = bh % H, b = bh / H;
     const T* Q = (const T*)a.q.ptr + (int64_t)b * a.q.sb + (int64_t)h * a.q.sh + (int64_t)m * a.q.sl;
     const T* C = (const T*)a.c.ptr + (int64_t)b * a.c.sb + (int64_t)h * a.c.sh + (int64_t)m * a.c.sl;
-    if (tid < DH) qs[tid] = (float)Q[tid];
-    else if (tid < DH + DS) cs[tid - DH] = (float)C[tid - DH];
     const float gq = ((const float*)a.gq.ptr)[(int64_t)b * a.gq.sb + (int64_t)h * a.gq.sh + (int64_t)m * a.gq.sl];
     const bool has_f = a.fq.ptr != nullptr;
     const float fq =
         has_f ? ((const float*)a.fq.ptr)[(int64_t)b * a.fq.sb + (int64_t)h * a.fq.sh + (int64_t)m * a.fq.sl] : 0.f;
     const float lam = a.lam[(int64_t)h * a.s_lam];
     const int last = a.q_start + m;                    // the row's last visible key
-    __syncthreads();
-
-    // score of the lane's key
-    const int j = chunk * KCH + w * 64 + lane;
-    const bool valid = j < a.N && j <= last;
-    float s = -__builtin_inff();
-    if (valid) {
-        const T* krow = (const T*)a.k.ptr + (int64_t)b * a.k.sb + (int64_t)h * a.k.sh + (int64_t)j * a.k.sl;
-        const T* brow = (const T*)a.b.ptr + (int64_t)b * a.b.sb + (int64_t)h * a.b.sh + (int64_t)j * a.b.sl;
-        float qk = 0.f, cb = 0.f;
-#pragma unroll
-        for (int v8 = 0; v8 < DH / 8; ++v8) {
-            const f32x8 kv = load_f32x8<T>(krow + 8 * v8);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qk = fmaf(qs[8 * v8 + e], kv[e], qk);
-        }
-#pragma unroll
-        for (int v8 = 0; v8 < DS / 8; ++v8) {
-            const f32x8 bv = load_f32x8<T>(brow + 8 * v8);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) cb = fmaf(cs[8 * v8 + e], bv[e], cb);
-        }
-        const float gk = ((const float*)a.gk.ptr)[(int64_t)b * a.gk.sb + (int64_t)h * a.gk.sh + (int64_t)j * a.gk.sl];
-        s = qk * 0.125f + lam * (expf(gq - gk) * cb);
-        if (has_f)
-            s += fq - ((const float*)a.fk.ptr)[(int64_t)b * a.fk.sb + (int64_t)h * a.fk.sh + (int64_t)j * a.fk.sl];
-    }
-    // wave softmax statistics (NaN scores propagate through the sum)
-    float mx = s;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    const float p = valid ? expf(s - mx) : 0.f;
-    float l = p;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
-    // weighted sum of V over the wave's 64 keys: lane l covers features 8 (l%8) .. +7 of keys l/8 + 8 i (i < 8),
-    // one 16-byte load each; the 8 lanes of a feature group are then summed with xor shuffles (fixed order). Keys at
-    // or beyond N are not read; masked keys have weight 0 (as in the reference's weights @ v).
-    const int jw = chunk * KCH + w * 64;
+    const int jw = chunk * KCH + w * 64;               // the wave's first key
+    const T* kbase = (const T*)a.k.ptr + (int64_t)b * a.k.sb + (int64_t)h * a.k.sh;
+    const T* bbase = (const T*)a.b.ptr + (int64_t)b * a.b.sb + (int64_t)h * a.b.sh;
     const T* vbase = (const T*)a.v.ptr + (int64_t)b * a.v.sb + (int64_t)h * a.v.sh;
-    const int fg = lane & 7, kq = lane >> 3;
+
+    // Row loads first (all independent): the lane's 8 features of k and v (and of b~ for fg < 4) for the keys
+    // jw + kq + 8 i, i < 8; 8 consecutive lanes cover one 128-byte (bf16) row.
+    frag8<T> kr[8], vr[8], br[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int jj = jw + kq + 8 * i;
+        if (jj < a.N && jj <= last) {
+            kr[i] = load8<T>(kbase + (int64_t)jj * a.k.sl + 8 * fg);
+            vr[i] = load8<T>(vbase + (int64_t)jj * a.v.sl + 8 * fg);
+            if (fg < DS / 8) br[i] = load8<T>(bbase + (int64_t)jj * a.b.sl + 8 * fg);
+        }
+    }
+    // per-key scalars with lane = key: lam * exp(g_m - g_j) and F_m - F_j
+    const int j = jw + lane;
+    float dec = 0.f, fd = 0.f;
+    if (j < a.N && j <= last) {
+        dec = lam * expf(gq - ((const float*)a.gk.ptr)[(int64_t)b * a.gk.sb + (int64_t)h * a.gk.sh +
+                                                       (int64_t)j * a.gk.sl]);
+        if (has_f)
+            fd = fq - ((const float*)a.fk.ptr)[(int64_t)b * a.fk.sb + (int64_t)h * a.fk.sh + (int64_t)j * a.fk.sl];
+    }
+    const f32x8 qv = load_f32x8<T>(Q + 8 * fg);
+    f32x8 cv;
+    if (fg < DS / 8) cv = load_f32x8<T>(C + 8 * fg);
+    else
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cv[e] = 0.f;
+
+    // scores: per key, the lane's share q.k/8 + dec * c.b over its 8 features, summed over the 8 lanes of the key
+    float s[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int jj = jw + kq + 8 * i;
+        const bool ok = jj < a.N && jj <= last;
+        const float di = __shfl(dec, kq + 8 * i), fi = __shfl(fd, kq + 8 * i);
+        float qk = 0.f, cb = 0.f;
+        if (ok) {
+            const f32x8 kv = __builtin_convertvector(kr[i], f32x8);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qk = fmaf(qv[e], kv[e], qk);
+            if (fg < DS / 8) {
+                const f32x8 bv = __builtin_convertvector(br[i], f32x8);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) cb = fmaf(cv[e], bv[e], cb);
+            }
+        }
+        float part = fmaf(qk, 0.125f, di * cb);
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) part += __shfl_xor(part, o);
+        s[i] = ok ? part + fi : -__builtin_inff();
+    }
+    // wave softmax statistics over its 64 keys (NaN scores propagate through the sum)
+    float mx = s[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) mx = fmaxf(mx, s[i]);
+#pragma unroll
+    for (int o = 8; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    float p[8], l = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int jj = jw + kq + 8 * i;
+        p[i] = (jj < a.N && jj <= last) ? expf(s[i] - mx) : 0.f;
+        l += p[i];
+    }
+#pragma unroll
+    for (int o = 8; o < 64; o <<= 1) l += __shfl_xor(l, o);
+    // weighted sum of V: the lane's 8 features over its 8 keys, then over the 8 key slots (fixed xor order)
     f32x8 acc;
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const int kk = kq + 8 * i;                     // key within the wave's 64
-        const float pk = __shfl(p, kk);
-        if (jw + kk < a.N) {
-            const f32x8 vv = load_f32x8<T>(vbase + (int64_t)(jw + kk) * a.v.sl + 8 * fg);
+        if (p[i] != 0.f) {
+            const f32x8 vv = __builtin_convertvector(vr[i], f32x8);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] = fmaf(pk, vv[e], acc[e]);
+            for (int e = 0; e < 8; ++e) acc[e] = fmaf(p[i], vv[e], acc[e]);
         }
     }
 #pragma unroll
@@ -130,19 +170,33 @@ __global__ __launch_bounds__(64 * DW) void decode_chunk_kernel(sisa_decode_args 
     }
 }
 
-// out[row] = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c, chunks in order
+// out[row] = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c. One wave per row: chunk c's max and sum are read by
+// lane c mod 64, its output row by lane = feature, chunks in order, 8 row loads issued ahead of their FMAs.
 __global__ __launch_bounds__(64) void decode_combine_kernel(sisa_decode_args a, int nchunk) {
     const int row = blockIdx.x, lane = threadIdx.x;
     const float* part = a.workspace + (int64_t)row * nchunk * PART;
     float M = -__builtin_inff();
-    for (int c = 0; c < nchunk; ++c) M = fmaxf(M, part[(int64_t)c * PART]);
+    for (int c = lane; c < nchunk; c += 64) M = fmaxf(M, part[(int64_t)c * PART]);
+    M = wave_max(M);
     float L = 0.f, o = 0.f;
-    for (int c = 0; c < nchunk; ++c) {
-        const float mc = part[(int64_t)c * PART];
-        const float sc = (mc == -__builtin_inff()) ? 0.f : expf(mc - M);
-        L = fmaf(part[(int64_t)c * PART + 1], sc, L);
-        o = fmaf(part[(int64_t)c * PART + 2 + lane], sc, o);
+    for (int c0 = 0; c0 < nchunk; c0 += 64) {
+        const int c = c0 + lane, nc = nchunk - c0 < 64 ? nchunk - c0 : 64;
+        float sc = 0.f;
+        if (c < nchunk) {
+            const float mc = part[(int64_t)c * PART];
+            sc = (mc == -__builtin_inff()) ? 0.f : expf(mc - M);
+            L = fmaf(part[(int64_t)c * PART + 1], sc, L);
+        }
+        for (int i0 = 0; i0 < nc; i0 += 8) {
+            float t[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                t[e] = i0 + e < nc ? __builtin_nontemporal_load(part + (int64_t)(c0 + i0 + e) * PART + 2 + lane) : 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o = fmaf(t[e], __shfl(sc, i0 + e), o);
+        }
     }
+    L = wave_sum(L);
     a.out[(int64_t)row * DH + lane] = o / L;
 }
 

@@ -123,6 +123,21 @@ __global__ __launch_bounds__(64 * RMS_WAVES) void rmsnorm_bwd_kernel(sisa_rmsnor
     }
 }
 
+// s + p[0] + p[stride] + ... + p[(n-1) stride], added in that order; the loads go out 8 at a time ahead of their adds
+// (a load-add chain would wait for every load in turn).
+SISA_DEV float ordered_sum(const float* __restrict__ p, int64_t stride, int64_t n, float s) {
+    int64_t k = 0;
+    for (; k + 8 <= n; k += 8) {
+        float t[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t[e] = __builtin_nontemporal_load(p + (k + e) * stride);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += t[e];
+    }
+    for (; k < n; ++k) s += p[k * stride];
+    return s;
+}
+
 // Level 2: column block blockIdx.x (256 columns), split blockIdx.y sums partial rows [k0, k1) in order.
 __global__ __launch_bounds__(256) void rmsnorm_dw2_kernel(const float* __restrict__ part, float* __restrict__ part2,
                                                          int64_t np, int D) {
@@ -130,10 +145,7 @@ __global__ __launch_bounds__(256) void rmsnorm_dw2_kernel(const float* __restric
     if (c >= D) return;
     const int64_t per = (np + DW_SPLIT - 1) / DW_SPLIT;
     const int64_t k0 = blockIdx.y * per, k1 = k0 + per < np ? k0 + per : np;
-    float s = 0.f;
-#pragma unroll 8
-    for (int64_t k = k0; k < k1; ++k) s += part[k * D + c];
-    part2[(int64_t)blockIdx.y * D + c] = s;
+    part2[(int64_t)blockIdx.y * D + c] = k1 > k0 ? ordered_sum(part + k0 * D + c, D, k1 - k0, 0.f) : 0.f;
 }
 
 // Level 3: dw[c] = sum over the DW_SPLIT level-2 partials in order.
@@ -141,10 +153,7 @@ __global__ __launch_bounds__(256) void rmsnorm_dw3_kernel(const float* __restric
                                                          int D) {
     const int c = blockIdx.x * 256 + threadIdx.x;
     if (c >= D) return;
-    float s = 0.f;
-#pragma unroll
-    for (int k = 0; k < DW_SPLIT; ++k) s += part2[(int64_t)k * D + c];
-    dw[c] = s;
+    dw[c] = ordered_sum(part2 + c, D, DW_SPLIT, 0.f);
 }
 
 // ------------------------------------------------------------------------------------------------ SwiGLU
