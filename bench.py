@@ -176,7 +176,8 @@ def bench_model(steps: int, warmup: int) -> dict:
 
 def bench_block_kernels(reps: int = 20) -> dict:
     """The decoder-block and decode kernels at config-4 shapes, each against the HBM roofline: RMSNorm forward and
-    backward (three launches: rows, two dw reduction levels) on the fp32 residual stream (16384 x 768), the SwiGLU
+    backward on the fp32 residual stream (16384 x 768) with the normalised rows in bf16 (the FFN norm), the same
+    with the fused 12-head forget projection (the attention norm; backward: row pass, dw reduction, dW_f), the SwiGLU
     activation forward and backward (16384 x 2744 bf16), and one decode step (chunk + combine launches) of 8
     sequences x 12 heads against a 16,384-position bf16 cache. Each entry point is called through the C-ABI with
     prepared arguments, reps times back to back behind a GPU spin so that host overhead is not timed; HIP events on
@@ -214,25 +215,34 @@ def bench_block_kernels(reps: int = 20) -> dict:
         return dict({"us": round(sec * 1e6, 2), "bytes": int(nbytes), "achieved": round(gbs, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4)}, **extra)
 
-    N, D, FF = 16384, 768, 2744
+    N, D, FF, HF = 16384, 768, 2744, 12
     x = torch.randn(N, D, generator=gen).to(dev)
     w = (1 + 0.1 * torch.randn(D, generator=gen)).to(dev)
-    dy = torch.randn(N, D, generator=gen).to(dev)
-    y, dx = torch.empty_like(x), torch.empty_like(x)
-    rstd, dw = torch.empty(N, device=dev), torch.empty(D, device=dev)
-    ws = torch.empty(_lib.workspace_bytes("sisa_rmsnorm_bwd_workspace_bytes", N, D) // 4, device=dev)
-    f32 = _lib.dtype_code(torch.float32)
-    rf = _lib.RmsNormArgs(N, D, f32, 1e-6, x.data_ptr(), D, w.data_ptr(), y.data_ptr(), D, rstd.data_ptr(), None, 0,
-                          None, 0, None, None)
-    rb = _lib.RmsNormArgs(N, D, f32, 1e-6, x.data_ptr(), D, w.data_ptr(), None, 0, rstd.data_ptr(), dy.data_ptr(), D,
-                          dx.data_ptr(), D, dw.data_ptr(), ws.data_ptr())
-    t_rms_f = timed("sisa_rmsnorm_fwd", rf, x)
-    t_rms_b = timed("sisa_rmsnorm_bwd", rb, x)
+    wf = (0.05 * torch.randn(HF, D, generator=gen)).to(dev)
+    bfz = torch.randn(HF, generator=gen).to(dev)
+    dy = torch.randn(N, D, generator=gen).to(torch.bfloat16).to(dev)
+    dz = torch.randn(N, HF, generator=gen).to(dev)
+    y, dx = torch.empty(N, D, device=dev, dtype=torch.bfloat16), torch.empty_like(x)
+    rstd, z, dw = torch.empty(N, device=dev), torch.empty(N, HF, device=dev), torch.empty(D, device=dev)
+    dwf, dbf = torch.empty(HF, D, device=dev), torch.empty(HF, device=dev)
+    ws = torch.empty(_lib.workspace_bytes("sisa_norm_bwd_workspace_bytes", N, D, HF) // 4, device=dev)
+    f32, bf = _lib.dtype_code(torch.float32), _lib.dtype_code(torch.bfloat16)
+
+    def norm_args(H):
+        return _lib.NormArgs(N, D, H, f32, bf, 1e-6, 0, x.data_ptr(), D, w.data_ptr(), wf.data_ptr(), bfz.data_ptr(),
+                             y.data_ptr(), D, rstd.data_ptr(), z.data_ptr(), dy.data_ptr(), D, dz.data_ptr(),
+                             dx.data_ptr(), D, dw.data_ptr(), dwf.data_ptr(), dbf.data_ptr(), ws.data_ptr())
+    # forward: x (fp32) read, y (bf16) and rstd written, + z; backward: x, dy (bf16), rstd read, dx (fp32) written,
+    # + dz read
+    fwd_bytes, bwd_bytes = N * D * (4 + 2) + N * 4, N * D * (4 + 2 + 4) + N * 4 + 2 * D * 4
+    t_rms_f = timed("sisa_norm_fwd", norm_args(0), x)
+    t_rms_b = timed("sisa_norm_bwd", norm_args(0), x)
+    t_nf_f = timed("sisa_norm_fwd", norm_args(HF), x)
+    t_nf_b = timed("sisa_norm_bwd", norm_args(HF), x)
     a, b, dh = (torch.randn(N, FF, generator=gen).to(torch.bfloat16).to(dev) for _ in range(3))
     h, da, db = torch.empty_like(a), torch.empty_like(a), torch.empty_like(a)
-    bf = _lib.dtype_code(torch.bfloat16)
-    sf = _lib.SwigluArgs(N * FF, bf, a.data_ptr(), b.data_ptr(), h.data_ptr(), None, None, None)
-    sb = _lib.SwigluArgs(N * FF, bf, a.data_ptr(), b.data_ptr(), None, dh.data_ptr(), da.data_ptr(), db.data_ptr())
+    sf = _lib.SwigluArgs(N * FF, bf, 0, a.data_ptr(), b.data_ptr(), h.data_ptr(), None, None, None)
+    sb = _lib.SwigluArgs(N * FF, bf, 0, a.data_ptr(), b.data_ptr(), None, dh.data_ptr(), da.data_ptr(), db.data_ptr())
     t_sw_f = timed("sisa_swiglu_fwd", sf, a)
     t_sw_b = timed("sisa_swiglu_bwd", sb, a)
     del a, b, dh, h, da, db
@@ -252,8 +262,10 @@ def bench_block_kernels(reps: int = 20) -> dict:
                           out.data_ptr(), dws.data_ptr())
     t_dec = timed("sisa_decode_attn", da_, q)
     return {"workload": "decoder-block and decode kernels at config-4 shapes (C-ABI calls, host overhead excluded)",
-            "rmsnorm_fwd": line(2 * N * D * 4 + N * 4, t_rms_f),
-            "rmsnorm_bwd": line(3 * N * D * 4 + N * 4 + 2 * D * 4, t_rms_b),
+            "rmsnorm_fwd": line(fwd_bytes, t_rms_f),
+            "rmsnorm_bwd": line(bwd_bytes, t_rms_b),
+            "norm_forget_fwd": line(fwd_bytes + N * HF * 4, t_nf_f),
+            "norm_forget_bwd": line(bwd_bytes + N * HF * 4 + 2 * HF * D * 4, t_nf_b),
             "swiglu_fwd": line(3 * N * FF * 2, t_sw_f),
             "swiglu_bwd": line(5 * N * FF * 2, t_sw_b),
             "decode_step": line(Bd * H * T * (160 * 2 + 8), t_dec, cache_positions=T, sequences=Bd, heads=H)}

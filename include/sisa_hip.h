@@ -211,12 +211,52 @@ int64_t sisa_rmsnorm_bwd_workspace_bytes(int64_t N, int32_t D);
 int sisa_rmsnorm_fwd(const sisa_rmsnorm_args* a, void* stream);
 int sisa_rmsnorm_bwd(const sisa_rmsnorm_args* a, void* stream);
 
+/* RMSNorm with an optional fused projection of the normalised rows, as the SISA attention sublayer uses it: the
+ * normalised input n feeds the concatenated projection GEMM (in the autocast dtype) and the forget-gate logits
+ * z = n W_f^T + b_f in fp32 (src/sisa/modeling.py:166-169, 217-220; RMSNorm modeling.py:26-36):
+ *   forward:  rstd = 1/sqrt(mean(x^2) + eps), n = round_x((x * rstd) * w), y = round_y(n), z = n . W_f^T + b_f
+ *   backward: dn = dy + dz W_f (summed in x's dtype as autograd does), dx = rstd * (du - u * mean(du * u)) with
+ *             u = x * rstd, du = dn * w; dw = sum_rows dn * u; dW_f = dz^T n; db_f = sum_rows dz
+ * Replaces RMSNorm.forward, the autocast cast of its output, `_forget_logits` and their autograd. H = 0 is a plain
+ * RMSNorm with an output dtype of its own. Weight gradients are reduced deterministically through the workspace
+ * (sisa_norm_bwd_workspace_bytes). */
+typedef struct {
+    int64_t N;                 /* rows */
+    int32_t D;                 /* row length, multiple of 8, <= 4096 */
+    int32_t H;                 /* projection outputs, 0..64 (0: none) */
+    int32_t xdtype;            /* of x, dx and of n as the projection reads it: SISA_F32, SISA_BF16 or SISA_F16 */
+    int32_t ydtype;            /* of y and dy: any of the three for an fp32 x, else xdtype */
+    float eps;
+    int32_t reserved;
+    const void* x; int64_t sx;         /* (N, D), row stride sx */
+    const float* w;                    /* (D) fp32 norm weight */
+    const float* wf;                   /* (H, D) fp32 projection weight, row stride D */
+    const float* bf;                   /* (H) fp32 projection bias */
+    void* y; int64_t sy;               /* forward output (N, D) */
+    float* rstd;                       /* (N): written by the forward (may be NULL without a backward), read back */
+    float* z;                          /* (N, H) fp32 forward output, row stride H */
+    const void* dy; int64_t sdy;       /* backward: gradient of y */
+    const float* dz;                   /* backward: (N, H) gradient of z */
+    void* dx; int64_t sdx;             /* backward: gradient of x */
+    float* dw;                         /* backward: (D) */
+    float* dwf;                        /* backward: (H, D) */
+    float* dbf;                        /* backward: (H) */
+    float* workspace;                  /* backward scratch, 16-byte aligned */
+} sisa_norm_args;
+
+int64_t sisa_norm_bwd_workspace_bytes(int64_t N, int32_t D, int32_t H);
+int sisa_norm_fwd(const sisa_norm_args* a, void* stream);
+int sisa_norm_bwd(const sisa_norm_args* a, void* stream);
+
 /* SwiGLU activation h = silu(a) * b (fp32 arithmetic, one rounding) and its backward da = dh * b * silu'(a),
  * db = dh * silu(a), over n contiguous elements (n a multiple of 8). Replaces `F.silu(self.w_gate(x)) * self.w_up(x)`
- * and its autograd (src/sisa/modeling.py:48-49). */
+ * and its autograd (src/sisa/modeling.py:48-49). With pairs = 1, a and b are one array of interleaved 8-element
+ * chunks (a_8k..a_8k+7, b_8k..b_8k+7), the output of one GEMM against the gate and up weights interleaved in 8-row
+ * chunks; the backward then writes the interleaved (da, db) chunks to da (b and db unused). */
 typedef struct {
-    int64_t n;
+    int64_t n;                 /* elements of h */
     int32_t dtype;             /* SISA_BF16, SISA_F16 or SISA_F32 */
+    int32_t pairs;             /* 0: separate a and b; 1: interleaved chunk pairs in a (and da) */
     const void* a;             /* gate pre-activation */
     const void* b;             /* up projection */
     void* h;                   /* forward output */

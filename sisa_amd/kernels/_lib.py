@@ -76,9 +76,17 @@ class RmsNormArgs(Structure):
                 ("dw", c_void_p), ("dw_partial", c_void_p)]
 
 
+class NormArgs(Structure):
+    _fields_ = [("N", c_int64), ("D", c_int32), ("H", c_int32), ("xdtype", c_int32), ("ydtype", c_int32),
+                ("eps", c_float), ("reserved", c_int32), ("x", c_void_p), ("sx", c_int64), ("w", c_void_p),
+                ("wf", c_void_p), ("bf", c_void_p), ("y", c_void_p), ("sy", c_int64), ("rstd", c_void_p),
+                ("z", c_void_p), ("dy", c_void_p), ("sdy", c_int64), ("dz", c_void_p), ("dx", c_void_p),
+                ("sdx", c_int64), ("dw", c_void_p), ("dwf", c_void_p), ("dbf", c_void_p), ("workspace", c_void_p)]
+
+
 class SwigluArgs(Structure):
-    _fields_ = [("n", c_int64), ("dtype", c_int32), ("a", c_void_p), ("b", c_void_p), ("h", c_void_p),
-                ("dh", c_void_p), ("da", c_void_p), ("db", c_void_p)]
+    _fields_ = [("n", c_int64), ("dtype", c_int32), ("pairs", c_int32), ("a", c_void_p), ("b", c_void_p),
+                ("h", c_void_p), ("dh", c_void_p), ("da", c_void_p), ("db", c_void_p)]
 
 
 class DecodeArgs(Structure):
@@ -103,6 +111,9 @@ SIGNATURES = {
     "sisa_rmsnorm_bwd_workspace_bytes": ([c_int64, c_int32], c_int64),
     "sisa_rmsnorm_fwd": ([POINTER(RmsNormArgs), c_void_p], c_int),
     "sisa_rmsnorm_bwd": ([POINTER(RmsNormArgs), c_void_p], c_int),
+    "sisa_norm_bwd_workspace_bytes": ([c_int64, c_int32, c_int32], c_int64),
+    "sisa_norm_fwd": ([POINTER(NormArgs), c_void_p], c_int),
+    "sisa_norm_bwd": ([POINTER(NormArgs), c_void_p], c_int),
     "sisa_swiglu_fwd": ([POINTER(SwigluArgs), c_void_p], c_int),
     "sisa_swiglu_bwd": ([POINTER(SwigluArgs), c_void_p], c_int),
     "sisa_decode_workspace_bytes": ([c_int32, c_int32, c_int32, c_int32], c_int64),

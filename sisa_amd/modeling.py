@@ -76,11 +76,17 @@ class SwiGLU(nn.Module):
         self._config = config
 
     def forward(self, x: Tensor) -> Tensor:
-        a, b = self.w_gate(x), self.w_up(x)
-        if self._config is not None and a.numel() % 8 == 0 and a.numel() > 0 and _use_hip_elementwise(a, self._config):
-            from .kernels.norm import swiglu_hip
+        d_ff = self.w_gate.out_features
+        if (self._config is not None and d_ff % 8 == 0 and x.numel() > 0 and x.shape[-1] % 8 == 0
+                and _use_hip_elementwise(x, self._config)):
+            # one GEMM against the gate and up weights interleaved in 8-row chunks, then the activation on the
+            # chunk pairs (the same dot products as the two projections of the reference)
+            from .kernels.norm import interleave_gate_up, swiglu_pairs_hip
 
-            return self.w_down(swiglu_hip(a, b))
+            cd = _compute_dtype(x)
+            w = interleave_gate_up(self.w_gate.weight.to(cd), self.w_up.weight.to(cd))
+            return self.w_down(swiglu_pairs_hip(F.linear(x, w)))
+        a, b = self.w_gate(x), self.w_up(x)
         return self.w_down(F.silu(a) * b)
 
 
@@ -212,7 +218,9 @@ class SISAAttention(nn.Module):
         bsz, h, seq_len, dh = y.shape
         return self.W_O(y.transpose(1, 2).reshape(bsz, seq_len, h * dh))
 
-    def _forward_fused(self, x: Tensor) -> Tensor:
+    def _forward_fused(self, x: Tensor, z: Tensor | None = None) -> Tensor:
+        """One projection GEMM + HIP prep + HIP attention (modeling.py:217-222). ``z``: the forget-gate logits when
+        the caller has computed them already (the decoder block's fused norm), else ``_forget_logits(x)``."""
         from .kernels.fused_prep import concat_fused_weights, sisa_fused
 
         bsz, seq_len, d = x.shape
@@ -220,7 +228,7 @@ class SISAAttention(nn.Module):
                                             self.W_C.weight, self.theta_proj.weight, self.alpha_proj.weight,
                                             self.alpha_proj.bias)
         proj = F.linear(x, weight, bias)                  # (B, L, NPAD), autocast dtype
-        y = sisa_fused(proj, self._forget_logits(x), self.lam(), self.config.n_head)
+        y = sisa_fused(proj, self._forget_logits(x) if z is None else z, self.lam(), self.config.n_head)
         return self.W_O(y.reshape(bsz, seq_len, d))
 
     def _forward_cached(self, x: Tensor, cache: "SISACache", requested: str) -> Tensor:
@@ -271,6 +279,7 @@ class SISABlock(nn.Module):
         self.attn = SISAAttention(config, layer_idx)
         self.ffn_norm = RMSNorm(config.d_model, config.norm_eps, config)
         self.ffn = SwiGLU(config.d_model, config.d_ff, config)
+        self.fuse_norm = True          # use the fused HIP norm path where it applies (see _fused_norm_ok)
         self._reset_ffn_and_norms()
 
     @torch.no_grad()
@@ -286,7 +295,34 @@ class SISABlock(nn.Module):
         self._reset_ffn_and_norms()
         self.attn.reset_parameters()
 
+    def _fused_norm_ok(self, x: Tensor) -> bool:
+        """The HIP block path applies: GPU input, the fused HIP attention selected for it, and rows the norm
+        kernels take."""
+        if not self.fuse_norm or x.device.type != "cuda" or x.dim() != 3 or x.numel() == 0:
+            return False
+        d, h = x.shape[-1], self.config.n_head
+        if d % 8 or d > 4096 or h > 64 or x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            return False
+        return _resolve_impl(self.config.attn_impl, x, self.config) == "hip_fused"
+
+    def _forward_hip(self, x: Tensor) -> Tensor:
+        """The block on the HIP kernels: the attention norm and the fp32 forget-gate projection in one pass that
+        also emits the normalised rows in the dtype of the projection GEMM (the reference casts them under autocast),
+        the fused attention sublayer, the FFN norm likewise, SwiGLU."""
+        from .kernels.norm import rms_norm_forget_hip, rms_norm_hip
+
+        cd = _compute_dtype(x)
+        out_dtype = cd if x.dtype == torch.float32 else x.dtype
+        at = self.attn
+        n, z = rms_norm_forget_hip(x, self.attn_norm.weight, self.attn_norm.eps, at.forget_proj.weight,
+                                   at.forget_proj.bias, out_dtype)
+        x = x + at._forward_fused(n, z)
+        m = rms_norm_hip(x, self.ffn_norm.weight, self.ffn_norm.eps, out_dtype)
+        return x + self.ffn(m)
+
     def forward(self, x: Tensor, cache: "SISACache | None" = None) -> Tensor:
+        if cache is None and self._fused_norm_ok(x):
+            return self._forward_hip(x)
         x = x + self.attn(self.attn_norm(x), cache=cache)
         return x + self.ffn(self.ffn_norm(x))
 

@@ -39,7 +39,7 @@ def _header_functions():
 def test_library_exports_every_header_function(lib):
     from sisa_amd.kernels import _lib
     declared = _header_functions()
-    assert len(declared) == 17
+    assert len(declared) == 20
     assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
     out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True, check=True)
     exported = set(re.findall(r"\bT (sisa_\w+)$", out.stdout, re.M))
@@ -53,7 +53,8 @@ def test_struct_layout_matches_c(tmp_path):
     pairs = {"View": "sisa_view", "FactorsArgs": "sisa_factors_args", "AttnFwdArgs": "sisa_attn_fwd_args",
              "AttnBwdArgs": "sisa_attn_bwd_args", "PrepFwdArgs": "sisa_prep_fwd_args",
              "PrepBwdArgs": "sisa_prep_bwd_args", "LmceRowsArgs": "sisa_lmce_rows_args",
-             "RmsNormArgs": "sisa_rmsnorm_args", "SwigluArgs": "sisa_swiglu_args", "DecodeArgs": "sisa_decode_args"}
+             "RmsNormArgs": "sisa_rmsnorm_args", "NormArgs": "sisa_norm_args", "SwigluArgs": "sisa_swiglu_args",
+             "DecodeArgs": "sisa_decode_args"}
     lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "sisa_hip.h"', "int main(void) {"]
     expect = []
     for py, c in pairs.items():
@@ -76,8 +77,8 @@ def test_entry_points_reject_bad_arguments_without_a_gpu(lib):
     from sisa_amd.kernels import _lib
     # null argument structs
     for name in ("sisa_attn_fwd", "sisa_attn_bwd", "sisa_prep_fwd", "sisa_prep_bwd", "sisa_lmce_rows",
-                 "sisa_factors", "sisa_rmsnorm_fwd", "sisa_rmsnorm_bwd", "sisa_swiglu_fwd", "sisa_swiglu_bwd",
-                 "sisa_decode_attn"):
+                 "sisa_factors", "sisa_rmsnorm_fwd", "sisa_rmsnorm_bwd", "sisa_norm_fwd", "sisa_norm_bwd",
+                 "sisa_swiglu_fwd", "sisa_swiglu_bwd", "sisa_decode_attn"):
         rc = getattr(lib, name)(None, None)
         assert rc != 0, name
         assert lib.sisa_last_error().decode().startswith(name), name
@@ -102,11 +103,22 @@ def test_decoder_block_entry_points_reject_bad_arguments(lib):
     assert lib.sisa_rmsnorm_fwd(ctypes.byref(r), None) != 0 and "4096" in lib.sisa_last_error().decode()
     r = _lib.RmsNormArgs(0, 64, _lib.BF16, 1e-6, 16, 64, 16, 16, 64, None, None, 0, None, 0, None, None)
     assert lib.sisa_rmsnorm_fwd(ctypes.byref(r), None) == 0               # zero rows: nothing to do
-    s = _lib.SwigluArgs(12, _lib.BF16, 16, 16, 16, None, None, None)
+    # fused norm + projection: width, dtype pair and the projection operands are checked before any launch
+    def norm(N=4, D=64, H=12, xd=_lib.F32, yd=_lib.BF16, wf=16, bf=16, z=16):
+        return _lib.NormArgs(N, D, H, xd, yd, 1e-6, 0, 16, D, 16, wf, bf, 16, D, 16, z)
+    for args, msg in ((norm(H=65), "[0, 64]"), (norm(xd=_lib.BF16, yd=_lib.F32), "dtype pair"),
+                      (norm(wf=None), "needs wf"), (norm(z=None), "needs z"), (norm(D=4100), "multiple of 8")):
+        assert lib.sisa_norm_fwd(ctypes.byref(args), None) != 0 and msg in lib.sisa_last_error().decode(), msg
+    assert lib.sisa_norm_fwd(ctypes.byref(norm(N=0)), None) == 0
+    bwd = norm()
+    assert lib.sisa_norm_bwd(ctypes.byref(bwd), None) != 0 and "workspace" in lib.sisa_last_error().decode()
+    s = _lib.SwigluArgs(12, _lib.BF16, 0, 16, 16, 16, None, None, None)
     assert lib.sisa_swiglu_fwd(ctypes.byref(s), None) != 0 and "multiple of 8" in lib.sisa_last_error().decode()
-    s = _lib.SwigluArgs(16, _lib.BF16, 16, 16, None, None, None, None)
+    s = _lib.SwigluArgs(16, _lib.BF16, 0, 16, 16, None, None, None, None)
     assert lib.sisa_swiglu_fwd(ctypes.byref(s), None) != 0 and "h must be given" in lib.sisa_last_error().decode()
-    s = _lib.SwigluArgs(0, _lib.BF16, 16, 16, 16, None, None, None)
+    s = _lib.SwigluArgs(16, _lib.BF16, 2, 16, 16, 16, None, None, None)
+    assert lib.sisa_swiglu_fwd(ctypes.byref(s), None) != 0 and "pairs" in lib.sisa_last_error().decode()
+    s = _lib.SwigluArgs(0, _lib.BF16, 0, 16, 16, 16, None, None, None)
     assert lib.sisa_swiglu_fwd(ctypes.byref(s), None) == 0
 
 
@@ -115,6 +127,7 @@ def test_workspace_sizes(lib):
     assert lib.sisa_attn_bwd_workspace_bytes(B, H, L) >= 6 * 4 * B * H * L
     assert lib.sisa_prep_bwd_workspace_bytes(B, L, H) > 0
     assert lib.sisa_rmsnorm_bwd_workspace_bytes(16384, 768) >= (16384 // 8 + 64) * 768 * 4
+    assert lib.sisa_norm_bwd_workspace_bytes(16384, 768, 12) >= (16384 // 8 + 64 + 64 * 16) * 768 * 4
 
 
 def test_missing_library_fails_loudly(monkeypatch):

@@ -43,6 +43,50 @@ def test_rmsnorm_kernel(dtype, N, D):
     assert torch.equal(again[0], dx) and torch.equal(again[1], dw)     # deterministic
 
 
+@pytest.mark.parametrize("xd,yd,N,D,H", [(torch.float32, torch.bfloat16, 1000, 768, 12),
+                                         (torch.float32, torch.float32, 257, 128, 2),
+                                         (torch.float32, torch.float16, 33, 1024, 16),
+                                         (torch.bfloat16, torch.bfloat16, 70, 512, 8),
+                                         (torch.float32, torch.bfloat16, 100, 1536, 24),
+                                         (torch.float32, torch.float32, 9, 4096, 64),
+                                         (torch.float16, torch.float16, 5, 200, 5),
+                                         (torch.float32, torch.bfloat16, 300, 768, 0)])
+def test_norm_forget_kernel(xd, yd, N, D, H):
+    """Fused RMSNorm + fp32 forget projection (forward y, z; backward dx, dw, dW_f, db_f) against float64 autograd
+    of the same formula: n = (x * rstd) * w, z = round_x(n) W_f^T + b_f, y = round_y(round_x(n))."""
+    from sisa_amd.kernels.norm import rms_norm_forget_hip, rms_norm_hip
+    gen = torch.Generator().manual_seed(N + D + H)
+    x = (2 * torch.randn(N, D, generator=gen)).to(xd).to(DEV).requires_grad_(True)
+    w = (1 + 0.1 * torch.randn(D, generator=gen)).to(DEV).requires_grad_(True)
+    wf = (0.05 * torch.randn(H, D, generator=gen)).to(DEV).requires_grad_(True)
+    bf = torch.randn(H, generator=gen).to(DEV).requires_grad_(True)
+    dy = torch.randn(N, D, generator=gen).to(yd).to(DEV)
+    dz = torch.randn(N, H, generator=gen).to(DEV)
+    if H:
+        y, z = rms_norm_forget_hip(x, w, 1e-6, wf, bf, yd)
+        dx, dw, dwf, dbf = torch.autograd.grad((y, z), (x, w, wf, bf), (dy, dz))
+    else:
+        y = rms_norm_hip(x, w, 1e-6, yd)
+        dx, dw = torch.autograd.grad(y, (x, w), dy)
+    x64, w64, wf64, bf64 = (t.detach().double().requires_grad_(True) for t in (x, w, wf, bf))
+    n64 = (x64 * torch.rsqrt(x64.pow(2).mean(-1, keepdim=True) + 1e-6)) * w64
+    nr = n64 + (n64.detach().to(xd).double() - n64.detach())          # the rounding to x's dtype, identity gradient
+    z64 = nr @ wf64.t() + bf64
+    outs, grads_in = ((n64, z64), (dy.double(), dz.double())) if H else ((n64,), (dy.double(),))
+    ref = torch.autograd.grad(outs, (x64, w64, wf64, bf64) if H else (x64, w64), grads_in)
+    half_x = xd != torch.float32
+    assert y.dtype == yd and dx.dtype == xd and dw.dtype == torch.float32
+    assert rel_err(y, n64) < (1e-6 if yd == torch.float32 else 1.5 * BF16_U) + (2 * BF16_U if half_x else 0)
+    gate = 1e-2 if half_x else 1e-5
+    assert rel_err(dx, ref[0]) < gate and rel_err(dw, ref[1]) < gate
+    if H:
+        assert z.dtype == torch.float32 and z.shape == (N, H)
+        assert rel_err(z, z64) < (2 * BF16_U if half_x else 1e-6)
+        assert rel_err(dwf, ref[2]) < gate and rel_err(dbf, ref[3]) < 1e-6
+        again = torch.autograd.grad(rms_norm_forget_hip(x, w, 1e-6, wf, bf, yd), (x, w, wf, bf), (dy, dz))
+        assert all(torch.equal(a, b) for a, b in zip(again, (dx, dw, dwf, dbf)))      # deterministic
+
+
 @pytest.mark.parametrize("dtype,shape", [(torch.bfloat16, (4, 77, 2744)), (torch.float32, (3, 40)),
                                          (torch.float16, (8, 512))])
 def test_swiglu_kernel(dtype, shape):
@@ -59,6 +103,31 @@ def test_swiglu_kernel(dtype, shape):
     tol = 1e-6 if dtype == torch.float32 else 1.5 * BF16_U
     for got, ref in ((h, h64), (da, da64), (db, db64)):
         assert got.dtype == dtype and rel_err(got, ref) < tol
+
+
+def test_swiglu_pairs_kernel():
+    """The interleaved-pairs form (one GEMM against the interleaved gate/up weights) gives bitwise the activation and
+    gradients of the two-array form, and the interleaved GEMM the two projections."""
+    from sisa_amd.kernels.norm import interleave_gate_up, swiglu_hip, swiglu_pairs_hip
+    gen = torch.Generator().manual_seed(2)
+    M_, F_, D = 300, 2744, 64
+    a = (2 * torch.randn(M_, F_, generator=gen)).to(torch.bfloat16).to(DEV)
+    b = torch.randn(M_, F_, generator=gen).to(torch.bfloat16).to(DEV)
+    dh = torch.randn(M_, F_, generator=gen).to(torch.bfloat16).to(DEV)
+    ab = torch.stack((a.view(M_, F_ // 8, 8), b.view(M_, F_ // 8, 8)), dim=2).reshape(M_, 2 * F_).requires_grad_(True)
+    h = swiglu_pairs_hip(ab)
+    (dab,) = torch.autograd.grad(h, (ab,), dh)
+    a_, b_ = a.clone().requires_grad_(True), b.clone().requires_grad_(True)
+    h2 = swiglu_hip(a_, b_)
+    da, db = torch.autograd.grad(h2, (a_, b_), dh)
+    assert torch.equal(h, h2)
+    pairs = dab.view(M_, F_ // 8, 2, 8)
+    assert torch.equal(pairs[:, :, 0].reshape(M_, F_), da) and torch.equal(pairs[:, :, 1].reshape(M_, F_), db)
+    x = torch.randn(M_, D, generator=gen).to(DEV)
+    wg, wu = torch.randn(F_, D, generator=gen).to(DEV), torch.randn(F_, D, generator=gen).to(DEV)
+    y = F.linear(x, interleave_gate_up(wg, wu)).view(M_, F_ // 8, 2, 8)
+    assert rel_err(y[:, :, 0].reshape(M_, F_), x @ wg.t()) < 1e-6
+    assert rel_err(y[:, :, 1].reshape(M_, F_), x @ wu.t()) < 1e-6
 
 
 def _decode_inputs(B, H, M, N, dtype, seed, has_f=True):
@@ -176,3 +245,24 @@ def test_gpu_decoding_matches_full_forward():
     with torch.no_grad():
         check = model(out[:, :-1]).logits
     assert torch.equal(check[:, 19:].argmax(-1), out[:, 20:])
+
+
+def test_block_fused_norm_path():
+    """The decoder block's fused HIP norm path (norm + forget projection in one kernel, normalised rows emitted in
+    the autocast dtype) against the same model with the unfused sublayers, and both against fp64."""
+    model = tiny_model(seed=6, theta_scale=0.25, attn_impl="hip_fused").to(DEV)
+    ids = token_ids(2, 140, seed=6).to(DEV)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        assert model.layers[0]._fused_norm_ok(torch.zeros(1, 8, 128, device=DEV))
+    loss64, logits64, grads64 = M64.loss_and_grads64(model, ids, ids)
+    fused = _run(model, ids, "hip_fused")
+    for blk in model.layers:
+        blk.fuse_norm = False
+    plain = _run(model, ids, "hip_fused")
+    for blk in model.layers:
+        blk.fuse_norm = True
+    assert abs(fused[0] - plain[0]) < 2e-3 and rel_err(fused[1], plain[1]) < 5e-3
+    assert rel_err(fused[1], logits64) <= 1.5 * rel_err(plain[1], logits64) + 1e-3
+    ref_g, f_g, p_g = _grouped(grads64), _grouped(fused[2]), _grouped(plain[2])
+    for grp in _GROUPS:
+        assert rel_err(f_g[grp], ref_g[grp]) <= 1.5 * rel_err(p_g[grp], ref_g[grp]) + 2e-3, grp
