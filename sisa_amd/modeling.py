@@ -375,6 +375,13 @@ class SISAModel(nn.Module):
             x = checkpoint(layer, x, use_reentrant=False) if use_ckpt else layer(x, cache=cache)
         return self.final_norm(x)
 
+    def compile_common(self) -> "SISAModel":
+        """The reference compiles the RMSNorm and SwiGLU submodules with ``torch.compile`` (modeling.py:396-414), so
+        that Inductor fuses their elementwise work. Here that work already runs in fused HIP kernels on the GPU
+        (norm + forget projection, interleaved gate/up + SwiGLU), and this build emits no Triton, so the modules are
+        left as they are: state-dict keys stay unchanged. Returns the model."""
+        return self
+
     def set_attn_impl(self, impl: str) -> None:
         """Switch the attention implementation (``auto``/``torch``/``hip``/``hip_fused``) of every layer."""
         self.config.replace(attn_impl=impl)     # validates
@@ -436,7 +443,7 @@ class SISAForCausalLM(SISAModel):
         fused_ce = fused_ce and labels is not None
         if fused_ce:
             if not hidden.is_cuda:
-                raise ValueError("fused_ce=True needs GPU tensors")
+                raise ValueError("fused_ce=True needs CUDA (GPU) tensors")
             from .kernels.linear_ce import linear_cross_entropy
 
             d = hidden.shape[-1]

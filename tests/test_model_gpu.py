@@ -266,3 +266,62 @@ def test_block_fused_norm_path():
     ref_g, f_g, p_g = _grouped(grads64), _grouped(fused[2]), _grouped(plain[2])
     for grp in _GROUPS:
         assert rel_err(f_g[grp], ref_g[grp]) <= 1.5 * rel_err(p_g[grp], ref_g[grp]) + 2e-3, grp
+
+
+def test_auto_selection_and_fallbacks():
+    """auto picks hip_fused under bf16 autocast and hip for fp32 compute; prepared inputs the kernels cannot take
+    (16-bit recurrences) fall back to torch with a warning under auto and raise when hip is forced."""
+    from sisa_amd import backends, sisa_attention
+    from sisa_amd.functional import sisa_attention_torch
+    model = tiny_model(seed=0, attn_impl="auto").to(DEV)
+    x = torch.randn(1, 8, 128, device=DEV)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        assert backends.select_impl("auto", x, model.config) == "hip_fused"
+    assert backends.select_impl("auto", x, model.config) == "hip"
+    gen = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(1, 2, 80, 64, generator=gen).bfloat16().to(DEV) for _ in range(3))
+    c, b = (torch.randn(1, 2, 80, 32, generator=gen).bfloat16().to(DEV) for _ in range(2))
+    g = torch.cumsum(-torch.rand(1, 2, 80, generator=gen), 2).to(DEV)
+    f = torch.cumsum(F.logsigmoid(torch.randn(1, 2, 80, generator=gen)), 2).to(DEV)
+    lam = torch.tensor([0.3, 1.0], device=DEV)
+    backends._WARNED.clear()
+    for g_in, f_in in ((g.bfloat16(), f), (g, f.bfloat16())):
+        with pytest.warns(UserWarning, match="torch attention implementation"):
+            out = sisa_attention(q, k, v, c, b, g_in, lam, f_in, impl="auto")
+        assert torch.equal(out, sisa_attention_torch(q, k, v, c, b, g_in, lam, f_in))
+        with pytest.raises(ValueError, match="float32"):
+            sisa_attention(q, k, v, c, b, g_in, lam, f_in, impl="hip")
+
+
+def test_torch_backend_is_fp32_under_cuda_autocast():
+    from sisa_amd.functional import sisa_attention_torch
+    gen = torch.Generator().manual_seed(1)
+    q, k, v = (torch.randn(1, 2, 200, 64, generator=gen).to(DEV) for _ in range(3))
+    c, b = (torch.randn(1, 2, 200, 32, generator=gen).to(DEV) for _ in range(2))
+    g = torch.cumsum(-0.5 * torch.rand(1, 2, 200, generator=gen), 2).to(DEV)
+    f = torch.cumsum(F.logsigmoid(torch.randn(1, 2, 200, generator=gen)), 2).to(DEV)
+    lam = torch.tensor([0.3, 1.0], device=DEV)
+    plain = sisa_attention_torch(q, k, v, c, b, g, lam, f, block_q=64)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out = sisa_attention_torch(q, k, v, c, b, g, lam, f, block_q=64)
+    assert out.dtype == torch.float32
+    torch.testing.assert_close(out, plain, rtol=1e-6, atol=1e-6)
+
+
+def test_bf16_decoding_close_to_full_forward():
+    """bf16 autocast: prefill + HIP decode-kernel steps against the full fused HIP forward, both judged against the
+    fp64 model (the decode rows are exact fp32 attention on the bf16 cache)."""
+    from sisa_amd import SISACache
+    model = tiny_model(seed=8, theta_scale=0.25, attn_impl="auto").to(DEV).eval()
+    ids = token_ids(2, 96, seed=8).to(DEV)
+    ref = M64.logits64(model, M64.params64(model, requires_grad=False), ids)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        full = model(ids).logits.float()
+        cache = SISACache()
+        parts = [model(ids[:, :33], cache=cache).logits.float()]
+        parts += [model(ids[:, t:t + 1], cache=cache).logits.float() for t in range(33, 96)]
+        out = model.generate(ids[:, :33], max_new_tokens=5)
+    dec = torch.cat(parts, 1)
+    assert out.shape == (2, 38)
+    assert rel_err(dec, ref) <= 2.0 * rel_err(full, ref) + 1e-3
+    assert max(rel_err(dec[:, t], full[:, t]) for t in range(96)) < 5e-2
