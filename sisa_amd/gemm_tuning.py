@@ -40,8 +40,9 @@ def enable_tuned_gemms(filename: str | None = None) -> bool:
 
 
 def tune_training_step(filename: str = TABLE, batch: int = 8, seq_len: int = 2048) -> None:
-    """Run the config-4 training step (sisa-152m, bf16 autocast, fused HIP attention, fused linear CE, AdamW) with
-    TunableOp tuning on, so that every GEMM shape of the step is measured; the table is written to ``filename``."""
+    """Run the config-4 training step (sisa-152m, bf16 autocast, fused HIP attention, fused linear CE, AdamW) and the
+    linear cross-entropy alone at config 3 with TunableOp tuning on, so that every GEMM shape of both is measured; the
+    table is written to ``filename``."""
     from sisa_amd import SISAConfig, SISAForCausalLM
 
     tun = torch.cuda.tunable
@@ -65,7 +66,17 @@ def tune_training_step(filename: str = TABLE, batch: int = 8, seq_len: int = 204
         loss.backward()
         opt.step()
         print(f"tuning step done, loss {float(loss):.4f}, {len(tun.get_results())} GEMM shapes", flush=True)
+    # the chunked linear cross-entropy on its own (config 3: 16,384 rows, no label shift)
+    from sisa_amd.kernels.linear_ce import linear_cross_entropy
+
+    hidden = torch.randn(batch * seq_len, cfg.d_model, device=dev, requires_grad=True)
+    head = (0.02 * torch.randn(cfg.vocab_size, cfg.d_model, device=dev)).requires_grad_(True)
+    labels = torch.randint(0, cfg.vocab_size, (batch * seq_len,), device=dev)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        ce = linear_cross_entropy(hidden, head, labels)
+    ce.backward()
     torch.cuda.synchronize()
+    print(f"tuning CE done, {len(tun.get_results())} GEMM shapes", flush=True)
     tun.tuning_enable(False)
 
 
