@@ -19,6 +19,8 @@ Reported (one JSON line on rank 0):
   model_step the full decoder training step at config 4 (sisa-152m, B=8, T=2048, bf16 autocast, fused attention,
              HIP RMSNorm/SwiGLU, fused linear CE, AdamW): tokens/s.
   block_kernels  RMSNorm, SwiGLU activation and decode-attention kernels against HBM peak (config-4 shapes).
+  projection_gemms  the library GEMMs of one config-4 layer (fwd, dx, dW of W_cat, W_O, gate/up, down) against
+             the bf16 MFMA peak.
   cpu_baseline   the reference's pure-PyTorch path (oracle restatement of src/sisa/functional.py:106-155 plus the
              modeling.py glue) on the host cores, on a bounded sample of the same workload (one batch row, all 8
              heads, T=4096, fp32 forward + backward).
@@ -295,6 +297,51 @@ def bench_block_kernels(reps: int = 20) -> dict:
             "decode_step": line(Bd * H * T * (160 * 2 + 8), t_dec, cache_positions=T, sequences=Bd, heads=H)}
 
 
+def bench_projection_gemms(reps: int = 20) -> dict:
+    """The library GEMMs of the config-4 training step around the hot path (per layer: the W_cat projection with its
+    bias, W_O, the interleaved gate/up projection and the down projection; forward, input-gradient and
+    weight-gradient products; N = 16,384 rows), bf16 in / bf16 out through torch with the shipped TunableOp table,
+    each against the dense bf16 MFMA peak: 2 M N K flop per call, HIP events over reps back-to-back calls."""
+    import torch
+    import torch.nn.functional as F
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(6)
+    M = 16384
+    out = {"workload": "projection GEMMs of one sisa-152m layer at B*T = 16384 rows (bf16, TunableOp table)"}
+    total_ms, total_flop = 0.0, 0.0
+    for name, n, k, bias in (("W_cat", 3280, 768, True), ("W_O", 768, 768, False), ("gate_up", 5488, 768, False),
+                             ("down", 768, 2744, False)):
+        x = torch.randn(M, k, generator=gen).to(torch.bfloat16).to(dev)
+        w = (0.02 * torch.randn(n, k, generator=gen)).to(torch.bfloat16).to(dev)
+        b = torch.zeros(n, dtype=torch.bfloat16, device=dev) if bias else None
+        dy = torch.randn(M, n, generator=gen).to(torch.bfloat16).to(dev)
+        fl = 2.0 * M * n * k
+        row = {}
+        for kind, fn in (("fwd", lambda: F.linear(x, w, b)), ("dx", lambda: dy @ w), ("dw", lambda: dy.t() @ x)):
+            fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            with _quiet_host():
+                torch.cuda._sleep(20_000_000)
+                e0.record()
+                for _ in range(reps):
+                    fn()
+                e1.record()
+                torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / reps
+            tf = fl / (ms * 1e-3) / 1e12
+            row[kind] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 1), "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+            total_ms += ms
+            total_flop += fl
+        out[name] = row
+        del x, w, dy
+    tf = total_flop / (total_ms * 1e-3) / 1e12
+    out["layer_total"] = {"us": round(total_ms * 1e3, 1), "tflops": round(tf, 1), "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                          "bound": "mfma", "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s"}
+    return out
+
+
 def cpu_baseline(reps: int) -> dict:
     """A bounded sample of the benchmark workload on the host cores: one batch row (all heads) of the north-star
     shape (T=4096, d_h=64, d_s=32, BASELINE.json config-0 distributions) in fp32, glue + blocked attention forward +
@@ -450,6 +497,7 @@ def main():
     if not args.no_model:
         out["model_step"] = bench_model(max(3, args.steps // 4), 2)
         out["block_kernels"] = bench_block_kernels()
+        out["projection_gemms"] = bench_projection_gemms()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_reps)
     print(json.dumps(out), flush=True)
