@@ -268,6 +268,29 @@ typedef struct {
 int sisa_swiglu_fwd(const sisa_swiglu_args* a, void* stream);
 int sisa_swiglu_bwd(const sisa_swiglu_args* a, void* stream);
 
+/* ------------------------------------------------------------------------------------------------ weight gradients */
+
+/* C[N x K] (fp32) = A^T B with A (M x N) and B (M x K) row-major bf16/fp16: the weight gradient dW = dY^T X of a
+ * linear layer y = x W^T over M tokens. Replaces the bf16 weight-gradient GEMMs autograd runs for the nn.Linear
+ * projections of the decoder block (src/sisa/modeling.py:79-291) and the cast of their result to the fp32
+ * parameter dtype. Split-K over M (nsplit splits of m_per_split rows, a multiple of 64; sisa_wgrad_splits gives the
+ * default) with a fixed-order reduction through the workspace (sisa_wgrad_workspace_bytes). */
+typedef struct {
+    int64_t M;                 /* reduction length (rows of A and B) */
+    int32_t N, K;              /* output rows and columns */
+    int32_t dtype;             /* of A and B: SISA_BF16 or SISA_F16 */
+    int32_t nsplit;            /* splits of M, 1..64 */
+    int64_t m_per_split;       /* rows per split, multiple of 64, nsplit * m_per_split >= M */
+    const void* a; int64_t lda;        /* (M, N), row stride lda >= N, multiple of 8 */
+    const void* b; int64_t ldb;        /* (M, K), row stride ldb >= K, multiple of 8 */
+    float* c; int64_t ldc;             /* (N, K) fp32 output, row stride ldc >= K */
+    float* workspace;                  /* nsplit * N * K fp32 when nsplit > 1 */
+} sisa_wgrad_args;
+
+int32_t sisa_wgrad_splits(int64_t M, int32_t N, int32_t K);
+int64_t sisa_wgrad_workspace_bytes(int64_t M, int32_t N, int32_t K, int32_t nsplit);
+int sisa_wgrad(const sisa_wgrad_args* a, void* stream);
+
 /* ------------------------------------------------------------------------------------------------ decoding */
 
 /* Attention of M new query rows (positions q_start .. q_start+M-1) against the N cached positions of a decode

@@ -144,13 +144,15 @@ template <class T> SISA_DEV vec4<T> to_vec4(f32x4 x) { return __builtin_convertv
 // A tile is 64 rows (sequence positions) x C features stored densely row-major in LDS, in 16-byte chunks. For 16-bit
 // types the chunks of a row are XOR-swizzled so that both fragment reads below are free of bank conflicts:
 //   C = 64 (8 chunks per row): physical chunk = chunk ^ (row % 8);
-//   C = 32 (4 chunks per row): physical chunk = chunk ^ 2 * ((row / 4) % 2).
+//   C = 32 (4 chunks per row): physical chunk = chunk ^ 2 * ((row / 4) % 2);
+//   C >= 128 (16+ chunks per row, transpose reads only): physical chunk = chunk ^ 2 * (row % 4).
 // (8 consecutive rows of one chunk column, and the 4-row x 32-byte footprint of a transpose read, then fall on
 // distinct banks.) fp32 tiles (the accuracy path) are not swizzled.
 template <class T, int C>
 SISA_DEV int swz(int row) {
     if constexpr (sizeof(T) != 2) return 0;
     else if constexpr (C == 64) return row & 7;
+    else if constexpr (C >= 128) return (row & 3) << 1;
     else return ((row >> 2) & 1) << 1;
 }
 // element offset of (row, 16-byte chunk) in a tile

@@ -89,6 +89,12 @@ class SwigluArgs(Structure):
                 ("h", c_void_p), ("dh", c_void_p), ("da", c_void_p), ("db", c_void_p)]
 
 
+class WgradArgs(Structure):
+    _fields_ = [("M", c_int64), ("N", c_int32), ("K", c_int32), ("dtype", c_int32), ("nsplit", c_int32),
+                ("m_per_split", c_int64), ("a", c_void_p), ("lda", c_int64), ("b", c_void_p), ("ldb", c_int64),
+                ("c", c_void_p), ("ldc", c_int64), ("workspace", c_void_p)]
+
+
 class DecodeArgs(Structure):
     _fields_ = [("B", c_int32), ("H", c_int32), ("M", c_int32), ("N", c_int32), ("dtype", c_int32),
                 ("q_start", c_int32), ("q", View), ("k", View), ("v", View), ("c", View), ("b", View),
@@ -116,6 +122,9 @@ SIGNATURES = {
     "sisa_norm_bwd": ([POINTER(NormArgs), c_void_p], c_int),
     "sisa_swiglu_fwd": ([POINTER(SwigluArgs), c_void_p], c_int),
     "sisa_swiglu_bwd": ([POINTER(SwigluArgs), c_void_p], c_int),
+    "sisa_wgrad_splits": ([c_int64, c_int32, c_int32], c_int32),
+    "sisa_wgrad_workspace_bytes": ([c_int64, c_int32, c_int32, c_int32], c_int64),
+    "sisa_wgrad": ([POINTER(WgradArgs), c_void_p], c_int),
     "sisa_decode_workspace_bytes": ([c_int32, c_int32, c_int32, c_int32], c_int64),
     "sisa_decode_attn": ([POINTER(DecodeArgs), c_void_p], c_int),
 }

@@ -1,0 +1,82 @@
+"""Weight gradients of linear layers on the HIP kernel ``sisa_wgrad`` (``include/sisa_hip.h``): ``dW = dY^T X`` in
+fp32 from bf16/fp16 operands, and ``linear_hip``, a linear layer whose forward and input gradient stay on the
+library GEMMs and whose weight gradient uses the kernel (the weight-gradient products autograd runs for the
+nn.Linear projections of src/sisa/modeling.py:79-291, written in fp32 without the bf16 rounding and cast pass).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+from . import _lib
+
+__all__ = ["wgrad_hip", "linear_hip"]
+
+TM = 64
+
+
+def _rows16(t: Tensor) -> Tensor:
+    t2 = t.reshape(-1, t.shape[-1])
+    if t2.stride(-1) != 1 or t2.stride(0) % 8 or t2.data_ptr() % 16:
+        t2 = t2.contiguous()
+    return t2
+
+
+def wgrad_hip(dy: Tensor, x: Tensor, out: Tensor | None = None, nsplit: int | None = None) -> Tensor:
+    """``dy^T x`` in fp32 for ``dy`` ``(..., N)`` and ``x`` ``(..., K)`` of one 16-bit dtype (the leading dims are
+    the reduction); returns ``(N, K)`` float32 (written into ``out`` when given)."""
+    if dy.dtype != x.dtype or dy.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"wgrad_hip: dy {dy.dtype} and x {x.dtype} must be one of bf16/fp16")
+    a, b = _rows16(dy), _rows16(x)
+    if a.shape[0] != b.shape[0]:
+        raise ValueError(f"wgrad_hip: {a.shape[0]} rows of dy vs {b.shape[0]} of x")
+    M, N = a.shape
+    K = b.shape[1]
+    lib = _lib.load()
+    s = int(lib.sisa_wgrad_splits(M, N, K)) if nsplit is None else int(nsplit)
+    per = -(-M // s)
+    per = -(-per // TM) * TM
+    if out is None:
+        out = torch.empty((N, K), device=dy.device, dtype=torch.float32)
+    elif out.shape != (N, K) or out.dtype != torch.float32 or out.stride(1) != 1:
+        raise ValueError("wgrad_hip: out must be an (N, K) float32 tensor with unit column stride")
+    ws_bytes = int(lib.sisa_wgrad_workspace_bytes(M, N, K, s))
+    ws = torch.empty(max(ws_bytes // 4, 1), device=dy.device, dtype=torch.float32) if ws_bytes else None
+    args = _lib.WgradArgs(M, N, K, _lib.dtype_code(dy.dtype), s, per, a.data_ptr(), a.stride(0), b.data_ptr(),
+                          b.stride(0), out.data_ptr(), out.stride(0), _lib.ptr(ws))
+    _lib.call("sisa_wgrad", args, dy)
+    return out
+
+
+class _LinearFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x: Tensor, weight: Tensor, bias: Tensor | None, cd: torch.dtype) -> Tensor:
+        w16 = weight.detach().to(cd)
+        x16 = x.detach().to(cd)
+        b16 = None if bias is None else bias.detach().to(cd)
+        ctx.save_for_backward(x16, w16)
+        ctx.has_bias, ctx.wdtype, ctx.bdtype = bias is not None, weight.dtype, None if bias is None else bias.dtype
+        ctx.xdtype = x.dtype
+        return F.linear(x16, w16, b16)
+
+    @staticmethod
+    def backward(ctx, dy: Tensor):
+        x16, w16 = ctx.saved_tensors
+        dy16 = dy.to(w16.dtype)
+        dx = (dy16 @ w16).to(ctx.xdtype) if ctx.needs_input_grad[0] else None
+        dw = wgrad_hip(dy16, x16).to(ctx.wdtype) if ctx.needs_input_grad[1] else None
+        db = None
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            db = dy16.reshape(-1, dy16.shape[-1]).sum(0, dtype=torch.float32).to(ctx.bdtype)
+        return dx, dw, db, None
+
+
+def linear_hip(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
+    """``F.linear(x, weight, bias)`` in the autocast dtype (bf16/fp16; the weights' dtype without autocast) with the
+    weight gradient from :func:`wgrad_hip` (fp32 accumulation, no rounding to 16 bits before the parameter's
+    dtype). The input gradient and the forward stay on the library GEMMs."""
+    cd = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else weight.dtype
+    if cd not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"linear_hip: compute dtype {cd} is not bf16/fp16")
+    return _LinearFn.apply(x, weight, bias, cd)

@@ -85,9 +85,20 @@ class SwiGLU(nn.Module):
 
             cd = _compute_dtype(x)
             w = interleave_gate_up(self.w_gate.weight.to(cd), self.w_up.weight.to(cd))
-            return self.w_down(swiglu_pairs_hip(F.linear(x, w)))
+            return _linear(swiglu_pairs_hip(F.linear(x, w)), self.w_down.weight)
         a, b = self.w_gate(x), self.w_up(x)
         return self.w_down(F.silu(a) * b)
+
+
+def _linear(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
+    """``F.linear`` of the HIP block path: with a 16-bit compute dtype on the GPU the weight gradient comes from the
+    HIP weight-gradient kernel (fp32, split-K over the tokens) instead of the library GEMM and its cast."""
+    if x.is_cuda and _compute_dtype(x) in (torch.bfloat16, torch.float16) and x.shape[-1] % 8 == 0 \
+            and weight.shape[0] % 8 == 0:
+        from .kernels.wgrad import linear_hip
+
+        return linear_hip(x, weight, bias)
+    return F.linear(x, weight, bias)
 
 
 def _compute_dtype(x: Tensor) -> torch.dtype:
@@ -227,9 +238,13 @@ class SISAAttention(nn.Module):
         weight, bias = concat_fused_weights(self.W_Q.weight, self.W_K.weight, self.W_V.weight, self.W_B.weight,
                                             self.W_C.weight, self.theta_proj.weight, self.alpha_proj.weight,
                                             self.alpha_proj.bias)
-        proj = F.linear(x, weight, bias)                  # (B, L, NPAD), autocast dtype
-        y = sisa_fused(proj, self._forget_logits(x) if z is None else z, self.lam(), self.config.n_head)
-        return self.W_O(y.reshape(bsz, seq_len, d))
+        if z is None:                                     # the sublayer on its own (reference dispatch)
+            proj = F.linear(x, weight, bias)              # (B, L, NPAD), autocast dtype
+            y = sisa_fused(proj, self._forget_logits(x), self.lam(), self.config.n_head)
+            return self.W_O(y.reshape(bsz, seq_len, d))
+        proj = _linear(x, weight, bias)                   # the decoder block's HIP path
+        y = sisa_fused(proj, z, self.lam(), self.config.n_head)
+        return _linear(y.reshape(bsz, seq_len, d), self.W_O.weight)
 
     def _forward_cached(self, x: Tensor, cache: "SISACache", requested: str) -> Tensor:
         """Prefill (empty layer cache: regular unfused attention) or decode step (modeling.py:224-238). Decode steps

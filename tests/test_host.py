@@ -39,7 +39,7 @@ def _header_functions():
 def test_library_exports_every_header_function(lib):
     from sisa_amd.kernels import _lib
     declared = _header_functions()
-    assert len(declared) == 20
+    assert len(declared) == 23
     assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
     out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True, check=True)
     exported = set(re.findall(r"\bT (sisa_\w+)$", out.stdout, re.M))
@@ -54,7 +54,7 @@ def test_struct_layout_matches_c(tmp_path):
              "AttnBwdArgs": "sisa_attn_bwd_args", "PrepFwdArgs": "sisa_prep_fwd_args",
              "PrepBwdArgs": "sisa_prep_bwd_args", "LmceRowsArgs": "sisa_lmce_rows_args",
              "RmsNormArgs": "sisa_rmsnorm_args", "NormArgs": "sisa_norm_args", "SwigluArgs": "sisa_swiglu_args",
-             "DecodeArgs": "sisa_decode_args"}
+             "DecodeArgs": "sisa_decode_args", "WgradArgs": "sisa_wgrad_args"}
     lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "sisa_hip.h"', "int main(void) {"]
     expect = []
     for py, c in pairs.items():
@@ -78,7 +78,7 @@ def test_entry_points_reject_bad_arguments_without_a_gpu(lib):
     # null argument structs
     for name in ("sisa_attn_fwd", "sisa_attn_bwd", "sisa_prep_fwd", "sisa_prep_bwd", "sisa_lmce_rows",
                  "sisa_factors", "sisa_rmsnorm_fwd", "sisa_rmsnorm_bwd", "sisa_norm_fwd", "sisa_norm_bwd",
-                 "sisa_swiglu_fwd", "sisa_swiglu_bwd", "sisa_decode_attn"):
+                 "sisa_swiglu_fwd", "sisa_swiglu_bwd", "sisa_decode_attn", "sisa_wgrad"):
         rc = getattr(lib, name)(None, None)
         assert rc != 0, name
         assert lib.sisa_last_error().decode().startswith(name), name
