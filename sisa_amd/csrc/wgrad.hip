@@ -9,7 +9,7 @@
 //
 // Decomposition: a workgroup of 4 waves (2 x 2) computes a 128 x 128 output tile over a range of M (split-K; the
 // partial tiles are summed in split order by a second launch, so results are bitwise reproducible). A wave owns 64 x
-// 64 outputs as 4 x 4 blocks of v_mfma_f32_16x16x32_bf16. Both operands are staged as 64-row tiles (rows = M)
+// 64 outputs as 4 x 4 blocks of v_mfma_f32_16x16x32_bf16. Both operands are staged as 32- or 64-row tiles (rows = M)
 // straight from global memory into LDS (buffer loads with the LDS destination, double-buffered, 16-byte chunks
 // XOR-swizzled per row) and read as MFMA fragments with the LDS transpose read (8 consecutive M of one column per
 // lane), the same sequence map for both operands. Workgroup i runs on XCD i % 8; split = i % nsplit (a power of two)
@@ -19,20 +19,54 @@
 
 namespace {
 
-constexpr int TM = 64;              // M rows per LDS tile (two K-steps of the MFMA)
 constexpr int NW = 4;               // waves per workgroup (2 x 2)
 constexpr int BN = 128, BK = 128;   // workgroup output tile
 constexpr int WTN = 64, WTK = 64;   // wave quarter
 
-template <class T>
+// Staging of a TM-row tile of C 16-bit columns straight into LDS: wave instruction k fills tile bytes
+// [1024 k, 1024 k + 1024), lane i the 16-byte chunk 64 k + i; the per-lane offsets are fixed, the tile's first row
+// enters as the scalar offset.
+template <class T, int C, int TM>
+struct Stage {
+    static constexpr int CPR = C * (int)sizeof(T) / 16;
+    static constexpr int INSTR = TM * CPR / 64;
+    static constexpr int PER = (INSTR + NW - 1) / NW;
+    int voff[PER];
+
+    SISA_DEV void init(int64_t srow, int w, int lane) {
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            const int ci = 64 * (w + NW * p) + lane;
+            const int row = ci / CPR, phys = ci % CPR;
+            voff[p] = (int)(row * srow * (int64_t)sizeof(T) + 16 * (phys ^ swz<T, C>(row)));
+        }
+    }
+};
+
+// ID: one specialization per kernel instantiation (see dma_issue in common.h)
+template <int ID, class T, int C, int TM>
+SISA_DEV void stage_issue(const Stage<T, C, TM>& st, const void* base, int64_t bytes, int soff, T* X, int w) {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(base, bytes);
+#pragma unroll
+    for (int p = 0; p < Stage<T, C, TM>::PER; ++p) {
+        const int k = w + NW * p;
+        if (k < Stage<T, C, TM>::INSTR)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                r, (__attribute__((address_space(3))) void*)(X + k * (1024 / (int)sizeof(T))), 16, st.voff[p], soff, 0,
+                0);
+    }
+}
+
+template <class T, int TM>
 struct __attribute__((aligned(16))) WgLds {
     T a[2][TM * BN];
     T b[2][TM * BK];
 };
 
-template <class T>
+// TM: M rows per LDS tile (32: more workgroups per CU; 64: fewer barriers, for grids of few tiles)
+template <class T, int TM>
 __global__ __launch_bounds__(64 * NW) void wgrad_kernel(sisa_wgrad_args g) {
-    __shared__ WgLds<T> sm;
+    __shared__ WgLds<T, TM> sm;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int split = blockIdx.x % g.nsplit;           // workgroup i runs on XCD i % 8: one split per XCD
@@ -43,8 +77,8 @@ __global__ __launch_bounds__(64 * NW) void wgrad_kernel(sisa_wgrad_args g) {
     const int64_t m_end = m_begin + g.m_per_split < g.M ? m_begin + g.m_per_split : g.M;
     const int ntiles = m_end > m_begin ? (int)((m_end - m_begin + TM - 1) / TM) : 0;
 
-    DmaStage<T, BN, NW> sa;
-    DmaStage<T, BK, NW> sb;
+    Stage<T, BN, TM> sa;
+    Stage<T, BK, TM> sb;
     sa.init(g.lda, w, lane);
     sb.init(g.ldb, w, lane);
     const T* A = (const T*)g.a + n0;
@@ -55,8 +89,8 @@ __global__ __launch_bounds__(64 * NW) void wgrad_kernel(sisa_wgrad_args g) {
     const int64_t bbytes = ((g.M - 1) * g.ldb + g.K - k0) * (int64_t)sizeof(T);
     auto issue = [&](int t, int buf) {
         const int64_t row0 = m_begin + (int64_t)t * TM;
-        dma_issue<0>(sa, A, abytes, (int)(row0 * g.lda * (int64_t)sizeof(T)), sm.a[buf], w);
-        dma_issue<1>(sb, B, bbytes, (int)(row0 * g.ldb * (int64_t)sizeof(T)), sm.b[buf], w);
+        stage_issue<2 * TM + 0>(sa, A, abytes, (int)(row0 * g.lda * (int64_t)sizeof(T)), sm.a[buf], w);
+        stage_issue<2 * TM + 1>(sb, B, bbytes, (int)(row0 * g.ldb * (int64_t)sizeof(T)), sm.b[buf], w);
     };
 
     const int wn = WTN * (w >> 1), wk = WTK * (w & 1);
@@ -127,7 +161,9 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(sisa_wgrad_args g) {
 template <class T>
 int launch_wgrad(const sisa_wgrad_args* g, hipStream_t st) {
     const int tiles = (int)(sisa::cdiv(g->N, BN) * sisa::cdiv(g->K, BK));
-    wgrad_kernel<T><<<(unsigned)(tiles * g->nsplit), 64 * NW, 0, st>>>(*g);
+    const unsigned grid = (unsigned)(tiles * g->nsplit);
+    if (tiles < 64) wgrad_kernel<T, 64><<<grid, 64 * NW, 0, st>>>(*g);
+    else wgrad_kernel<T, 32><<<grid, 64 * NW, 0, st>>>(*g);
     int rc = sisa::launch_status("sisa_wgrad");
     if (rc || g->nsplit == 1) return rc;
     wgrad_reduce_kernel<<<(unsigned)sisa::cdiv((int64_t)g->N * g->K, 256), 256, 0, st>>>(*g);
@@ -137,12 +173,11 @@ int launch_wgrad(const sisa_wgrad_args* g, hipStream_t st) {
 }  // namespace
 
 extern "C" int32_t sisa_wgrad_splits(int64_t M, int32_t N, int32_t K) {
-    // a power of two up to 8 (it divides the 8 XCDs: one split per XCD), each split at least 1024 rows; none when
-    // the output tiles alone fill the chip several times
+    // the smallest power of two up to 8 (it divides the 8 XCDs: one split per XCD) that gives about two workgroups
+    // per CU, each split at least 1024 rows
     const int64_t tiles = sisa::cdiv(N, BN) * sisa::cdiv(K, BK);
-    if (tiles >= 1024) return 1;
     int64_t s = 1;
-    while (s < 8 && M / (s * 2) >= 1024) s *= 2;
+    while (s < 8 && tiles * s < 500 && M / (s * 2) >= 1024) s *= 2;
     return (int32_t)s;
 }
 
@@ -163,8 +198,8 @@ extern "C" int sisa_wgrad(const sisa_wgrad_args* g, void* stream) {
     SISA_REQUIRE(g->M * g->lda * 2 < ((int64_t)1 << 31) && g->M * g->ldb * 2 < ((int64_t)1 << 31),
                  "sisa_wgrad: operands must be below 2 GiB");
     SISA_REQUIRE(g->nsplit >= 1 && g->nsplit <= 64 && g->m_per_split >= 1 &&
-                     (int64_t)g->nsplit * g->m_per_split >= g->M && g->m_per_split % TM == 0,
-                 "sisa_wgrad: nsplit in [1, 64] and m_per_split (a multiple of %d) covering M", TM);
+                     (int64_t)g->nsplit * g->m_per_split >= g->M && g->m_per_split % 64 == 0,
+                 "sisa_wgrad: nsplit in [1, 64] and m_per_split (a multiple of 64) covering M");
     SISA_REQUIRE(g->nsplit == 1 || (g->workspace && sisa::aligned16(g->workspace)),
                  "sisa_wgrad: split-K needs a workspace of sisa_wgrad_workspace_bytes");
     hipStream_t st = (hipStream_t)stream;
