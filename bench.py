@@ -298,17 +298,22 @@ def bench_block_kernels(reps: int = 20) -> dict:
 
 
 def bench_projection_gemms(reps: int = 20) -> dict:
-    """The library GEMMs of the config-4 training step around the hot path (per layer: the W_cat projection with its
-    bias, W_O, the interleaved gate/up projection and the down projection; forward, input-gradient and
-    weight-gradient products; N = 16,384 rows), bf16 in / bf16 out through torch with the shipped TunableOp table,
-    each against the dense bf16 MFMA peak: 2 M N K flop per call, HIP events over reps back-to-back calls."""
+    """The projection GEMMs of the config-4 training step around the hot path (per layer: the W_cat projection with
+    its bias, W_O, the interleaved gate/up projection and the down projection; forward, input-gradient and
+    weight-gradient products; N = 16,384 rows) as the HIP block path runs them: forward and input gradient on the
+    library GEMMs (bf16, the shipped TunableOp table), weight gradients of W_cat, W_O and down on the HIP kernel
+    sisa_wgrad (fp32 output), that of gate/up on the library. Each against the dense bf16 MFMA peak: 2 M N K flop
+    per call, HIP events over reps back-to-back calls."""
     import torch
     import torch.nn.functional as F
+
+    from sisa_amd.kernels.wgrad import wgrad_hip
 
     dev = torch.device("cuda:0")
     gen = torch.Generator().manual_seed(6)
     M = 16384
-    out = {"workload": "projection GEMMs of one sisa-152m layer at B*T = 16384 rows (bf16, TunableOp table)"}
+    out = {"workload": "projection GEMMs of one sisa-152m layer at B*T = 16384 rows (bf16; library GEMMs with the "
+                       "TunableOp table, HIP weight-gradient kernel for W_cat, W_O, down)"}
     total_ms, total_flop = 0.0, 0.0
     for name, n, k, bias in (("W_cat", 3280, 768, True), ("W_O", 768, 768, False), ("gate_up", 5488, 768, False),
                              ("down", 768, 2744, False)):
@@ -318,7 +323,8 @@ def bench_projection_gemms(reps: int = 20) -> dict:
         dy = torch.randn(M, n, generator=gen).to(torch.bfloat16).to(dev)
         fl = 2.0 * M * n * k
         row = {}
-        for kind, fn in (("fwd", lambda: F.linear(x, w, b)), ("dx", lambda: dy @ w), ("dw", lambda: dy.t() @ x)):
+        dw_fn = (lambda: dy.t() @ x) if name == "gate_up" else (lambda: wgrad_hip(dy, x))
+        for kind, fn in (("fwd", lambda: F.linear(x, w, b)), ("dx", lambda: dy @ w), ("dw", dw_fn)):
             fn()
             torch.cuda.synchronize()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
