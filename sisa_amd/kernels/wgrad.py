@@ -51,13 +51,13 @@ def wgrad_hip(dy: Tensor, x: Tensor, out: Tensor | None = None, nsplit: int | No
 
 class _LinearFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x: Tensor, weight: Tensor, bias: Tensor | None, cd: torch.dtype) -> Tensor:
+    def forward(ctx, x: Tensor, weight: Tensor, bias: Tensor | None, cd: torch.dtype, bias_cols) -> Tensor:
         w16 = weight.detach().to(cd)
         x16 = x.detach().to(cd)
         b16 = None if bias is None else bias.detach().to(cd)
         ctx.save_for_backward(x16, w16)
         ctx.has_bias, ctx.wdtype, ctx.bdtype = bias is not None, weight.dtype, None if bias is None else bias.dtype
-        ctx.xdtype = x.dtype
+        ctx.xdtype, ctx.bias_cols = x.dtype, bias_cols
         return F.linear(x16, w16, b16)
 
     @staticmethod
@@ -68,15 +68,23 @@ class _LinearFn(torch.autograd.Function):
         dw = wgrad_hip(dy16, x16).to(ctx.wdtype) if ctx.needs_input_grad[1] else None
         db = None
         if ctx.has_bias and ctx.needs_input_grad[2]:
-            db = dy16.reshape(-1, dy16.shape[-1]).sum(0, dtype=torch.float32).to(ctx.bdtype)
-        return dx, dw, db, None
+            d2 = dy16.reshape(-1, dy16.shape[-1])
+            if ctx.bias_cols is None:
+                db = d2.sum(0, dtype=torch.float32).to(ctx.bdtype)
+            else:                       # only these bias entries reach a parameter: sum just their columns
+                c0, c1 = ctx.bias_cols
+                db = torch.zeros(d2.shape[1], device=d2.device, dtype=ctx.bdtype)
+                db[c0:c1] = d2[:, c0:c1].sum(0, dtype=torch.float32).to(ctx.bdtype)
+        return dx, dw, db, None, None
 
 
-def linear_hip(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
+def linear_hip(x: Tensor, weight: Tensor, bias: Tensor | None = None, bias_cols: tuple[int, int] | None = None
+               ) -> Tensor:
     """``F.linear(x, weight, bias)`` in the autocast dtype (bf16/fp16; the weights' dtype without autocast) with the
     weight gradient from :func:`wgrad_hip` (fp32 accumulation, no rounding to 16 bits before the parameter's
-    dtype). The input gradient and the forward stay on the library GEMMs."""
+    dtype). The input gradient and the forward stay on the library GEMMs. ``bias_cols = (c0, c1)``: only bias entries
+    c0..c1-1 lead to parameters (the rest is constant padding), so the backward sums only those columns of dy."""
     cd = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else weight.dtype
     if cd not in (torch.bfloat16, torch.float16):
         raise TypeError(f"linear_hip: compute dtype {cd} is not bf16/fp16")
-    return _LinearFn.apply(x, weight, bias, cd)
+    return _LinearFn.apply(x, weight, bias, cd, bias_cols)

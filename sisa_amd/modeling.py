@@ -90,14 +90,15 @@ class SwiGLU(nn.Module):
         return self.w_down(F.silu(a) * b)
 
 
-def _linear(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
+def _linear(x: Tensor, weight: Tensor, bias: Tensor | None = None, bias_cols: tuple[int, int] | None = None
+            ) -> Tensor:
     """``F.linear`` of the HIP block path: with a 16-bit compute dtype on the GPU the weight gradient comes from the
     HIP weight-gradient kernel (fp32, split-K over the tokens) instead of the library GEMM and its cast."""
     if x.is_cuda and _compute_dtype(x) in (torch.bfloat16, torch.float16) and x.shape[-1] % 8 == 0 \
             and weight.shape[0] % 8 == 0:
         from .kernels.wgrad import linear_hip
 
-        return linear_hip(x, weight, bias)
+        return linear_hip(x, weight, bias, bias_cols)
     return F.linear(x, weight, bias)
 
 
@@ -242,7 +243,10 @@ class SISAAttention(nn.Module):
             proj = F.linear(x, weight, bias)              # (B, L, NPAD), autocast dtype
             y = sisa_fused(proj, self._forget_logits(x), self.lam(), self.config.n_head)
             return self.W_O(y.reshape(bsz, seq_len, d))
-        proj = _linear(x, weight, bias)                   # the decoder block's HIP path
+        from .kernels.fused_prep import fused_layout
+
+        a0 = fused_layout(self.config.n_head)["A"]      # only the alpha columns of the bias are parameters
+        proj = _linear(x, weight, bias, (a0, a0 + self.config.n_head))   # the decoder block's HIP path
         y = sisa_fused(proj, z, self.lam(), self.config.n_head)
         return _linear(y.reshape(bsz, seq_len, d), self.W_O.weight)
 

@@ -57,3 +57,18 @@ def test_linear_hip_matches_autograd():
     assert rel_err(dw, dy16.reshape(-1, 384).t() @ x16.reshape(-1, 256)) < 2e-6
     assert rel_err(dx, dy16 @ w16) < 1e-2 and rel_err(db, dy16.sum((0, 1))) < 1e-6
     assert rel_err(y, x16 @ w16.t() + b.detach().bfloat16().double()) < 1e-2
+
+
+def test_linear_hip_bias_columns():
+    """With bias_cols only those bias entries get a gradient (the rest is constant padding); they match the full
+    bias gradient."""
+    from sisa_amd.kernels.wgrad import linear_hip
+    gen = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 200, 128, generator=gen).to(DEV).bfloat16()
+    w = (0.05 * torch.randn(256, 128, generator=gen)).to(DEV).requires_grad_(True)
+    b = torch.randn(256, generator=gen).to(DEV).requires_grad_(True)
+    dy = torch.randn(2, 200, 256, generator=gen).to(DEV)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        full = torch.autograd.grad(linear_hip(x, w, b), (b,), dy)[0]
+        part = torch.autograd.grad(linear_hip(x, w, b, (40, 52)), (b,), dy)[0]
+    assert torch.equal(part[40:52], full[40:52]) and not part[:40].any() and not part[52:].any()
