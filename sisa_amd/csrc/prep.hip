@@ -93,46 +93,108 @@ struct ScanLds {
     float x[HC][CH + 1];
 };
 
-// Stage theta (comps 2..17) of the chunk into the scan lanes.
+// Staging loads of one thread: theta vector `tid` of the chunk (row tid>>3, head (tid>>1)&3, pairs 8*(tid&1)..+7)
+// and, for tid < 256, alpha and z of (row tid>>2, head tid&3). Split from the LDS stores so that a kernel issues
+// every global load it needs before the first wait.
+static_assert(NT == CH * HG * 2, "one theta vector per thread");
 template <class T>
-SISA_DEV void stage_theta(ScanLds& sm, const T* P, int64_t s_pl, int nrows, int hn, const Layout& off, int h0,
-                          int tid) {
-#pragma unroll
-    for (int i = 0; i < 512 / NT; ++i) {
-        const int v = tid + NT * i;
-        const int row = v >> 3, hl = (v >> 1) & 3, half = v & 1;
+struct StageVals {
+    frag8<T> th;
+    float al, zv;
+};
+template <class T, bool AZ = true>
+SISA_DEV StageVals<T> stage_load(const T* P, int64_t s_pl, const float* Z, int64_t s_zl, int nrows, int hn,
+                                 const Layout& off, int h0, int tid) {
+    StageVals<T> s;
+    {
+        const int row = tid >> 3, hl = (tid >> 1) & 3, half = tid & 1;
+        s.th = load8_if<T>(P + (int64_t)row * s_pl + off.TH + (h0 + hl) * S2 + 8 * half, row < nrows && hl < hn);
+    }
+    s.al = 0.f;
+    s.zv = 0.f;
+    if (AZ && tid < CH * HG) {
+        const int row = tid >> 2, hl = tid & 3;
         const bool ok = row < nrows && hl < hn;
-        const frag8<T> t = load8_if<T>(P + (int64_t)row * s_pl + off.TH + (h0 + hl) * S2 + 8 * half, ok);
+        if (ok) s.al = (float)P[(int64_t)row * s_pl + off.A + h0 + hl];
+        if (ok && Z) s.zv = Z[(int64_t)row * s_zl + h0 + hl];
+    }
+    return s;
+}
+// theta into components 2..17; with AZ, the element functions of alpha and z into components 0 and 1.
+template <class T, bool AZ>
+SISA_DEV void stage_store(ScanLds& sm, const StageVals<T>& s, int nrows, int hn, bool has_z, int tid) {
+    {
+        const int row = tid >> 3, hl = (tid >> 1) & 3, half = tid & 1;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) sm.x[hl * NCOMP + 2 + 8 * half + j][row] = (float)t[j];
+        for (int j = 0; j < 8; ++j) sm.x[hl * NCOMP + 2 + 8 * half + j][row] = (float)s.th[j];
+    }
+    if (AZ && tid < CH * HG) {
+        const int row = tid >> 2, hl = tid & 3;
+        const bool ok = row < nrows && hl < hn;
+        sm.x[hl * NCOMP + 0][row] = ok ? neg_softplus(s.al) : 0.f;
+        sm.x[hl * NCOMP + 1][row] = (ok && has_z) ? logsigmoid(s.zv) : 0.f;
     }
 }
 
-// Element functions of alpha and z into components 0 and 1 (one (row, head) per thread).
-template <class T>
-SISA_DEV void stage_alpha_z(ScanLds& sm, const T* P, int64_t s_pl, const float* Z, int64_t s_zl, int nrows, int hn,
-                            const Layout& off, int h0, int tid) {
-    if (tid >= CH * HG) return;
-    const int row = tid >> 2, hl = tid & 3;
-    const bool ok = row < nrows && hl < hn;
-    const float al = ok ? (float)P[(int64_t)row * s_pl + off.A + h0 + hl] : 0.f;
-    const float zv = (ok && Z) ? Z[(int64_t)row * s_zl + h0 + hl] : 0.f;
-    sm.x[hl * NCOMP + 0][row] = ok ? neg_softplus(al) : 0.f;
-    sm.x[hl * NCOMP + 1][row] = (ok && Z) ? logsigmoid(zv) : 0.f;
-}
-
-// Left fold, in chunk order, of the totals of chunks [c0, c1) of one scan lane (`col` points at the lane's component
-// of chunk 0; consecutive chunks are NCOMP apart). The loads of a batch are all issued before the first add.
+// Carries of the scans: the left fold, in chunk order, of the chunk totals of a range of chunks [c0, c1) (the
+// preceding chunks for the forward scans, fp32; the following chunks for the reverse scans, fp64). The totals of up
+// to TB chunks are staged through LDS by all threads (coalesced loads of at most TPT values per thread, issued with
+// the kernel's other loads); after a barrier each scan lane folds its column sequentially, so that in the forward
+// carry_{c+1} = carry_c + TOT_c bit for bit. Longer ranges take further batches.
+constexpr int TB = 64;                         // chunks per staged batch
+constexpr int TPT = (HG * TB * NCOMP) / NT;    // totals loaded per thread and batch
+static_assert(TPT * NT == HG * TB * NCOMP, "staged totals split evenly over the threads");
 template <class Acc>
-SISA_DEV Acc fold_totals(const Acc* col, int c0, int c1, Acc acc) {
-    constexpr int NB = 16;
-    for (int cb = c0; cb < c1; cb += NB) {
-        Acc buf[NB];
+struct TotLds {
+    Acc t[HG][TB * NCOMP];
+};
+// Loads of the totals of chunks [c0, c1) (at most TB of them) of the workgroup's heads; zero past the range.
+template <class Acc>
+SISA_DEV void tot_load(Acc (&v)[TPT], const Acc* tot, int bh0, int hn, int NCH, int c0, int c1, int tid) {
+    const int n = (c1 - c0) * NCOMP;
 #pragma unroll
-        for (int k = 0; k < NB; ++k) buf[k] = (cb + k < c1) ? col[(int64_t)(cb + k) * NCOMP] : (Acc)0;
+    for (int q = 0; q < TPT; ++q) {
+        const int e = tid + NT * q;
+        const int hl = e / (TB * NCOMP), idx = e - hl * (TB * NCOMP);
+        v[q] = (hl < hn && idx < n) ? tot[((int64_t)(bh0 + hl) * NCH + c0) * NCOMP + idx] : (Acc)0;
+    }
+}
+template <class Acc>
+SISA_DEV void tot_store(TotLds<Acc>& tl, const Acc (&v)[TPT], int tid) {
 #pragma unroll
-        for (int k = 0; k < NB; ++k)
-            if (cb + k < c1) acc += buf[k];
+    for (int q = 0; q < TPT; ++q) (&tl.t[0][0])[tid + NT * q] = v[q];
+}
+// Sequential fold of `n` <= TB staged chunks into acc for scan lane (hl, comp). The LDS reads of a batch of FB
+// chunks are all issued before the first add; chunks past n (still inside the staged array) add zero.
+template <class Acc>
+SISA_DEV Acc tot_fold(const TotLds<Acc>& tl, int hl, int comp, int n, Acc acc) {
+    constexpr int FB = 16;
+    static_assert(TB % FB == 0, "whole batches");
+    const Acc* col = tl.t[hl] + comp;
+    for (int k0 = 0; k0 < n; k0 += FB) {
+        Acc buf[FB];
+#pragma unroll
+        for (int k = 0; k < FB; ++k) buf[k] = col[(k0 + k) * NCOMP];
+#pragma unroll
+        for (int k = 0; k < FB; ++k) acc += (k0 + k < n) ? buf[k] : (Acc)0;
+    }
+    return acc;
+}
+// The carry of scan lane tid (when `lane`) over chunks [c0, c1). The caller has loaded the first batch into v with
+// tot_load(v, ..., c0, min(c1, c0 + TB)), stored it (tot_store) and passed a barrier. Further batches are loaded and
+// folded here; every thread of the workgroup calls this (it has barriers when c1 - c0 > TB).
+template <class Acc>
+SISA_DEV Acc carry_of(TotLds<Acc>& tl, Acc (&v)[TPT], const Acc* tot, int bh0, int hn, int NCH, int c0, int c1,
+                      bool lane, int tid) {
+    const int hl = tid / NCOMP, comp = tid % NCOMP;
+    Acc acc = lane ? tot_fold(tl, hl, comp, (c1 - c0 < TB) ? c1 - c0 : TB, (Acc)0) : (Acc)0;
+    for (int cb = c0 + TB; cb < c1; cb += TB) {
+        const int ce = (c1 - cb < TB) ? c1 : cb + TB;
+        tot_load(v, tot, bh0, hn, NCH, cb, ce, tid);
+        __syncthreads();   // every lane is done with the previous batch
+        tot_store(tl, v, tid);
+        __syncthreads();
+        if (lane) acc = tot_fold(tl, hl, comp, ce - cb, acc);
     }
     return acc;
 }
@@ -164,8 +226,8 @@ __global__ __launch_bounds__(NT) void prep_sums_kernel(sisa_prep_fwd_args a) {
     const int tid = threadIdx.x;
     const T* P = (const T*)a.proj + (int64_t)b * a.s_pb + (int64_t)c * CH * a.s_pl;
     const float* Z = a.z ? a.z + (int64_t)b * a.s_zb + (int64_t)c * CH * a.s_zl : nullptr;
-    stage_theta<T>(sm, P, a.s_pl, nrows, hn, off, h0, tid);
-    stage_alpha_z<T>(sm, P, a.s_pl, Z, a.s_zl, nrows, hn, off, h0, tid);
+    stage_store<T, true>(sm, stage_load<T>(P, a.s_pl, Z, a.s_zl, nrows, hn, off, h0, tid), nrows, hn, Z != nullptr,
+                         tid);
     __syncthreads();
     if (tid < HC && tid / NCOMP < hn) {
         float incl = 0.f;
@@ -179,6 +241,7 @@ __global__ __launch_bounds__(NT) void prep_sums_kernel(sisa_prep_fwd_args a) {
 template <class T>
 __global__ __launch_bounds__(NT) void prep_fwd_kernel(sisa_prep_fwd_args a) {
     __shared__ ScanLds sm;
+    __shared__ TotLds<float> tl;
     const int c = blockIdx.x, b = blockIdx.y, h0 = blockIdx.z * HG;
     const int H = a.H, L = a.L, NCH = gridDim.x;
     const int hn = (H - h0 < HG) ? H - h0 : HG;
@@ -187,7 +250,12 @@ __global__ __launch_bounds__(NT) void prep_fwd_kernel(sisa_prep_fwd_args a) {
     const int tid = threadIdx.x;
     const T* P = (const T*)a.proj + (int64_t)b * a.s_pb + (int64_t)c * CH * a.s_pl;
     const float* Z = a.z ? a.z + (int64_t)b * a.s_zb + (int64_t)c * CH * a.s_zl : nullptr;
-    // the C and B vectors this thread rotates: loads issued first, consumed last
+    // Every global load is issued before the first wait, in the order of use: the staged scan inputs, the totals of
+    // the preceding chunks, then the C and B vectors this thread rotates.
+    const StageVals<T> sv = stage_load<T>(P, a.s_pl, Z, a.s_zl, nrows, hn, off, h0, tid);
+    const bool lane = tid < HC && tid / NCOMP < hn;
+    float tv[TPT];
+    tot_load(tv, a.tot, b * H + h0, hn, NCH, 0, c < TB ? c : TB, tid);
     frag8<T> cv[NU], bv[NU];
 #pragma unroll
     for (int i = 0; i < NU; ++i) {
@@ -197,13 +265,10 @@ __global__ __launch_bounds__(NT) void prep_fwd_kernel(sisa_prep_fwd_args a) {
         cv[i] = load8_if<T>(prow + off.C, ok);
         bv[i] = load8_if<T>(prow + off.B, ok);
     }
-    const bool lane = tid < HC && tid / NCOMP < hn;
-    const float carry =
-        lane ? fold_totals<float>(a.tot + ((int64_t)(b * H + h0 + tid / NCOMP) * NCH) * NCOMP + tid % NCOMP, 0, c, 0.f)
-             : 0.f;
-    stage_theta<T>(sm, P, a.s_pl, nrows, hn, off, h0, tid);
-    stage_alpha_z<T>(sm, P, a.s_pl, Z, a.s_zl, nrows, hn, off, h0, tid);
+    stage_store<T, true>(sm, sv, nrows, hn, Z != nullptr, tid);
+    tot_store(tl, tv, tid);
     __syncthreads();
+    const float carry = carry_of(tl, tv, a.tot, b * H + h0, hn, NCH, 0, c, lane, tid);
     if (lane) scan_lane(sm.x[tid], carry);
     __syncthreads();
     // g, F, rowf, colf: (B,H,L) rows, one (head, row) per thread, coalesced along L
@@ -259,6 +324,7 @@ __host__ __device__ inline int64_t bt_bytes(int B, int L, int H) {
 template <class T>
 __global__ __launch_bounds__(NT) void prep_bsums_kernel(sisa_prep_bwd_args a) {
     __shared__ ScanLds sm;
+    __shared__ TotLds<float> tl;
     const int c = blockIdx.x, b = blockIdx.y, h0 = blockIdx.z * HG;
     const int H = a.H, L = a.L, NCH = gridDim.x;
     const int hn = (H - h0 < HG) ? H - h0 : HG;
@@ -266,6 +332,20 @@ __global__ __launch_bounds__(NT) void prep_bsums_kernel(sisa_prep_bwd_args a) {
     const Layout off = layout_of(H);
     const int tid = threadIdx.x;
     const T* P = (const T*)a.proj + (int64_t)b * a.s_pb + (int64_t)c * CH * a.s_pl;
+    // Every global load is issued before the first wait, in the order of use: theta, dg and dF, the forward totals
+    // of the preceding chunks, then the C, B, dC~ and dB~ vectors of this thread.
+    const StageVals<T> sv = stage_load<T, false>(P, a.s_pl, nullptr, 0, nrows, hn, off, h0, tid);
+    float dgv = 0.f, dfv = 0.f;   // dg and dF of (head tid>>6, row tid&63)
+    if (tid < CH * HG) {
+        const int hh = tid >> 6, r = tid & 63;
+        const bool ok = hh < hn && r < nrows;
+        const int64_t o = (int64_t)(b * H + h0 + hh) * L + c * CH + r;
+        if (ok) dgv = a.dg[o];
+        if (ok && a.df) dfv = a.df[o];
+    }
+    const bool lane = tid < HC && tid / NCOMP < hn && tid % NCOMP >= 2;   // Phi lanes (components 2..17)
+    float tv[TPT];
+    tot_load(tv, a.tot, b * H + h0, hn, NCH, 0, c < TB ? c : TB, tid);
     frag8<T> cv[NU], bv[NU];
     f32x4 dc[NU][2], db[NU][2];
 #pragma unroll
@@ -282,22 +362,15 @@ __global__ __launch_bounds__(NT) void prep_bsums_kernel(sisa_prep_bwd_args a) {
             db[i][k] = ok ? *reinterpret_cast<const f32x4*>(a.dbr + o + 4 * k) : zero4();
         }
     }
-    // dg and dF of the chunk into components 0 and 1 (one (head, row) per thread)
+    stage_store<T, false>(sm, sv, nrows, hn, false, tid);
     if (tid < CH * HG) {
         const int hh = tid >> 6, r = tid & 63;
-        const bool ok = hh < hn && r < nrows;
-        const int64_t o = (int64_t)(b * H + h0 + hh) * L + c * CH + r;
-        const float dgv = ok ? a.dg[o] : 0.f;
-        const float dfv = (ok && a.df) ? a.df[o] : 0.f;
         sm.x[(hh & 3) * NCOMP + 0][r] = dgv;
         sm.x[(hh & 3) * NCOMP + 1][r] = dfv;
     }
-    const bool lane = tid < HC && tid / NCOMP < hn && tid % NCOMP >= 2;   // Phi lanes (components 2..17)
-    const float carry =
-        lane ? fold_totals<float>(a.tot + ((int64_t)(b * H + h0 + tid / NCOMP) * NCH) * NCOMP + tid % NCOMP, 0, c, 0.f)
-             : 0.f;
-    stage_theta<T>(sm, P, a.s_pl, nrows, hn, off, h0, tid);
+    tot_store(tl, tv, tid);
     __syncthreads();
+    const float carry = carry_of(tl, tv, a.tot, b * H + h0, hn, NCH, 0, c, lane, tid);
     if (lane) scan_lane(sm.x[tid], carry);   // Phi: the forward scan of theta
     __syncthreads();
     T* DP = (T*)a.dproj + (int64_t)b * a.s_db + (int64_t)c * CH * a.s_dl;
@@ -355,11 +428,12 @@ __global__ __launch_bounds__(NT) void prep_bsums_kernel(sisa_prep_bwd_args a) {
 }
 
 // Pass 2: reverse scans (fp64 carry of the following chunks + in-chunk reverse sums) into d alpha, dz, d theta; pad
-// columns set to zero.
+// columns set to zero. d alpha = -suffix * softplus'(alpha) and dz = suffix * logsigmoid'(z) are formed by the
+// threads that loaded alpha and z, when they write them.
 template <class T>
 __global__ __launch_bounds__(NT) void prep_bwd_kernel(sisa_prep_bwd_args a) {
     __shared__ ScanLds sm;
-    __shared__ float dal[CH][HG], dzz[CH][HG];   // softplus'(alpha), logsigmoid'(z)
+    __shared__ TotLds<double> tl;
     const int c = blockIdx.x, b = blockIdx.y, h0 = blockIdx.z * HG;
     const int H = a.H, L = a.L, NCH = gridDim.x;
     const int hn = (H - h0 < HG) ? H - h0 : HG;
@@ -368,39 +442,51 @@ __global__ __launch_bounds__(NT) void prep_bwd_kernel(sisa_prep_bwd_args a) {
     const int tid = threadIdx.x;
     const T* P = (const T*)a.proj + (int64_t)b * a.s_pb + (int64_t)c * CH * a.s_pl;
     const float* DPHI = (const float*)((const char*)a.workspace + bt_bytes(a.B, L, H));
-    // dPhi rows (written by pass 1): one (row, head, 4 pairs) vector per thread and iteration
+    const double* BT = (const double*)a.workspace;
+    // Every global load is issued before the first wait: dPhi rows (written by pass 1; one (row, head, 4 pairs)
+    // vector per thread and iteration), dg and dF, alpha and z, and the fp64 totals of the following chunks.
+    f32x4 dph[NU];
 #pragma unroll
     for (int i = 0; i < NU; ++i) {
         const Unit u = cb_unit(tid + NT * i);
         const bool ok = u.row < nrows && u.hl < hn;
         const int64_t o = (((int64_t)b * L + c * CH + u.row) * H + h0 + u.hl) * S2 + 4 * u.q;
-        const f32x4 d = ok ? *reinterpret_cast<const f32x4*>(DPHI + o) : zero4();
+        dph[i] = ok ? *reinterpret_cast<const f32x4*>(DPHI + o) : zero4();
+    }
+    float dgv = 0.f, dfv = 0.f, al = 0.f, zv = 0.f;
+    if (tid < CH * HG) {
+        const int hh = tid >> 6, r = tid & 63;   // dg, dF of (head hh, row r): coalesced along L
+        if (hh < hn && r < nrows) {
+            const int64_t o = (int64_t)(b * H + h0 + hh) * L + c * CH + r;
+            dgv = a.dg[o];
+            if (a.df) dfv = a.df[o];
+        }
+        const int row = tid >> 2, hl = tid & 3;   // alpha, z of (row, head hl): contiguous in the row
+        if (row < nrows && hl < hn) {
+            al = (float)P[(int64_t)row * a.s_pl + off.A + h0 + hl];
+            if (a.z) zv = a.z[(int64_t)b * a.s_zb + (int64_t)(c * CH + row) * a.s_zl + h0 + hl];
+        }
+    }
+    // fp64 totals of the following chunks (carries of the reverse scans)
+    const int c0 = c + 1;
+    double tv[TPT];
+    tot_load(tv, BT, b * H + h0, hn, NCH, c0, (NCH - c0 < TB) ? NCH : c0 + TB, tid);
 #pragma unroll
-        for (int p = 0; p < 4; ++p) sm.x[u.hl * NCOMP + 2 + 4 * u.q + p][u.row] = d[p];
+    for (int i = 0; i < NU; ++i) {
+        const Unit u = cb_unit(tid + NT * i);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) sm.x[u.hl * NCOMP + 2 + 4 * u.q + p][u.row] = dph[i][p];
     }
     if (tid < CH * HG) {
         const int hh = tid >> 6, r = tid & 63;
-        const bool ok = hh < hn && r < nrows;
-        const int64_t o = (int64_t)(b * H + h0 + hh) * L + c * CH + r;
-        sm.x[(hh & 3) * NCOMP + 0][r] = ok ? a.dg[o] : 0.f;
-        sm.x[(hh & 3) * NCOMP + 1][r] = (ok && a.df) ? a.df[o] : 0.f;
+        sm.x[hh * NCOMP + 0][r] = dgv;
+        sm.x[hh * NCOMP + 1][r] = dfv;
     }
-    if (tid < CH * HG) {
-        const int row = tid >> 2, hl = tid & 3;
-        const bool ok = row < nrows && hl < hn;
-        const float al = ok ? (float)P[(int64_t)row * a.s_pl + off.A + h0 + hl] : 0.f;
-        const float zv = (ok && a.z) ? a.z[(int64_t)b * a.s_zb + (int64_t)(c * CH + row) * a.s_zl + h0 + hl] : 0.f;
-        dal[row][hl] = softplus_grad(al);
-        dzz[row][hl] = logsigmoid_grad(zv);
-    }
+    tot_store(tl, tv, tid);
     const bool lane = tid < HC && tid / NCOMP < hn;
-    const double sa =
-        lane ? fold_totals<double>((const double*)a.workspace + ((int64_t)(b * H + h0 + tid / NCOMP) * NCH) * NCOMP +
-                                       tid % NCOMP, c + 1, NCH, 0.0)
-             : 0.0;
     __syncthreads();
+    const double sa = carry_of(tl, tv, BT, b * H + h0, hn, NCH, c0, NCH, lane, tid);
     if (lane) {
-        const int hl = tid / NCOMP, comp = tid % NCOMP;
         float* x = sm.x[tid];
         float v[CH];
 #pragma unroll
@@ -409,8 +495,7 @@ __global__ __launch_bounds__(NT) void prep_bwd_kernel(sisa_prep_bwd_args a) {
 #pragma unroll
         for (int r = CH - 1; r >= 0; --r) {
             rev += (double)v[r];
-            const float tot = (float)(sa + rev);
-            x[r] = comp == 0 ? -tot * dal[r][hl] : (comp == 1 ? tot * dzz[r][hl] : tot);
+            x[r] = (float)(sa + rev);   // the suffix sum; d alpha and dz take their element derivative below
         }
     }
     __syncthreads();
@@ -433,8 +518,10 @@ __global__ __launch_bounds__(NT) void prep_bwd_kernel(sisa_prep_bwd_args a) {
     if (tid < CH * HG) {
         const int row = tid >> 2, hl = tid & 3;
         if (row < nrows && hl < hn) {
-            DP[(int64_t)row * a.s_dl + off.A + h0 + hl] = cvt<T>(sm.x[hl * NCOMP + 0][row]);
-            if (a.dz) a.dz[(int64_t)b * a.s_dzb + (int64_t)(c * CH + row) * a.s_dzl + h0 + hl] = sm.x[hl * NCOMP + 1][row];
+            DP[(int64_t)row * a.s_dl + off.A + h0 + hl] = cvt<T>(-sm.x[hl * NCOMP + 0][row] * softplus_grad(al));
+            if (a.dz)
+                a.dz[(int64_t)b * a.s_dzb + (int64_t)(c * CH + row) * a.s_dzl + h0 + hl] =
+                    sm.x[hl * NCOMP + 1][row] * logsigmoid_grad(zv);
         }
     }
     // zero padding columns (they multiply the zero rows of W_cat; keeps NaN out of dX)

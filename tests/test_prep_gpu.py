@@ -34,7 +34,8 @@ def torch_glue(proj, z, H):
 
 @pytest.mark.parametrize("B,L,H,seed,hasf,kw", [
     (2, 2048, 8, 1, True, {}), (1, 300, 12, 2, True, {}), (1, 1, 8, 3, True, {}), (1, 129, 8, 4, False, {}),
-    (1, 2048, 8, 6, True, dict(alpha_mu=-8.0, alpha_sd=0.5)), (1, 1000, 16, 7, True, {}), (1, 65, 5, 8, True, {})])
+    (1, 2048, 8, 6, True, dict(alpha_mu=-8.0, alpha_sd=0.5)), (1, 1000, 16, 7, True, {}), (1, 65, 5, 8, True, {}),
+    (1, 8300, 6, 9, True, {})])
 def test_prep_accuracy(B, L, H, seed, hasf, kw):
     from sisa_amd.kernels import attention as A
     proj, z, off = R.make_proj(B, L, H, seed, device=DEV, **kw)
@@ -93,7 +94,7 @@ def run_glue_hip(proj, z, lam, H, dy):
 
 
 @pytest.mark.parametrize("B,L,H,seed,hasf", [(1, 300, 4, 11, True), (1, 1024, 8, 12, True), (1, 129, 4, 13, False),
-                                              (1, 1, 4, 14, True), (2, 700, 4, 15, True)])
+                                              (1, 1, 4, 14, True), (2, 700, 4, 15, True), (1, 4200, 4, 16, True)])
 def test_fused_gradients_vs_fp64(B, L, H, seed, hasf):
     print(f"[fused] B={B} L={L} H={H} seed={seed} hasf={hasf}", flush=True)
     proj, z, off = R.make_proj(B, L, H, seed, device=DEV)
