@@ -13,7 +13,11 @@ Reported (one JSON line on rank 0):
              bwd 832 P) / step time. tokens_per_s = B*T / step time.
   roofline   the attention kernels (forward + backward launches, the dominant work) against the bf16 dense MFMA
              peak: achieved = 1152 P / (their summed average duration, HIP events on the launch stream).
-  roofline_prep  the prep forward against HBM peak: algorithmic bytes / its average duration.
+  roofline_prep  the prep forward (its two launches, queued behind a GPU spin so that host work is not timed)
+             against HBM peak: algorithmic bytes / their average duration; beside it a plain device copy moving the
+             same number of bytes (half read, half written), timed the same way, as the ceiling HBM offers to a
+             transfer of this size (copy_same_bytes_gbs, frac_of_copy); the prep backward likewise (backward).
+             phases_ms are the step's own event phases, host gaps included.
   lmce       the linear cross-entropy at config 3 (N=16384, d=768, V=50277): step time, TFLOP/s of its three GEMMs
              (6 N V d), hipBLASLt GEMM roofline and the HIP row pass against HBM peak.
   model_step the full decoder training step at config 4 (sisa-152m, B=8, T=2048, bf16 autocast, fused attention,
@@ -76,6 +80,78 @@ def parse():
     p.add_argument("--copy-mib", type=int, default=0,
                    help="run one plain device copy of this many MiB first (calibrates HBM byte counters)")
     return p.parse_args()
+
+
+def queued_seconds(launch, reps: int = 20) -> float:
+    """Average seconds per call of ``launch()`` (one or more back-to-back GPU launches), the calls queued behind a GPU
+    spin so that host work between them is not timed: HIP events around the reps on the launch stream."""
+    import torch
+
+    launch()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with _quiet_host():
+        torch.cuda._sleep(20_000_000)      # the GPU spins while the host queues the timed launches
+        e0.record()
+        for _ in range(reps):
+            launch()
+        e1.record()
+        torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps * 1e-3
+
+
+def prep_kernel_rates(proj, z, H: int) -> dict:
+    """The prep forward (prep_sums + prep_fwd) and backward (prep_bsums + prep_bwd) launches through the C-ABI with
+    prepared arguments, timed by queued_seconds, against HBM peak; beside them a plain device copy moving the same
+    number of bytes (half read, half written) as the ceiling HBM offers to a transfer of that size."""
+    import ctypes
+    import torch
+    from sisa_amd.kernels import _lib
+    from sisa_amd.kernels import fused_prep as FP
+
+    B, L, _ = proj.shape
+    dev = proj.device
+    lib = _lib.load()
+    st = _lib.stream_of(proj)
+    pf = FP._launch_prep_forward(proj, z, H)
+    fa = _lib.PrepFwdArgs(B, L, H, _lib.dtype_code(proj.dtype), proj.data_ptr(), proj.stride(0), proj.stride(1),
+                          _lib.ptr(z), z.stride(0), z.stride(1), pf["CR"].data_ptr(), pf["BR"].data_ptr(),
+                          pf["G"].data_ptr(), _lib.ptr(pf["F"]), pf["ROWF"].data_ptr(), pf["COLF"].data_ptr(),
+                          pf["TOT"].data_ptr())
+    gen = torch.Generator().manual_seed(9)
+    dg, dF = (torch.randn(B, H, L, generator=gen).to(dev) for _ in range(2))
+    DCR, DBR = (torch.randn(B, L, H, 32, generator=gen).to(dev) for _ in range(2))
+    DP = torch.zeros_like(proj)
+    DZ = torch.empty(B, L, H, device=dev)
+    ws = torch.empty((_lib.workspace_bytes("sisa_prep_bwd_workspace_bytes", B, L, H),), device=dev, dtype=torch.uint8)
+    ba = _lib.PrepBwdArgs(B, L, H, _lib.dtype_code(proj.dtype), proj.data_ptr(), proj.stride(0), proj.stride(1),
+                          _lib.ptr(z), z.stride(0), z.stride(1), pf["TOT"].data_ptr(), dg.data_ptr(), dF.data_ptr(),
+                          DCR.data_ptr(), DBR.data_ptr(), DP.data_ptr(), DP.stride(0), DP.stride(1), DZ.data_ptr(),
+                          DZ.stride(0), DZ.stride(1), ws.data_ptr())
+
+    def call(name, args):
+        def go():
+            if getattr(lib, name)(ctypes.byref(args), st) != 0:
+                raise RuntimeError(f"{name}: {lib.sisa_last_error().decode()}")
+        return go
+
+    th = B * L * H
+    # backward per (token, head): read C, B (2*32 * 2 B), theta (16 * 2 B), dC~, dB~ (2*32 * 4 B), dg, dF (4 B each),
+    # alpha (2 B), z (4 B); write dC, dB (2*32 * 2 B), dtheta (16 * 2 B), dalpha (2 B), dz (4 B): 596 B
+    sizes = {"prep_fwd": FP.prep_bytes(B, L, H)["total"], "prep_bwd": th * 596}
+    out = {}
+    for key, fn in (("prep_fwd", call("sisa_prep_fwd", fa)), ("prep_bwd", call("sisa_prep_bwd", ba))):
+        nbytes = sizes[key]
+        sec = queued_seconds(fn)
+        n = nbytes // 2 // 16 * 4                      # fp32 elements of a copy moving nbytes in total
+        src = torch.ones(n, device=dev)
+        dst = torch.empty_like(src)
+        csec = queued_seconds(lambda: dst.copy_(src))
+        gbs, cgbs = nbytes / sec / 1e9, 2 * n * 4 / csec / 1e9
+        out[key] = {"us": round(sec * 1e6, 2), "bytes": int(nbytes), "achieved": round(gbs, 1),
+                    "frac": round(gbs / PEAK_HBM_GBS, 4), "copy_same_bytes_gbs": round(cgbs, 1),
+                    "frac_of_copy": round(gbs / cgbs, 4)}
+    return out
 
 
 def bench_ce(steps: int, warmup: int) -> dict:
@@ -468,7 +544,8 @@ def main():
     attn_ms = phases["attn_fwd"] + phases["attn_bwd"]
     achieved = total_flop / (attn_ms * 1e-3) / 1e12
     pb = FP.prep_bytes(B, L, H)
-    prep_gbs = pb["total"] / (phases["prep_fwd"] * 1e-3) / 1e9
+    prk = prep_kernel_rates(proj, z, H)
+    prep_gbs = prk["prep_fwd"]["achieved"]
     out = {
         "metric": "SISA attn fwd+bwd TFLOP/s & tokens/s, bf16 T=4096 1xMI355X; MFMA util %",
         "value": round(value, 3),
@@ -496,7 +573,11 @@ def main():
         "roofline_prep": {"bound": "hbm", "achieved": round(prep_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": round(prep_gbs / PEAK_HBM_GBS, 4),
                           "traffic": TRAFFIC_PREP_FWD_NS if cfg == "ns" else None,
-                          "algorithmic": f"{pb['total'] / 1e6:.1f} MB per prep forward (310 B per token-head)"},
+                          "algorithmic": f"{pb['total'] / 1e6:.1f} MB per prep forward (310 B per token-head)",
+                          "kernels": "prep_sums + prep_fwd, queued behind a GPU spin (HIP events)",
+                          "copy_same_bytes_gbs": prk["prep_fwd"]["copy_same_bytes_gbs"],
+                          "frac_of_copy": prk["prep_fwd"]["frac_of_copy"],
+                          "backward": prk["prep_bwd"]},
     }
     if not args.no_ce:
         out["lmce"] = bench_ce(max(3, args.steps // 2), 2)
