@@ -35,7 +35,7 @@ def torch_glue(proj, z, H):
 @pytest.mark.parametrize("B,L,H,seed,hasf,kw", [
     (2, 2048, 8, 1, True, {}), (1, 300, 12, 2, True, {}), (1, 1, 8, 3, True, {}), (1, 129, 8, 4, False, {}),
     (1, 2048, 8, 6, True, dict(alpha_mu=-8.0, alpha_sd=0.5)), (1, 1000, 16, 7, True, {}), (1, 65, 5, 8, True, {}),
-    (1, 8300, 6, 9, True, {})])
+    (1, 8300, 6, 9, True, {}), (1, 16384, 16, 10, True, dict(alpha_mu=-7.0, alpha_sd=1.0))])
 def test_prep_accuracy(B, L, H, seed, hasf, kw):
     from sisa_amd.kernels import attention as A
     proj, z, off = R.make_proj(B, L, H, seed, device=DEV, **kw)
