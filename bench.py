@@ -272,7 +272,7 @@ def bench_model(steps: int, warmup: int) -> dict:
     return {"workload": "full decoder training step (config 4): sisa-152m, B=8, T=2048, bf16 autocast, hip_fused "
                         "attention + HIP RMSNorm/SwiGLU + fused linear CE + AdamW", "B": B, "T": T,
             "params": model.num_parameters(), "steps": steps, "ms_per_step": round(ms, 3),
-            "tokens_per_s": round(B * T / (ms * 1e-3), 1), "loss": round(float(loss), 4), "tuned_gemms": tuned}
+            "tokens_per_s": round(B * T / (ms * 1e-3), 1), "loss": round(float(loss.detach()), 4), "tuned_gemms": tuned}
 
 
 def bench_block_kernels(reps: int = 20) -> dict:

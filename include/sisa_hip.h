@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SISA_ABI_VERSION 1
+#define SISA_ABI_VERSION 2
 
 enum sisa_dtype { SISA_F32 = 0, SISA_BF16 = 1, SISA_F16 = 2, SISA_F64 = 3 };
 
@@ -219,7 +219,11 @@ int sisa_rmsnorm_bwd(const sisa_rmsnorm_args* a, void* stream);
  *             u = x * rstd, du = dn * w; dw = sum_rows dn * u; dW_f = dz^T n; db_f = sum_rows dz
  * Replaces RMSNorm.forward, the autocast cast of its output, `_forget_logits` and their autograd. H = 0 is a plain
  * RMSNorm with an output dtype of its own. Weight gradients are reduced deterministically through the workspace
- * (sisa_norm_bwd_workspace_bytes). */
+ * (sisa_norm_bwd_workspace_bytes).
+ * Residual (optional, replaces the residual add before the norm, `x = x + sublayer(...)`, modeling.py:288-291):
+ *   forward with res:  h = round_x(x + res) is written to h and normalised in place of x;
+ *   backward with dh:  dx = round_x(dx_norm) + dh, the gradient of h summed over its two consumers (the norm and
+ *   the residual stream), as autograd sums them; x is then the h of the forward. */
 typedef struct {
     int64_t N;                 /* rows */
     int32_t D;                 /* row length, multiple of 8, <= 4096 */
@@ -242,6 +246,9 @@ typedef struct {
     float* dwf;                        /* backward: (H, D) */
     float* dbf;                        /* backward: (H) */
     float* workspace;                  /* backward scratch, 16-byte aligned */
+    const void* res; int64_t sres;     /* forward: residual (N, D) in ydtype, or NULL */
+    void* h; int64_t sh;               /* forward: x + res (N, D) in xdtype; required with res */
+    const void* dh; int64_t sdh;       /* backward: (N, D) gradient of h from the residual stream, xdtype, or NULL */
 } sisa_norm_args;
 
 int64_t sisa_norm_bwd_workspace_bytes(int64_t N, int32_t D, int32_t H);

@@ -105,6 +105,22 @@ __global__ __launch_bounds__(64 * NORM_WAVES) void norm_fwd_kernel(sisa_norm_arg
             }
         }
     }
+    if (a.res) {   // h = x + res, rounded to x's dtype as the residual add, normalised in place of x
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int64_t row = r0 + r;
+#pragma unroll
+            for (int i = 0; i < NVL; ++i) {
+                const int c = lane + 64 * i;
+                if (row < a.N && c < nv) {
+                    const f32x8 rv = load_f32x8<TY>((const TY*)a.res + row * a.sres + 8 * c);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) n[r][i][e] = rnd<TX>(n[r][i][e] + rv[e]);
+                    store_f32x8<TX>((TX*)a.h + row * a.sh + 8 * c, n[r][i]);
+                }
+            }
+        }
+    }
     const float* wf = a.H > 0 ? stage_wf<HP>(a, wlds) : nullptr;
     if (r0 >= a.N) return;
     float rstd[RB];
@@ -275,6 +291,11 @@ __global__ __launch_bounds__(64 * NORM_WAVES) void norm_bwd_kernel(sisa_norm_arg
                         f32x8 o;
 #pragma unroll
                         for (int e = 0; e < 8; ++e) o[e] = rstd[r] * (dn[r][i][e] - u[r][i][e] * mdot);
+                        if (a.dh) {   // plus the residual stream's gradient of h, summed in x's dtype
+                            const f32x8 hv = load_f32x8<TX>((const TX*)a.dh + row * a.sdh + 8 * c);
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) o[e] = rnd<TX>(o[e]) + hv[e];
+                        }
                         store_f32x8<TX>((TX*)a.dx + row * a.sdx + 8 * c, o);
                     }
                 }
@@ -497,7 +518,11 @@ int check_norm(const sisa_norm_args* a, int bwd, const char* fn) {
     if (!bwd) {
         SISA_REQUIRE(rows_ok(a->y, a->sy, a->D, y), "%s: bad y (16-byte aligned rows, stride >= D)", fn);
         SISA_REQUIRE(a->H == 0 || a->z, "%s: a projection (H > 0) needs z", fn);
+        SISA_REQUIRE(a->res == nullptr || (rows_ok(a->res, a->sres, a->D, y) && rows_ok(a->h, a->sh, a->D, x)),
+                     "%s: a residual needs res (ydtype) and h (xdtype) with 16-byte aligned rows, stride >= D", fn);
     } else {
+        SISA_REQUIRE(a->dh == nullptr || rows_ok(a->dh, a->sdh, a->D, x),
+                     "%s: dh must have 16-byte aligned rows (xdtype, stride >= D)", fn);
         SISA_REQUIRE(rows_ok(a->dy, a->sdy, a->D, y) && rows_ok(a->dx, a->sdx, a->D, x) && a->rstd && a->dw &&
                          a->workspace && sisa::aligned16(a->workspace),
                      "%s: dy/dx (16-byte aligned rows), rstd, dw and a 16-byte aligned workspace must be given", fn);

@@ -15,7 +15,7 @@ from ctypes import POINTER, Structure, c_char_p, c_float, c_int, c_int32, c_int6
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "libsisa_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F32, BF16, F16, F64 = 0, 1, 2, 3
 _DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.float64: F64}
@@ -81,7 +81,9 @@ class NormArgs(Structure):
                 ("eps", c_float), ("reserved", c_int32), ("x", c_void_p), ("sx", c_int64), ("w", c_void_p),
                 ("wf", c_void_p), ("bf", c_void_p), ("y", c_void_p), ("sy", c_int64), ("rstd", c_void_p),
                 ("z", c_void_p), ("dy", c_void_p), ("sdy", c_int64), ("dz", c_void_p), ("dx", c_void_p),
-                ("sdx", c_int64), ("dw", c_void_p), ("dwf", c_void_p), ("dbf", c_void_p), ("workspace", c_void_p)]
+                ("sdx", c_int64), ("dw", c_void_p), ("dwf", c_void_p), ("dbf", c_void_p), ("workspace", c_void_p),
+                ("res", c_void_p), ("sres", c_int64), ("h", c_void_p), ("sh", c_int64), ("dh", c_void_p),
+                ("sdh", c_int64)]
 
 
 class SwigluArgs(Structure):

@@ -11,7 +11,8 @@ from torch import Tensor
 
 from . import _lib
 
-__all__ = ["rms_norm_hip", "rms_norm_forget_hip", "swiglu_hip", "swiglu_pairs_hip", "interleave_gate_up"]
+__all__ = ["rms_norm_hip", "rms_norm_add_hip", "rms_norm_forget_hip", "swiglu_hip", "swiglu_pairs_hip",
+           "interleave_gate_up"]
 
 
 def _rows(x: Tensor) -> Tensor:
@@ -81,6 +82,50 @@ class _NormFn(torch.autograd.Function):
         return dx.view(ctx.shape), dw.to(ctx.wdtype), dwf_out, dbf_out, None, None
 
 
+class _AddNormFn(torch.autograd.Function):
+    """The residual add and the RMSNorm that follows it in one pass: ``h = x + res`` (in ``x``'s dtype) and
+    ``y = RMSNorm(h)`` in ``out_dtype`` -- one ``sisa_norm_fwd`` launch. The backward sums the gradient of ``h`` from
+    the residual stream into the norm's dx inside the ``sisa_norm_bwd`` row pass; ``res`` receives that sum in its
+    own dtype, as autograd gives it to the operand of the add."""
+
+    @staticmethod
+    def forward(ctx, x: Tensor, res: Tensor, weight: Tensor, eps: float, out_dtype: torch.dtype):
+        x2, r2 = _rows(x), _rows(res)
+        w = weight.detach().float().contiguous()
+        N, D = x2.shape
+        h = torch.empty((N, D), device=x.device, dtype=x.dtype)
+        y = torch.empty((N, D), device=x.device, dtype=out_dtype)
+        rstd = torch.empty(N, device=x.device, dtype=torch.float32)
+        args = _lib.NormArgs(N, D, 0, _lib.dtype_code(x.dtype), _lib.dtype_code(out_dtype), float(eps), 0,
+                             x2.data_ptr(), x2.stride(0), w.data_ptr(), None, None, y.data_ptr(), y.stride(0),
+                             rstd.data_ptr(), None, None, 0, None, None, 0, None, None, None, None,
+                             r2.data_ptr(), r2.stride(0), h.data_ptr(), h.stride(0))
+        _lib.call("sisa_norm_fwd", args, x)
+        ctx.save_for_backward(h, w, rstd)
+        ctx.eps, ctx.shape, ctx.wdtype, ctx.out_dtype, ctx.rdtype = eps, x.shape, weight.dtype, out_dtype, res.dtype
+        return h.view(x.shape), y.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dh: Tensor | None, dy: Tensor | None):
+        h2, w, rstd = ctx.saved_tensors
+        N, D = h2.shape
+        if dy is None:
+            dy = torch.zeros((N, D), device=h2.device, dtype=ctx.out_dtype)
+        dy2 = _rows(dy.to(ctx.out_dtype))
+        dh2 = None if dh is None else _rows(dh.to(h2.dtype))
+        dx = torch.empty((N, D), device=h2.device, dtype=h2.dtype)
+        dw = torch.empty(D, device=h2.device, dtype=torch.float32)
+        ws = torch.empty(_lib.workspace_bytes("sisa_norm_bwd_workspace_bytes", N, D, 0) // 4, device=h2.device,
+                         dtype=torch.float32)
+        args = _lib.NormArgs(N, D, 0, _lib.dtype_code(h2.dtype), _lib.dtype_code(ctx.out_dtype), float(ctx.eps), 0,
+                             h2.data_ptr(), h2.stride(0), w.data_ptr(), None, None, None, 0, rstd.data_ptr(), None,
+                             dy2.data_ptr(), dy2.stride(0), None, dx.data_ptr(), dx.stride(0), dw.data_ptr(), None,
+                             None, ws.data_ptr(), None, 0, None, 0, _lib.ptr(dh2), 0 if dh2 is None else dh2.stride(0))
+        _lib.call("sisa_norm_bwd", args, h2)
+        dx = dx.view(ctx.shape)
+        return dx, dx.to(ctx.rdtype), dw.to(ctx.wdtype), None, None
+
+
 def _check_norm(x: Tensor, out_dtype: torch.dtype, H: int) -> None:
     if x.dtype not in (torch.float32, *_HALF):
         raise TypeError(f"rms_norm_hip: unsupported dtype {x.dtype}")
@@ -100,6 +145,20 @@ def rms_norm_hip(x: Tensor, weight: Tensor, eps: float, out_dtype: torch.dtype |
     out_dtype = out_dtype or x.dtype
     _check_norm(x, out_dtype, 0)
     return _NormFn.apply(x, weight, None, None, eps, out_dtype)
+
+
+def rms_norm_add_hip(x: Tensor, res: Tensor, weight: Tensor, eps: float,
+                     out_dtype: torch.dtype | None = None) -> tuple[Tensor, Tensor]:
+    """``h = x + res`` followed by :func:`rms_norm_hip` of ``h``, in one kernel pass each way: the residual add of a
+    pre-norm block and the next sublayer's norm (src/sisa/modeling.py:288-291). ``res`` must have ``out_dtype``
+    (the consuming GEMM's autocast dtype, as the sublayer outputs under autocast) and ``x``'s shape; ``h`` is in
+    ``x.dtype``, rounded once as ``x + res`` is. Returns ``(h, y)``."""
+    out_dtype = out_dtype or x.dtype
+    _check_norm(x, out_dtype, 0)
+    if res.shape != x.shape or res.dtype != out_dtype:
+        raise ValueError(f"rms_norm_add_hip: residual {tuple(res.shape)} {res.dtype} must match x {tuple(x.shape)} "
+                         f"and have the output dtype {out_dtype}")
+    return _AddNormFn.apply(x, res, weight, eps, out_dtype)
 
 
 def rms_norm_forget_hip(x: Tensor, weight: Tensor, eps: float, wf: Tensor, bf: Tensor,

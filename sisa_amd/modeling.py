@@ -327,16 +327,20 @@ class SISABlock(nn.Module):
     def _forward_hip(self, x: Tensor) -> Tensor:
         """The block on the HIP kernels: the attention norm and the fp32 forget-gate projection in one pass that
         also emits the normalised rows in the dtype of the projection GEMM (the reference casts them under autocast),
-        the fused attention sublayer, the FFN norm likewise, SwiGLU."""
-        from .kernels.norm import rms_norm_forget_hip, rms_norm_hip
+        the fused attention sublayer, the residual add and the FFN norm in one pass, SwiGLU."""
+        from .kernels.norm import rms_norm_add_hip, rms_norm_forget_hip, rms_norm_hip
 
         cd = _compute_dtype(x)
         out_dtype = cd if x.dtype == torch.float32 else x.dtype
         at = self.attn
         n, z = rms_norm_forget_hip(x, self.attn_norm.weight, self.attn_norm.eps, at.forget_proj.weight,
                                    at.forget_proj.bias, out_dtype)
-        x = x + at._forward_fused(n, z)
-        m = rms_norm_hip(x, self.ffn_norm.weight, self.ffn_norm.eps, out_dtype)
+        a = at._forward_fused(n, z)
+        if a.dtype == out_dtype and a.shape == x.shape:   # residual add fused into the FFN norm
+            x, m = rms_norm_add_hip(x, a, self.ffn_norm.weight, self.ffn_norm.eps, out_dtype)
+        else:
+            x = x + a
+            m = rms_norm_hip(x, self.ffn_norm.weight, self.ffn_norm.eps, out_dtype)
         return x + self.ffn(m)
 
     def forward(self, x: Tensor, cache: "SISACache | None" = None) -> Tensor:

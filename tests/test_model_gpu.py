@@ -43,6 +43,34 @@ def test_rmsnorm_kernel(dtype, N, D):
     assert torch.equal(again[0], dx) and torch.equal(again[1], dw)     # deterministic
 
 
+@pytest.mark.parametrize("xd,yd,N,D", [(torch.float32, torch.bfloat16, 300, 768), (torch.bfloat16, torch.bfloat16, 70, 512),
+                                      (torch.float32, torch.float32, 33, 1536), (torch.float16, torch.float16, 5, 200)])
+def test_add_norm_kernel(xd, yd, N, D):
+    """Residual add fused into the RMSNorm (h = x + res, y = RMSNorm(h)) against the unfused ops it replaces
+    (torch's add, then the norm kernel), bitwise: h, y, and the gradients of x, res and w when h also feeds the
+    residual stream (its gradient arrives both from the norm and from the stream, as in the decoder block)."""
+    from sisa_amd.kernels.norm import rms_norm_add_hip, rms_norm_hip
+    gen = torch.Generator().manual_seed(N + D)
+    x0 = (2 * torch.randn(N, D, generator=gen)).to(xd).to(DEV)
+    r0 = torch.randn(N, D, generator=gen).to(yd).to(DEV)
+    w0 = (1 + 0.1 * torch.randn(D, generator=gen)).to(DEV)
+    dy = torch.randn(N, D, generator=gen).to(yd).to(DEV)
+    dh = torch.randn(N, D, generator=gen).to(xd).to(DEV)
+    res = {}
+    for fused in (True, False):
+        x, r, w = (t.clone().requires_grad_(True) for t in (x0, r0, w0))
+        if fused:
+            h, y = rms_norm_add_hip(x, r, w, 1e-6, yd)
+        else:
+            h = x + r
+            y = rms_norm_hip(h, w, 1e-6, yd)
+        grads = torch.autograd.grad((h, y), (x, r, w), (dh, dy))
+        res[fused] = (h.detach(), y.detach(), *grads)
+    names = ("h", "y", "dx", "dres", "dw")
+    for n, a, b in zip(names, res[True], res[False]):
+        assert a.dtype == b.dtype and torch.equal(a, b), f"{n} differs from the unfused add + norm"
+
+
 @pytest.mark.parametrize("xd,yd,N,D,H", [(torch.float32, torch.bfloat16, 1000, 768, 12),
                                          (torch.float32, torch.float32, 257, 128, 2),
                                          (torch.float32, torch.float16, 33, 1024, 16),
