@@ -64,15 +64,54 @@ SISA_DEV float col_value(const frag8<T>& v, int j, int nreal) {
 // columns of the vector at col that lie inside the real vocabulary, in [0, 8]
 SISA_DEV int real_cols(int col, int V) { return min(max(V - col, 0), 8); }
 
+// Vectors wholly inside the real vocabulary (every one but the last of a row) take the branch-free forms below; the
+// masked forms differ only in the columns they exclude, so both give the same value for a full vector.
+
+// running maximum over a vector (fmaxf: a NaN logit still makes the row NaN, through its exponential in the sum)
+template <class T>
+SISA_DEV float vec_max(const frag8<T>& v, int col, int V, float m) {
+    if (col + 8 <= V) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) m = fmaxf(m, (float)v[j]);
+    } else {
+        const int nreal = real_cols(col, V);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) m = fmaxf(m, col_value<T>(v, j, nreal));
+    }
+    return m;
+}
+
+// running sum of exp(x - M) over a vector, in column order
+template <class T>
+SISA_DEV float vec_sumexp(const frag8<T>& v, int col, int V, float m2, float s) {
+    if (col + 8 <= V) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += fast_exp2((float)v[j] * LOG2E - m2);
+    } else {
+        const int nreal = real_cols(col, V);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += fast_exp2(col_value<T>(v, j, nreal) * LOG2E - m2);
+    }
+    return s;
+}
+
 template <class T>
 SISA_DEV void store_grad(T* p, int col, const frag8<T>& v, int V, int hot, float lse2, float scale) {
-    const int nreal = real_cols(col, V), jh = hot - col;
     f32x4 lo, hi;
+    if (col + 8 <= V && (unsigned)(hot - col) >= 8u) {   // no masked column, not the label's vector
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const float e = fast_exp2(col_value<T>(v, j, nreal) * LOG2E - lse2);
-        const float g = (e - (j == jh ? 1.f : 0.f)) * scale;
-        if (j < 4) lo[j] = g; else hi[j - 4] = g;
+        for (int j = 0; j < 8; ++j) {
+            const float g = fast_exp2((float)v[j] * LOG2E - lse2) * scale;
+            if (j < 4) lo[j] = g; else hi[j - 4] = g;
+        }
+    } else {
+        const int nreal = real_cols(col, V), jh = hot - col;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float e = fast_exp2(col_value<T>(v, j, nreal) * LOG2E - lse2);
+            const float g = (e - (j == jh ? 1.f : 0.f)) * scale;
+            if (j < 4) lo[j] = g; else hi[j - 4] = g;
+        }
     }
     *reinterpret_cast<frag8<T>*>(p + col) = pack8<T>(lo, hi);
 }
@@ -99,21 +138,16 @@ __global__ __launch_bounds__(RT) void lmce_rows_kernel(sisa_lmce_rows_args a) {
         for (int v = 0; v < NV; ++v) {
             const int col = v * COLS + 8 * tid;
             x[v] = col < Vp ? *reinterpret_cast<const frag8<T>*>(p + col) : zero8<T>();
-            const int nreal = real_cols(col, V);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) m = nmax(m, col_value<T>(x[v], j, nreal));
         }
+#pragma unroll
+        for (int v = 0; v < NV; ++v) m = vec_max<T>(x[v], v * COLS + 8 * tid, V, m);
         M = row_max(m, red, tid);
 #pragma unroll
         for (int v = 0; v < NV; ++v) keep_packed<T>(x[v]);
         const float m2 = M * LOG2E;
         float s = 0.f;
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            const int nreal = real_cols(v * COLS + 8 * tid, V);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) s += fast_exp2(col_value<T>(x[v], j, nreal) * LOG2E - m2);
-        }
+        for (int v = 0; v < NV; ++v) s = vec_sumexp<T>(x[v], v * COLS + 8 * tid, V, m2, s);
         S = row_sum(s, red, tid);
 #pragma unroll
         for (int v = 0; v < NV; ++v) keep_packed<T>(x[v]);
