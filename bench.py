@@ -10,7 +10,9 @@ box its device-assert kernel was seen to slow the following attention launches o
 
 Reported (one JSON line on rank 0):
   value      algorithmic attention TFLOP/s of the step: 1152 * P flop (P = B*H*T^2/2 causal pairs; fwd 320 P,
-             bwd 832 P) / step time. tokens_per_s = B*T / step time.
+             bwd 832 P) / step time. tokens_per_s = B*T / step time. The timed steps are replays of a HIP graph
+             holding one step's launches (every kernel runs in every replay; no host work between launches);
+             eager_ms_per_step is the same step as eager launches (--eager times that instead).
   roofline   the attention kernels (forward + backward launches, the dominant work) against the bf16 dense MFMA
              peak: achieved = 1152 P / (their summed average duration, HIP events on the launch stream).
   roofline_prep  the prep forward (its two launches, queued behind a GPU spin so that host work is not timed)
@@ -77,6 +79,8 @@ def parse():
     p.add_argument("--cpu-reps", type=int, default=8)
     p.add_argument("--no-ce", action="store_true", help="skip the linear cross-entropy leg (config 3)")
     p.add_argument("--no-model", action="store_true", help="skip the full decoder training step leg (config 4)")
+    p.add_argument("--eager", action="store_true",
+                   help="time the step as eager launches instead of replays of a HIP graph of one step")
     p.add_argument("--copy-mib", type=int, default=0,
                    help="run one plain device copy of this many MiB first (calibrates HBM byte counters)")
     return p.parse_args()
@@ -529,14 +533,39 @@ def main():
     for _ in range(args.warmup):
         step(False)
     torch.cuda.synchronize()
+    # eager steps: the per-phase HIP-event breakdown (host work between launches included)
     with _quiet_host():
         t0 = time.perf_counter()
         for _ in range(args.steps):
             step(True)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-    ms_step = (t1 - t0) * 1e3 / args.steps
+    ms_eager = (t1 - t0) * 1e3 / args.steps
     phases = {k: statistics.mean(a.elapsed_time(b_) for a, b_ in v) for k, v in marks.items()}
+    ms_step = ms_eager
+    if not args.eager:
+        # the headline: the same step's launches (prep forward, attention forward, attention backward, prep
+        # backward; allocations from the graph's pool) captured once into a HIP graph and replayed, so that no host
+        # work sits between the launches; every kernel runs in every replay
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step(False)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step(False)
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        with _quiet_host():
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                graph.replay()
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+        ms_step = (t1 - t0) * 1e3 / args.steps
 
     fl = A.flops(B, H, L)
     total_flop = fl["total"]
@@ -563,6 +592,8 @@ def main():
                    else f"fused SISA layer core fwd+bwd, config {cfg}",
                    "B": B, "T": L, "H": H, "d_head": D, "d_state": S, "parallelism": "none (1 GPU)"},
         "tokens_per_s": round(B * L / (ms_step * 1e-3), 1),
+        "timing": "eager launches" if args.eager else "replays of a HIP graph of one step",
+        "eager_ms_per_step": round(ms_eager, 4),
         "mfma_util_pct": round(100 * value / PEAK_BF16_TFLOPS, 2),
         "phases_ms": {k: round(v, 4) for k, v in phases.items()},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
