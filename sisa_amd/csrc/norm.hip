@@ -597,7 +597,14 @@ extern "C" int sisa_rmsnorm_bwd(const sisa_rmsnorm_args* r, void* stream) {
 namespace {
 
 // ------------------------------------------------------------------------------------------------ SwiGLU
-SISA_DEV float sigmoidf_(float a) { return 1.f / (1.f + expf(-a)); }
+// sigmoid(a) = 1 / (1 + exp(-a)). For 16-bit data (results rounded to 8 or 11 bits) from the hardware base-2
+// exponential and reciprocal, 1 / (1 + 2^(-a log2 e)), a few fp32 ulp; for fp32 data with the library expf and an
+// IEEE division. Both give 0 for a -> -inf, 1 for a -> +inf and propagate NaN.
+template <class T>
+SISA_DEV float sigmoidf_(float a) {
+    if constexpr (sizeof(T) == 2) return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-a * LOG2E));
+    else return 1.f / (1.f + expf(-a));
+}
 
 // h = silu(a) * b. PAIRS: a and b come interleaved in 8-element chunks from one array (a_8k..a_8k+7, b_8k..b_8k+7),
 // the layout of a GEMM against the gate and up weights interleaved in 8-row chunks.
@@ -610,7 +617,7 @@ __global__ __launch_bounds__(256) void swiglu_fwd_kernel(sisa_swiglu_args a) {
         const f32x8 x = load_f32x8<T>(pa), y = load_f32x8<T>(pb);
         f32x8 h;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) h[j] = (x[j] * sigmoidf_(x[j])) * y[j];
+        for (int j = 0; j < 8; ++j) h[j] = (x[j] * sigmoidf_<T>(x[j])) * y[j];
         store_f32x8<T>((T*)a.h + 8 * v, h);
     }
 }
@@ -628,7 +635,7 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(sisa_swiglu_args a) {
         f32x8 da, db;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float s = sigmoidf_(x[j]);
+            const float s = sigmoidf_<T>(x[j]);
             db[j] = g[j] * (x[j] * s);
             da[j] = (g[j] * y[j]) * (s * (1.f + x[j] * (1.f - s)));
         }
