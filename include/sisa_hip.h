@@ -158,6 +158,11 @@ typedef struct {
 int sisa_prep_fwd(const sisa_prep_fwd_args* a, void* stream);
 int sisa_prep_bwd(const sisa_prep_bwd_args* a, void* stream);
 
+/* Non-finite input check of the fused path: *ok (one byte on the device) = 1 if sum(a[0..na)) + sum(b[0..nb)) is
+ * finite, else 0, summed in fp32 in a fixed order in one launch; a and b 16-byte aligned. Replaces the torch
+ * reductions of `_nan_guard` (src/sisa/kernels/fused_prep.py:502-523), whose result feeds `torch._assert_async`. */
+int sisa_finite_sum(const float* a, int64_t na, const float* b, int64_t nb, uint8_t* ok, void* stream);
+
 /* ------------------------------------------------------------------------------------------------ linear CE */
 
 /* Row pass of the chunked linear cross-entropy over one chunk of low-precision logits (logits = x W_pad^T from the

@@ -534,6 +534,48 @@ __global__ __launch_bounds__(NT) void prep_bwd_kernel(sisa_prep_bwd_args a) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------ non-finite guard
+// ok = (sum(a) + sum(b) is finite) as one byte: the input check of the fused path (fused_prep.py:502-523: a NaN or
+// inf anywhere in lse, where every score input meets, or in the block totals makes the sum non-finite) in one
+// launch of one workgroup. fp32 sums in a fixed order (per-thread strided partials over 16-byte vectors, then a
+// fixed tree), so the result does not depend on scheduling.
+constexpr int GT = 1024;
+SISA_DEV float strided_sum(const float* p, int64_t n, int tid) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    const int64_t nv = n / 4;
+    const f32x4* pv = reinterpret_cast<const f32x4*>(p);
+    int64_t i = tid;
+    for (; i + 3 * GT < nv; i += 4 * GT) {   // four vectors in flight per thread
+        const f32x4 v0 = pv[i], v1 = pv[i + GT], v2 = pv[i + 2 * GT], v3 = pv[i + 3 * GT];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] += (v0[e] + v1[e]) + (v2[e] + v3[e]);
+    }
+    for (; i < nv; i += GT) {
+        const f32x4 v = pv[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] += v[e];
+    }
+    for (int64_t j = 4 * nv + tid; j < n; j += GT) acc[0] += p[j];
+    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+}
+
+__global__ __launch_bounds__(GT) void finite_sum_kernel(const float* a, int64_t na, const float* b, int64_t nb,
+                                                        uint8_t* ok) {
+    __shared__ float red[GT / 64];
+    const int tid = threadIdx.x;
+    float s = strided_sum(a, na, tid) + strided_sum(b, nb, tid);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if ((tid & 63) == 0) red[tid >> 6] = s;
+    __syncthreads();
+    if (tid == 0) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < GT / 64; ++w) t += red[w];
+        ok[0] = (t - t == 0.f) ? 1 : 0;   // x - x is 0 for finite x, NaN for NaN and +-inf
+    }
+}
+
 template <class T>
 int launch_prep_fwd(const sisa_prep_fwd_args* a, hipStream_t st) {
     dim3 grid((unsigned)sisa::cdiv(a->L, CH), (unsigned)a->B, (unsigned)sisa::cdiv(a->H, HG));
@@ -568,6 +610,15 @@ extern "C" int sisa_prep_fwd(const sisa_prep_fwd_args* a, void* stream) {
     SISA_REQUIRE(sisa::aligned16(a->cr) && sisa::aligned16(a->br), "sisa_prep_fwd: cr/br must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     return a->dtype == SISA_BF16 ? launch_prep_fwd<__bf16>(a, st) : launch_prep_fwd<_Float16>(a, st);
+}
+
+extern "C" int sisa_finite_sum(const float* a, int64_t na, const float* b, int64_t nb, uint8_t* ok, void* stream) {
+    SISA_REQUIRE(ok != nullptr && na >= 0 && nb >= 0 && (na == 0 || a) && (nb == 0 || b),
+                 "sisa_finite_sum: bad arguments (na=%lld nb=%lld)", (long long)na, (long long)nb);
+    SISA_REQUIRE((na == 0 || sisa::aligned16(a)) && (nb == 0 || sisa::aligned16(b)),
+                 "sisa_finite_sum: a and b must be 16-byte aligned");
+    finite_sum_kernel<<<1, GT, 0, (hipStream_t)stream>>>(a, na, b, nb, ok);
+    return sisa::launch_status("sisa_finite_sum");
 }
 
 extern "C" int64_t sisa_prep_bwd_workspace_bytes(int32_t B, int32_t L, int32_t H) {

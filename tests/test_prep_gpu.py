@@ -205,3 +205,24 @@ def test_nan_guard_sync_mode():
             FP().sisa_fused(pn, z, lam, H)
     finally:
         backends.set_check_mode(old)
+
+
+def test_finite_sum_flag():
+    """The fused non-finite check (one launch, fixed-order fp32 sum): 1 for finite data, 0 when a NaN or an inf sits
+    anywhere in either operand, and for sizes that are not multiples of the 16-byte vector; the flag is read back
+    here, never asserted on the device."""
+    fp = FP()
+    gen = torch.Generator().manual_seed(3)
+    for na, nb in ((196608, 55296), (1003, 7), (4, 0), (0, 33)):
+        a = torch.randn(na, generator=gen).to(DEV)
+        b = torch.randn(nb, generator=gen).to(DEV)
+        assert bool(fp.finite_sum_flag(a, b).item())
+        for bad in (float("nan"), float("inf"), float("-inf")):
+            for t in (a, b):
+                if t.numel() == 0:
+                    continue
+                i = int(torch.randint(0, t.numel(), (1,), generator=gen))
+                keep = t[i].item()
+                t[i] = bad
+                assert not bool(fp.finite_sum_flag(a, b).item()), (na, nb, bad)
+                t[i] = keep
