@@ -11,8 +11,8 @@ from torch import Tensor
 
 from . import _lib
 
-__all__ = ["rms_norm_hip", "rms_norm_add_hip", "rms_norm_forget_hip", "swiglu_hip", "swiglu_pairs_hip",
-           "interleave_gate_up"]
+__all__ = ["rms_norm_hip", "rms_norm_add_hip", "rms_norm_forget_hip", "rms_norm_forget_add_hip", "swiglu_hip",
+           "swiglu_pairs_hip", "interleave_gate_up"]
 
 
 def _rows(x: Tensor) -> Tensor:
@@ -84,46 +84,64 @@ class _NormFn(torch.autograd.Function):
 
 class _AddNormFn(torch.autograd.Function):
     """The residual add and the RMSNorm that follows it in one pass: ``h = x + res`` (in ``x``'s dtype) and
-    ``y = RMSNorm(h)`` in ``out_dtype`` -- one ``sisa_norm_fwd`` launch. The backward sums the gradient of ``h`` from
-    the residual stream into the norm's dx inside the ``sisa_norm_bwd`` row pass; ``res`` receives that sum in its
-    own dtype, as autograd gives it to the operand of the add."""
+    ``y = RMSNorm(h)`` in ``out_dtype``, with the fp32 forget projection ``z`` of the normalised rows when ``wf`` is
+    given -- one ``sisa_norm_fwd`` launch. The backward sums the gradient of ``h`` from the residual stream into the
+    norm's dx inside the ``sisa_norm_bwd`` row pass; ``res`` receives that sum in its own dtype, as autograd gives it
+    to the operand of the add."""
 
     @staticmethod
-    def forward(ctx, x: Tensor, res: Tensor, weight: Tensor, eps: float, out_dtype: torch.dtype):
+    def forward(ctx, x: Tensor, res: Tensor, weight: Tensor, wf, bf, eps: float, out_dtype: torch.dtype):
         x2, r2 = _rows(x), _rows(res)
         w = weight.detach().float().contiguous()
         N, D = x2.shape
+        H = 0 if wf is None else wf.shape[0]
+        wf32 = None if wf is None else wf.detach().float().contiguous()
+        bf32 = None if bf is None else bf.detach().float().contiguous()
         h = torch.empty((N, D), device=x.device, dtype=x.dtype)
         y = torch.empty((N, D), device=x.device, dtype=out_dtype)
         rstd = torch.empty(N, device=x.device, dtype=torch.float32)
-        args = _lib.NormArgs(N, D, 0, _lib.dtype_code(x.dtype), _lib.dtype_code(out_dtype), float(eps), 0,
-                             x2.data_ptr(), x2.stride(0), w.data_ptr(), None, None, y.data_ptr(), y.stride(0),
-                             rstd.data_ptr(), None, None, 0, None, None, 0, None, None, None, None,
-                             r2.data_ptr(), r2.stride(0), h.data_ptr(), h.stride(0))
+        z = torch.empty((N, H), device=x.device, dtype=torch.float32) if H else None
+        args = _lib.NormArgs(N, D, H, _lib.dtype_code(x.dtype), _lib.dtype_code(out_dtype), float(eps), 0,
+                             x2.data_ptr(), x2.stride(0), w.data_ptr(), _lib.ptr(wf32), _lib.ptr(bf32), y.data_ptr(),
+                             y.stride(0), rstd.data_ptr(), _lib.ptr(z), None, 0, None, None, 0, None, None, None,
+                             None, r2.data_ptr(), r2.stride(0), h.data_ptr(), h.stride(0))
         _lib.call("sisa_norm_fwd", args, x)
-        ctx.save_for_backward(h, w, rstd)
+        ctx.save_for_backward(h, w, rstd, wf32, bf32)
         ctx.eps, ctx.shape, ctx.wdtype, ctx.out_dtype, ctx.rdtype = eps, x.shape, weight.dtype, out_dtype, res.dtype
+        ctx.fdtypes = (None, None) if wf is None else (wf.dtype, bf.dtype)
+        if H:
+            return h.view(x.shape), y.view(x.shape), z.view(*x.shape[:-1], H)
         return h.view(x.shape), y.view(x.shape)
 
     @staticmethod
-    def backward(ctx, dh: Tensor | None, dy: Tensor | None):
-        h2, w, rstd = ctx.saved_tensors
+    def backward(ctx, dh: Tensor | None, dy: Tensor | None, dz: Tensor | None = None):
+        h2, w, rstd, wf32, bf32 = ctx.saved_tensors
         N, D = h2.shape
+        H = 0 if wf32 is None else wf32.shape[0]
         if dy is None:
             dy = torch.zeros((N, D), device=h2.device, dtype=ctx.out_dtype)
         dy2 = _rows(dy.to(ctx.out_dtype))
         dh2 = None if dh is None else _rows(dh.to(h2.dtype))
+        dz2 = None
+        if H:
+            dz2 = (torch.zeros((N, H), device=h2.device, dtype=torch.float32) if dz is None
+                   else dz.reshape(N, H).float().contiguous())
         dx = torch.empty((N, D), device=h2.device, dtype=h2.dtype)
         dw = torch.empty(D, device=h2.device, dtype=torch.float32)
-        ws = torch.empty(_lib.workspace_bytes("sisa_norm_bwd_workspace_bytes", N, D, 0) // 4, device=h2.device,
+        dwf = torch.empty((H, D), device=h2.device, dtype=torch.float32) if H else None
+        dbf = torch.empty(H, device=h2.device, dtype=torch.float32) if H else None
+        ws = torch.empty(_lib.workspace_bytes("sisa_norm_bwd_workspace_bytes", N, D, H) // 4, device=h2.device,
                          dtype=torch.float32)
-        args = _lib.NormArgs(N, D, 0, _lib.dtype_code(h2.dtype), _lib.dtype_code(ctx.out_dtype), float(ctx.eps), 0,
-                             h2.data_ptr(), h2.stride(0), w.data_ptr(), None, None, None, 0, rstd.data_ptr(), None,
-                             dy2.data_ptr(), dy2.stride(0), None, dx.data_ptr(), dx.stride(0), dw.data_ptr(), None,
-                             None, ws.data_ptr(), None, 0, None, 0, _lib.ptr(dh2), 0 if dh2 is None else dh2.stride(0))
+        args = _lib.NormArgs(N, D, H, _lib.dtype_code(h2.dtype), _lib.dtype_code(ctx.out_dtype), float(ctx.eps), 0,
+                             h2.data_ptr(), h2.stride(0), w.data_ptr(), _lib.ptr(wf32), _lib.ptr(bf32), None, 0,
+                             rstd.data_ptr(), None, dy2.data_ptr(), dy2.stride(0), _lib.ptr(dz2), dx.data_ptr(),
+                             dx.stride(0), dw.data_ptr(), _lib.ptr(dwf), _lib.ptr(dbf), ws.data_ptr(), None, 0, None,
+                             0, _lib.ptr(dh2), 0 if dh2 is None else dh2.stride(0))
         _lib.call("sisa_norm_bwd", args, h2)
         dx = dx.view(ctx.shape)
-        return dx, dx.to(ctx.rdtype), dw.to(ctx.wdtype), None, None
+        dwf_out = None if dwf is None else dwf.to(ctx.fdtypes[0])
+        dbf_out = None if dbf is None else dbf.to(ctx.fdtypes[1])
+        return dx, dx.to(ctx.rdtype), dw.to(ctx.wdtype), dwf_out, dbf_out, None, None
 
 
 def _check_norm(x: Tensor, out_dtype: torch.dtype, H: int) -> None:
@@ -158,7 +176,23 @@ def rms_norm_add_hip(x: Tensor, res: Tensor, weight: Tensor, eps: float,
     if res.shape != x.shape or res.dtype != out_dtype:
         raise ValueError(f"rms_norm_add_hip: residual {tuple(res.shape)} {res.dtype} must match x {tuple(x.shape)} "
                          f"and have the output dtype {out_dtype}")
-    return _AddNormFn.apply(x, res, weight, eps, out_dtype)
+    return _AddNormFn.apply(x, res, weight, None, None, eps, out_dtype)
+
+
+def rms_norm_forget_add_hip(x: Tensor, res: Tensor, weight: Tensor, eps: float, wf: Tensor, bf: Tensor,
+                            out_dtype: torch.dtype | None = None) -> tuple[Tensor, Tensor, Tensor]:
+    """``h = x + res`` followed by :func:`rms_norm_forget_hip` of ``h`` in one pass each way: the residual add that
+    ends a decoder block and the next block's attention norm with its forget-gate projection. Returns
+    ``(h, y, z)``; ``res`` as in :func:`rms_norm_add_hip`."""
+    out_dtype = out_dtype or x.dtype
+    if wf.dim() != 2 or wf.shape[1] != x.shape[-1] or bf.shape != (wf.shape[0],):
+        raise ValueError(f"rms_norm_forget_add_hip: projection {tuple(wf.shape)} / bias {tuple(bf.shape)} do not "
+                         f"match rows of {x.shape[-1]}")
+    _check_norm(x, out_dtype, wf.shape[0])
+    if res.shape != x.shape or res.dtype != out_dtype:
+        raise ValueError(f"rms_norm_forget_add_hip: residual {tuple(res.shape)} {res.dtype} must match x "
+                         f"{tuple(x.shape)} and have the output dtype {out_dtype}")
+    return _AddNormFn.apply(x, res, weight, wf, bf, eps, out_dtype)
 
 
 def rms_norm_forget_hip(x: Tensor, weight: Tensor, eps: float, wf: Tensor, bf: Tensor,

@@ -324,24 +324,36 @@ class SISABlock(nn.Module):
             return False
         return _resolve_impl(self.config.attn_impl, x, self.config) == "hip_fused"
 
-    def _forward_hip(self, x: Tensor) -> Tensor:
+    def _forward_hip(self, x: Tensor, res: Tensor | None = None, defer: bool = False):
         """The block on the HIP kernels: the attention norm and the fp32 forget-gate projection in one pass that
         also emits the normalised rows in the dtype of the projection GEMM (the reference casts them under autocast),
-        the fused attention sublayer, the residual add and the FFN norm in one pass, SwiGLU."""
-        from .kernels.norm import rms_norm_add_hip, rms_norm_forget_hip, rms_norm_hip
+        the fused attention sublayer, the residual add and the FFN norm in one pass, SwiGLU.
+
+        ``res``: the previous block's FFN output, whose residual add (``x + res``) runs in this block's attention
+        norm. ``defer=True`` returns ``(h, f)`` -- the stream before the FFN residual and the FFN output -- for the
+        next block to add the same way (``(h + f, None)`` when ``f`` cannot be passed on); otherwise ``h + f``."""
+        from .kernels.norm import rms_norm_add_hip, rms_norm_forget_add_hip, rms_norm_forget_hip, rms_norm_hip
 
         cd = _compute_dtype(x)
         out_dtype = cd if x.dtype == torch.float32 else x.dtype
         at = self.attn
-        n, z = rms_norm_forget_hip(x, self.attn_norm.weight, self.attn_norm.eps, at.forget_proj.weight,
-                                   at.forget_proj.bias, out_dtype)
+        nw, eps, wf, bf = self.attn_norm.weight, self.attn_norm.eps, at.forget_proj.weight, at.forget_proj.bias
+        if res is not None and res.dtype == out_dtype and res.shape == x.shape:
+            x, n, z = rms_norm_forget_add_hip(x, res, nw, eps, wf, bf, out_dtype)
+        else:
+            if res is not None:
+                x = x + res
+            n, z = rms_norm_forget_hip(x, nw, eps, wf, bf, out_dtype)
         a = at._forward_fused(n, z)
         if a.dtype == out_dtype and a.shape == x.shape:   # residual add fused into the FFN norm
             x, m = rms_norm_add_hip(x, a, self.ffn_norm.weight, self.ffn_norm.eps, out_dtype)
         else:
             x = x + a
             m = rms_norm_hip(x, self.ffn_norm.weight, self.ffn_norm.eps, out_dtype)
-        return x + self.ffn(m)
+        f = self.ffn(m)
+        if defer:
+            return (x, f) if (f.dtype == out_dtype and f.shape == x.shape) else (x + f, None)
+        return x + f
 
     def forward(self, x: Tensor, cache: "SISACache | None" = None) -> Tensor:
         if cache is None and self._fused_norm_ok(x):
@@ -363,6 +375,11 @@ def _lm_head_loss(hidden: Tensor, weight: Tensor, labels: Tensor) -> Tensor:
     logits = F.linear(hidden, weight)
     return F.cross_entropy(logits.reshape(-1, logits.shape[-1]).float(), labels.reshape(-1),
                            ignore_index=IGNORE_INDEX)
+
+
+# Consecutive fused HIP blocks pass the FFN output on to the next block's attention norm (SISAModel.forward); False
+# adds it in each block instead (same results bit for bit).
+DEFER_RESIDUAL = True
 
 
 class SISAModel(nn.Module):
@@ -394,8 +411,18 @@ class SISAModel(nn.Module):
         x = self.embed(input_ids)
         use_ckpt = (self.config.gradient_checkpointing and self.training and cache is None
                     and torch.is_grad_enabled())
+        # Consecutive blocks on the fused HIP path pass their FFN output on instead of adding it: the next block's
+        # attention norm adds it in its own pass (same arithmetic, one launch less each way per block).
+        pending = None
         for layer in self.layers:
+            if DEFER_RESIDUAL and not use_ckpt and cache is None and layer._fused_norm_ok(x):
+                x, pending = layer._forward_hip(x, pending, defer=True)
+                continue
+            if pending is not None:
+                x, pending = x + pending, None
             x = checkpoint(layer, x, use_reentrant=False) if use_ckpt else layer(x, cache=cache)
+        if pending is not None:
+            x = x + pending
         return self.final_norm(x)
 
     def compile_common(self) -> "SISAModel":

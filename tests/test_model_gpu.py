@@ -353,3 +353,29 @@ def test_bf16_decoding_close_to_full_forward():
     assert out.shape == (2, 38)
     assert rel_err(dec, ref) <= 2.0 * rel_err(full, ref) + 1e-3
     assert max(rel_err(dec[:, t], full[:, t]) for t in range(96)) < 5e-2
+
+
+def test_deferred_residual_bitwise():
+    """Consecutive fused blocks hand their FFN output to the next block's attention norm, which adds it in its own
+    pass (SISAModel.forward, modeling.DEFER_RESIDUAL): loss and every parameter gradient bitwise equal to adding it in
+    each block, under bf16 autocast (fp32 stream) and with bf16 parameters (bf16 stream)."""
+    from sisa_amd import modeling
+    for autocast in (True, False):
+        res = {}
+        for defer in (True, False):
+            modeling.DEFER_RESIDUAL = defer
+            try:
+                torch.manual_seed(0)
+                model = tiny_model(seed=3, attn_impl="hip_fused", n_layer=3).to(DEV)
+                if not autocast:
+                    model = model.to(torch.bfloat16)
+                ids = token_ids(2, 96).to(DEV)
+                with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+                    loss = model(ids, labels=ids).loss
+                loss.backward()
+                res[defer] = (loss.detach(), {n: p.grad.detach().clone() for n, p in model.named_parameters()})
+            finally:
+                modeling.DEFER_RESIDUAL = True
+        assert torch.equal(res[True][0], res[False][0])
+        bad = [n for n, g in res[True][1].items() if not torch.equal(g, res[False][1][n])]
+        assert not bad, f"autocast={autocast}: gradients differ for {bad[:5]}"
