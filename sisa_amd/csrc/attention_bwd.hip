@@ -1,0 +1,619 @@
+// SISA attention backward for gfx950: the query-owned dq kernel and the key-owned dkv kernel of the exact-delta
+// backward (the decomposition, score arithmetic and reference citations are described in attention.hip). A
+// translation unit of its own so that the build can give these two kernels their own machine scheduler.
+#include "attention_common.h"
+
+namespace {
+
+// ------------------------------------------------------------------------------------------------ backward: dq
+
+template <class T>
+struct __attribute__((aligned(16))) DqLds {
+    T ks[64 * DH];               // K (scores; transposed reads for dq)
+    T vs[64 * DH];               // V (dP)
+    T bs[64 * DS];               // B~ (scores; transposed reads for dc)
+    float fk[64], gk[64];
+    float nfe[64];               // F_e - F_j (F_e = F at the tile's last key; anchored off-block scores)
+    float cfm[64];               // colf * mid for the workgroup's query block
+};
+
+// Per-query row sums of the dq kernel (diagonal excluded): xa = sum dS^ u, ya = sum P u, wa = D = sum dS^,
+// za = Z = sum P, ptt = P_tt, dptt = dP_tt, xd = cb_tt. Off-block tiles accumulate xa, ya without the row factor
+// rowf; a wave's own-block tile is its last one, and rowf (lam*rowf for dc) is applied once before it.
+struct RowSums {
+    float xa, ya, wa, za, ptt, dptt, xd;
+};
+
+// Score arithmetic as in the forward: q is pre-scaled by 1/8; for 16-bit inputs off-block tiles are anchored at the
+// key tile's last F (F_e - F_j enters the q.k MFMA as its accumulator input, (F_i - F_e) log2e - lse is one offset
+// per query and tile) and dP - Delta comes out of the dO.V MFMA (-Delta as its accumulator input). The dkv kernel
+// evaluates the same pairs with the same anchors and the same accumulator inputs.
+template <class T, bool DIAG>
+SISA_DEV void dq_tile(const DqLds<T>& sm, int lane, int n0, int q0, int L, const frag8<T> (&qf)[2],
+                      const frag8<T>& cfr, const frag8<T> (&dof)[2], float fq, float rs, float gq, float lse,
+                      float dhat, float lam, RowSums& R, f32x4 (&dqa)[4], f32x4 (&dca)[2]) {
+    constexpr bool F16 = Anchor<T>::on;
+    constexpr bool ANCH = F16 && !DIAG;
+    const int grp = lane >> 4, lc = lane & 15;
+    const int qq = q0 + lc;
+    const float* cfm = sm.cfm;
+    const float ftl = ANCH ? fmaf(fq - sm.fk[63], LOG2E, -lse) : -lse;
+    const f32x4 ndh = F16 ? f32x4{-dhat, -dhat, -dhat, -dhat} : zero4();
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {           // 32 keys (one K-step of the dq/dc products) at a time
+        f32x4 dsv[2], wv[2];                   // dq and dc operands of the two 16-key blocks (before rounding)
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {       // one 16-key block at a time keeps the live set small
+            __builtin_amdgcn_sched_barrier(0);
+            const int kb = 2 * st + hb;
+            const int j0 = kb * 16 + 4 * grp;
+            const f32x4 sc = mma(frag_rows<T, DH>(sm.ks, kb * 16, 1, lane), qf[1],
+                                 mma(frag_rows<T, DH>(sm.ks, kb * 16, 0, lane), qf[0],
+                                     ANCH ? lds4f(&sm.nfe[j0]) : zero4()));
+            const f32x4 cb = mma(frag_rows<T, DS>(sm.bs, kb * 16, 0, lane), cfr, zero4());
+            const f32x4 dp = mma(frag_rows<T, DH>(sm.vs, kb * 16, 1, lane), dof[1],
+                                 mma(frag_rows<T, DH>(sm.vs, kb * 16, 0, lane), dof[0], ndh));
+            const f32x4 fk = lds4f(&sm.fk[j0]);
+            if (DIAG) {
+                const f32x4 gk = lds4f(&sm.gk[j0]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int jj = n0 + j0 + i;
+                    const bool valid = jj <= qq && jj < L && qq < L;
+                    const bool eye = valid && jj == qq;
+                    const float dec = valid ? exp2_le0((gq - gk[i]) * LOG2E) : 0.f;
+                    const float cbv = cb[i];
+                    const float u = dec * cbv;
+                    float s = sc[i] + (fq - fk[i]);
+                    s = s + lam * u;
+                    const float pr = valid ? fast_exp2(fmaf(s, LOG2E, -lse)) : 0.f;
+                    const float dpd = F16 ? dp[i] : dp[i] - dhat;   // dP - Delta
+                    const float ds = pr * dpd;
+                    const float dso = eye ? 0.f : ds;
+                    R.ptt += eye ? pr : 0.f;
+                    R.dptt += eye ? dpd : 0.f;
+                    R.xd += eye ? cbv : 0.f;
+                    const float po = eye ? 0.f : pr;
+                    R.za += po;
+                    R.ya += po * u;
+                    R.wa += dso;
+                    R.xa += dso * u;
+                    dsv[hb][i] = dso;
+                    wv[hb][i] = dso * (lam * dec);
+                }
+            } else {
+                const f32x4 cf = lds4f(&cfm[j0]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float uc = cb[i] * cf[i];
+                    float s;
+                    if constexpr (ANCH) s = fmaf(rs, uc, sc[i]);
+                    else s = (sc[i] + (fq - fk[i])) + rs * uc;
+                    const float pr = fast_exp2(fmaf(s, LOG2E, ftl));
+                    const float ds = pr * (F16 ? dp[i] : dp[i] - dhat);
+                    R.xa += ds * uc;
+                    R.ya += pr * uc;
+                    R.za += pr;
+                    R.wa += ds;
+                    dsv[hb][i] = ds;
+                    wv[hb][i] = ds * cf[i];
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const frag8<T> dsf = pack8<T>(dsv[0], dsv[1]);
+        const frag8<T> wf = pack8<T>(wv[0], wv[1]);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) dqa[db] = mma(frag_tr<T, DH>(sm.ks, db * 16, st, lane), dsf, dqa[db]);
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) dca[sb] = mma(frag_tr<T, DS>(sm.bs, sb * 16, st, lane), wf, dca[sb]);
+    }
+}
+
+template <class T>
+__global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void attn_bwd_dq_kernel(sisa_attn_bwd_args a) {
+    constexpr int NBUF = sizeof(T) == 2 ? 2 : 1;
+    __shared__ DqLds<T> smb[NBUF];
+    const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int NQT = (a.L + 63) / 64;
+    int bh, rank;
+    xcd_map(blockIdx.x, NQT, a.B * a.H, bh, rank);
+    const int tile = NQT - 1 - rank;               // heavy (late) query blocks first
+    const int H = a.H, L = a.L;
+    const int b = bh / H, h = bh % H;
+    const bool has_f = a.f.ptr != nullptr;
+    const T* Q = (const T*)a.q.ptr + (int64_t)b * a.q.sb + (int64_t)h * a.q.sh;
+    const T* K = (const T*)a.k.ptr + (int64_t)b * a.k.sb + (int64_t)h * a.k.sh;
+    const T* V = (const T*)a.v.ptr + (int64_t)b * a.v.sb + (int64_t)h * a.v.sh;
+    const T* C = (const T*)a.c.ptr + (int64_t)b * a.c.sb + (int64_t)h * a.c.sh;
+    const T* Bm = (const T*)a.b.ptr + (int64_t)b * a.b.sb + (int64_t)h * a.b.sh;
+    const T* O = (const T*)a.o.ptr + (int64_t)b * a.o.sb + (int64_t)h * a.o.sh;
+    const T* DO = (const T*)a.dout.ptr + (int64_t)b * a.dout.sb + (int64_t)h * a.dout.sh;
+    const float* G = (const float*)a.g.ptr + (int64_t)b * a.g.sb + (int64_t)h * a.g.sh;
+    const float* FF = has_f ? (const float*)a.f.ptr + (int64_t)b * a.f.sb + (int64_t)h * a.f.sh : nullptr;
+    const float* ROWF = a.rowf + (int64_t)bh * L;
+    const float* COLF = a.colf + (int64_t)bh * L;
+    const float* LSE = a.lse + (int64_t)bh * L;
+    const float lam = a.lam[(int64_t)h * a.s_lam];
+    const int64_t skl = a.k.sl, svl = a.v.sl, sbl = a.b.sl, sgl = a.g.sl;
+    const int64_t sfl = has_f ? a.f.sl : 0;
+    const int64_t BHL = (int64_t)a.B * H * L;
+    float* WS = (float*)a.workspace;
+
+    const int tile0 = tile * 64;                   // the workgroup's 64-row decay block
+    const int q0 = tile0 + 16 * w;
+    const bool live = q0 < L;
+    const float ga = G[(int64_t)tile0 * sgl];      // anchor: g at the start of the block
+
+    frag8<T> qf[2], cfr, dof[2];
+    float fq, rowfq, rs, gq, lse, dhat;
+    {
+        const int qq = q0 + lc;
+        const bool ok = qq < L;
+        float part = 0.f;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            qf[st] = ok ? scale_frag<T>(load8<T>(Q + (int64_t)qq * a.q.sl + 32 * st + 8 * grp), QSCALE) : zero8<T>();
+            dof[st] = ok ? load8<T>(DO + (int64_t)qq * a.dout.sl + 32 * st + 8 * grp) : zero8<T>();
+            if (ok) {
+                const frag8<T> ov = load8<T>(O + (int64_t)qq * a.o.sl + 32 * st + 8 * grp);
+                f32x4 o32a = zero4(), o32b = zero4();
+                if (a.o32) {
+                    const float* p32 = a.o32 + ((int64_t)bh * L + qq) * DH + 32 * st + 8 * grp;
+                    o32a = *reinterpret_cast<const f32x4*>(p32);
+                    o32b = *reinterpret_cast<const f32x4*>(p32 + 4);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    float o = (float)ov[j];
+                    if (a.o32) {
+                        // o'' agrees with the DT o to within 2^-15 relative: use the DT value (attention.py:341-349)
+                        const float o2 = j < 4 ? o32a[j] : o32b[j - 4];
+                        o = (fabsf(o2 - o) <= 3.0517578125e-05f * fabsf(o)) ? o : o2;
+                    }
+                    part += o * (float)dof[st][j];
+                }
+            }
+        }
+        dhat = group_sum(part);
+        cfr = ok ? load8<T>(C + (int64_t)qq * a.c.sl + 8 * grp) : zero8<T>();
+        fq = (has_f && ok) ? FF[(int64_t)qq * sfl] : 0.f;
+        rowfq = ok ? ROWF[qq] : 0.f;
+        rs = lam * rowfq;
+        gq = G[(int64_t)(ok ? qq : L - 1) * sgl];
+        lse = ok ? LSE[qq] : __builtin_inff();
+    }
+
+    f32x4 dqa[4], dca[2];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) dqa[db] = zero4();
+    dca[0] = dca[1] = zero4();
+    RowSums R{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+
+    // Key tiles straight into LDS (DMA buffer loads); 16-bit types double-buffer them (one barrier per tile), fp32
+    // uses one buffer. The per-key scalars (F_j, g_j, colf_j, g at the tile's last key) are fetched into registers by
+    // the first wave one tile ahead.
+    DmaStage<T, DH, NWB> dk, dv;
+    DmaStage<T, DS, NWB> dbt;
+    const int64_t xk = ((int64_t)(L - 1) * skl + DH) * (int64_t)sizeof(T);   // view extents (bytes)
+    const int64_t xv = ((int64_t)(L - 1) * svl + DH) * (int64_t)sizeof(T);
+    const int64_t xb = ((int64_t)(L - 1) * sbl + DS) * (int64_t)sizeof(T);
+    dk.init(skl, w, lane);
+    dv.init(svl, w, lane);
+    dbt.init(sbl, w, lane);
+    float pf_f = 0.f, pf_g = 0.f, pf_cf = 0.f, pf_ge = 0.f, pf_fe = 0.f;
+    auto fetch_scalars = [&](int n0) {
+        if (tid < 64) {
+            const int j = n0 + tid;
+            const int jc = j < L ? j : L - 1;
+            const int je = n0 + 63 < L ? n0 + 63 : L - 1;   // end of the key block
+            pf_f = (has_f && j < L) ? FF[(int64_t)j * sfl] : 0.f;
+            pf_g = G[(int64_t)jc * sgl];
+            pf_cf = j < L ? COLF[j] : 0.f;
+            pf_ge = G[(int64_t)je * sgl];
+            pf_fe = has_f ? FF[(int64_t)je * sfl] : 0.f;
+        }
+    };
+    auto issue_tile = [&](DqLds<T>& d, int n0) {   // rows >= L read as zero
+        dma_issue<1>(dk, K, xk, (int)(n0 * skl * (int64_t)sizeof(T)), d.ks, w);
+        dma_issue<1>(dv, V, xv, (int)(n0 * svl * (int64_t)sizeof(T)), d.vs, w);
+        dma_issue<1>(dbt, Bm, xb, (int)(n0 * sbl * (int64_t)sizeof(T)), d.bs, w);
+        if (tid < 64) {
+            d.fk[tid] = pf_f;
+            d.nfe[tid] = pf_fe - pf_f;
+            d.gk[tid] = pf_g;
+            d.cfm[tid] = pf_cf * exp2_le0((ga - pf_ge) * LOG2E);
+        }
+    };
+    // tile t (keys 64 t ..) is in buffer t & (NBUF-1) after advance(t) (and, for two buffers, the barrier before it)
+    auto advance = [&](int t) {
+        const int n0 = 64 * t;
+        if (NBUF == 2) {
+            if (n0 + 64 <= tile0) {
+                issue_tile(smb[(t + 1) & (NBUF - 1)], n0 + 64);
+                if (n0 + 128 <= tile0) fetch_scalars(n0 + 128);
+            }
+        } else if (t > 0) {
+            __syncthreads();
+            issue_tile(smb[0], n0);
+            __syncthreads();
+            if (n0 + 64 <= tile0) fetch_scalars(n0 + 64);
+        }
+    };
+    fetch_scalars(0);
+    issue_tile(smb[0], 0);
+    if (64 <= tile0) fetch_scalars(64);
+    __syncthreads();
+    // key tiles before the block (all off-block), then the block's own tile
+    const int nt = tile0 / 64;
+    for (int t = 0; t < nt; ++t) {
+        advance(t);
+        if (live) {
+            const DqLds<T>& sm = smb[t & (NBUF - 1)];
+            dq_tile<T, false>(sm, lane, 64 * t, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, R, dqa, dca);
+        }
+        if (NBUF == 2) __syncthreads();
+    }
+    advance(nt);
+    if (live) {
+        // the block's own tile: apply the off-block row factors once, in fp32, then the diagonal path
+        const DqLds<T>& sm = smb[nt & (NBUF - 1)];
+        R.xa *= rowfq;
+        R.ya *= rowfq;
+        dca[0] *= rs;
+        dca[1] *= rs;
+        dq_tile<T, true>(sm, lane, tile0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, R, dqa, dca);
+    }
+    if (!live) return;
+    const float xat = group_sum(R.xa), yat = group_sum(R.ya), Wa = group_sum(R.wa), Za = group_sum(R.za);
+    const float Ptt = group_sum(R.ptt), Dptt = group_sum(R.dptt), Xd = group_sum(R.xd);
+    const int qq = q0 + lc;
+    if (qq >= L) return;
+    // self-normalised exact delta and the delta-free diagonal (attention.py:453-463)
+    float ssum = Ptt + Za;
+    ssum = ssum > 0.f ? ssum : 1.f;
+    const float x0 = Dptt;   // dP_tt - Delta
+    const float tt = dhat + (Ptt * x0 + Wa) / ssum;
+    const float dstt = Ptt * (Za * x0 - Wa) / ssum;
+    const float dl_row = xat + (dhat - tt) * yat;
+    const float dsq = (float)cvt<T>(dstt);           // one DT rounding of the diagonal operands
+    const float dsc = (float)cvt<T>(dstt * lam);
+    const T* krow = K + (int64_t)qq * skl;
+    const T* brow = Bm + (int64_t)qq * sbl;
+    T* dqp = (T*)a.dq.ptr + (int64_t)b * a.dq.sb + (int64_t)h * a.dq.sh + (int64_t)qq * a.dq.sl;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+        const int d = db * 16 + 4 * grp;
+        const vec4<T> kv = load4<T>(krow + d);
+        f32x4 r = dqa[db];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = fmaf(dsq, (float)kv[i], r[i]);
+        store_row4<T, T>(dqp + d, r * QSCALE);
+    }
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+        const int s0 = sb * 16 + 4 * grp;
+        const vec4<T> bv = load4<T>(brow + s0);
+        f32x4 r = dca[sb];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] = fmaf(dsc, (float)bv[i], r[i]);
+        if (a.dcb_dtype == SISA_F32) {
+            float* dcp = (float*)a.dc.ptr + (int64_t)b * a.dc.sb + (int64_t)h * a.dc.sh + (int64_t)qq * a.dc.sl;
+            *reinterpret_cast<f32x4*>(dcp + s0) = r;
+        } else {
+            T* dcp = (T*)a.dc.ptr + (int64_t)b * a.dc.sb + (int64_t)h * a.dc.sh + (int64_t)qq * a.dc.sl;
+            store_row4<T, T>(dcp + s0, r);
+        }
+    }
+    if (grp == 0) {
+        const int64_t o = (int64_t)bh * L + qq;
+        WS[WS_DELTA * BHL + o] = dhat;
+        WS[WS_DDEL * BHL + o] = tt - dhat;
+        WS[WS_DSD * BHL + o] = dstt;
+        WS[WS_RG * BHL + o] = lam * dl_row;
+        WS[WS_RL * BHL + o] = dl_row + dstt * Xd;
+        WS[WS_RF * BHL + o] = Wa - Za * (tt - dhat);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ backward: dk dv db
+// Scores are computed as S = Q K^T (a lane owns one key's column sums); query tiles are visited in descending order
+// so that the keys' own 64-block is every wave's last tile.
+template <class T>
+struct __attribute__((aligned(16))) DkvLds {
+    T qs[64 * DH];               // Q (scores; transposed reads for dk)
+    T cs[64 * DS];               // C~ (scores; transposed reads for db)
+    T ds[64 * DH];               // dO (dP; transposed reads for dv)
+    float lse[64], dhat[64], ddel[64], fq[64], gq[64];
+    float rq[64];                // rowf * mid for the query block against the workgroup's key block
+    float ftl[64];               // (F_i - F_e) log2e - lse_i (16-bit: anchored off-block scores)
+    float ndh[64];               // -Delta_i (16-bit: the dO.V MFMA's accumulator input)
+};
+
+// kf holds k/8 (the same exact products as the dq kernel's q/8); for 16-bit inputs off-block tiles use the dq kernel's
+// anchor (nfe = F_e - F_j of the workgroup's key block as the q.k accumulator input, ftl per query) and -Delta as the
+// dO.V accumulator input, so both kernels evaluate every pair with the same operations.
+template <class T, bool PAIR>
+SISA_DEV void dkv_tile(const DkvLds<T>& sm, int lane, int m0, int k0, int L, const frag8<T> (&kf)[2],
+                       const frag8<T> (&vf)[2], const frag8<T>& bfr, float fk, float nfe, float rk, float gk, float dsd,
+                       float lam, float& dgu, float& dfs, f32x4 (&dva)[4], f32x4 (&dka)[4], f32x4 (&dba)[2]) {
+    constexpr bool F16 = Anchor<T>::on;
+    constexpr bool ANCH = F16 && !PAIR;
+    const int grp = lane >> 4, lc = lane & 15;
+    const int kk = k0 + lc;
+    const float* rqm = sm.rq;
+    const f32x4 nfe4 = ANCH ? f32x4{nfe, nfe, nfe, nfe} : zero4();
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {           // 32 queries (one K-step of the dk/dv/db products) at a time
+        f32x4 pv[2], kv[2], bv[2];             // dv, dk and db operands of the two 16-query blocks (before rounding)
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {       // one 16-query block at a time keeps the live set small
+            __builtin_amdgcn_sched_barrier(0);
+            const int qb = 2 * st + hb;
+            const int i0 = qb * 16 + 4 * grp;
+            const f32x4 sc = mma(frag_rows<T, DH>(sm.qs, qb * 16, 1, lane), kf[1],
+                                 mma(frag_rows<T, DH>(sm.qs, qb * 16, 0, lane), kf[0], nfe4));
+            const f32x4 cb = mma(frag_rows<T, DS>(sm.cs, qb * 16, 0, lane), bfr, zero4());
+            const f32x4 dp = mma(frag_rows<T, DH>(sm.ds, qb * 16, 1, lane), vf[1],
+                                 mma(frag_rows<T, DH>(sm.ds, qb * 16, 0, lane), vf[0],
+                                     F16 ? lds4f(&sm.ndh[i0]) : zero4()));
+            const f32x4 dd = lds4f(&sm.ddel[i0]);
+            if (PAIR) {
+                const f32x4 gq = lds4f(&sm.gq[i0]);
+                const f32x4 lq = lds4f(&sm.lse[i0]), fq = lds4f(&sm.fq[i0]);
+                const f32x4 dh = F16 ? zero4() : lds4f(&sm.dhat[i0]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int qq = m0 + i0 + i;
+                    const bool valid = qq >= kk && qq < L;
+                    const bool strict = valid && qq > kk;
+                    const bool eye = valid && qq == kk;
+                    const float dec = valid ? exp2_le0((gq[i] - gk) * LOG2E) : 0.f;
+                    const float u = dec * cb[i];
+                    float s = sc[i] + (fq[i] - fk);
+                    s = s + lam * u;
+                    const float p = valid ? fast_exp2(fmaf(s, LOG2E, -lq[i])) : 0.f;
+                    const float dsh = p * (F16 ? dp[i] : dp[i] - dh[i]);
+                    const float dsx = dsh - p * dd[i];
+                    const float dso = strict ? dsx : 0.f;
+                    dgu += dso * u;
+                    dfs += dso;
+                    pv[hb][i] = p;
+                    kv[hb][i] = eye ? dsd : dso;
+                    bv[hb][i] = (eye ? dsd : (strict ? dsh : 0.f)) * (lam * dec);
+                }
+            } else {
+                const f32x4 rq = lds4f(&rqm[i0]);
+                const f32x4 off = ANCH ? lds4f(&sm.ftl[i0]) : zero4();
+                const f32x4 lq = ANCH ? zero4() : lds4f(&sm.lse[i0]);
+                const f32x4 fq = ANCH ? zero4() : lds4f(&sm.fq[i0]);
+                const f32x4 dh = F16 ? zero4() : lds4f(&sm.dhat[i0]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float uc = cb[i] * rq[i];
+                    float s;
+                    if constexpr (ANCH) s = fmaf(rk, uc, sc[i]);
+                    else s = (sc[i] + (fq[i] - fk)) + rk * uc;
+                    const float p = fast_exp2(fmaf(s, LOG2E, ANCH ? off[i] : -lq[i]));
+                    const float dsh = p * (F16 ? dp[i] : dp[i] - dh[i]);
+                    const float dsx = dsh - p * dd[i];
+                    dgu += dsx * uc;
+                    dfs += dsx;
+                    pv[hb][i] = p;
+                    kv[hb][i] = dsx;
+                    bv[hb][i] = dsh * rq[i];
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const frag8<T> pf = pack8<T>(pv[0], pv[1]);
+        const frag8<T> kfr = pack8<T>(kv[0], kv[1]);
+        const frag8<T> bf = pack8<T>(bv[0], bv[1]);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            dva[db] = mma(frag_tr<T, DH>(sm.ds, db * 16, st, lane), pf, dva[db]);
+            dka[db] = mma(frag_tr<T, DH>(sm.qs, db * 16, st, lane), kfr, dka[db]);
+        }
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) dba[sb] = mma(frag_tr<T, DS>(sm.cs, sb * 16, st, lane), bf, dba[sb]);
+    }
+}
+
+template <class T>
+__global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a) {
+    constexpr int NBUF = sizeof(T) == 2 ? 2 : 1;
+    __shared__ DkvLds<T> smb[NBUF];
+    const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int bh, ktile;
+    xcd_map(blockIdx.x, (a.L + 63) / 64, a.B * a.H, bh, ktile);   // early key blocks carry the most queries: first
+    const int H = a.H, L = a.L;
+    const int b = bh / H, h = bh % H;
+    const bool has_f = a.f.ptr != nullptr;
+    const T* Q = (const T*)a.q.ptr + (int64_t)b * a.q.sb + (int64_t)h * a.q.sh;
+    const T* K = (const T*)a.k.ptr + (int64_t)b * a.k.sb + (int64_t)h * a.k.sh;
+    const T* V = (const T*)a.v.ptr + (int64_t)b * a.v.sb + (int64_t)h * a.v.sh;
+    const T* C = (const T*)a.c.ptr + (int64_t)b * a.c.sb + (int64_t)h * a.c.sh;
+    const T* Bm = (const T*)a.b.ptr + (int64_t)b * a.b.sb + (int64_t)h * a.b.sh;
+    const T* DO = (const T*)a.dout.ptr + (int64_t)b * a.dout.sb + (int64_t)h * a.dout.sh;
+    const float* G = (const float*)a.g.ptr + (int64_t)b * a.g.sb + (int64_t)h * a.g.sh;
+    const float* FF = has_f ? (const float*)a.f.ptr + (int64_t)b * a.f.sb + (int64_t)h * a.f.sh : nullptr;
+    const float* ROWF = a.rowf + (int64_t)bh * L;
+    const float* COLF = a.colf + (int64_t)bh * L;
+    const float* LSE = a.lse + (int64_t)bh * L;
+    const float lam = a.lam[(int64_t)h * a.s_lam];
+    const int64_t sql = a.q.sl, scl = a.c.sl, sdl = a.dout.sl, sgl = a.g.sl;
+    const int64_t sfl = has_f ? a.f.sl : 0;
+    const int64_t BHL = (int64_t)a.B * H * L;
+    const float* WS = (const float*)a.workspace;
+    const float* DELTA = WS + WS_DELTA * BHL + (int64_t)bh * L;
+    const float* DDEL = WS + WS_DDEL * BHL + (int64_t)bh * L;
+
+    const int ktile0 = ktile * 64;                 // the workgroup's 64-key decay block
+    const int k0 = ktile0 + 16 * w;
+    const bool live = k0 < L;
+    const int kend = ktile0 + 63 < L ? ktile0 + 63 : L - 1;
+    const float ge = G[(int64_t)kend * sgl];       // anchors: g and F at the block end
+    const float fe = has_f ? FF[(int64_t)kend * sfl] : 0.f;
+
+    frag8<T> kf[2], vf[2], bfr;
+    float fk, nfe, colf, rk, gk, dsd;
+    {
+        const int kk = k0 + lc;
+        const bool ok = kk < L;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            kf[st] = ok ? scale_frag<T>(load8<T>(K + (int64_t)kk * a.k.sl + 32 * st + 8 * grp), QSCALE) : zero8<T>();
+            vf[st] = ok ? load8<T>(V + (int64_t)kk * a.v.sl + 32 * st + 8 * grp) : zero8<T>();
+        }
+        bfr = ok ? load8<T>(Bm + (int64_t)kk * a.b.sl + 8 * grp) : zero8<T>();
+        fk = (has_f && ok) ? FF[(int64_t)kk * sfl] : 0.f;
+        nfe = fe - fk;
+        colf = ok ? COLF[kk] : 0.f;
+        rk = lam * colf;
+        gk = G[(int64_t)(ok ? kk : L - 1) * sgl];
+        dsd = ok ? WS[WS_DSD * BHL + (int64_t)bh * L + kk] : 0.f;
+    }
+
+    f32x4 dva[4], dka[4], dba[2];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) dva[db] = dka[db] = zero4();
+    dba[0] = dba[1] = zero4();
+    // column sums (diagonal excluded); off-block tiles accumulate dgu without the column factor colf
+    float dgu = 0.f, dfs = 0.f;
+
+    // Query tiles straight into LDS (DMA buffer loads), from the last one down to the block's own tile; 16-bit types
+    // double-buffer them (one barrier per tile), fp32 uses one buffer. The per-query scalars are fetched into
+    // registers by the first wave one tile ahead.
+    DmaStage<T, DH, NWB> dmq, dmd;
+    DmaStage<T, DS, NWB> dmc;
+    const int64_t xq = ((int64_t)(L - 1) * sql + DH) * (int64_t)sizeof(T);   // view extents (bytes)
+    const int64_t xd = ((int64_t)(L - 1) * sdl + DH) * (int64_t)sizeof(T);
+    const int64_t xc = ((int64_t)(L - 1) * scl + DS) * (int64_t)sizeof(T);
+    dmq.init(sql, w, lane);
+    dmd.init(sdl, w, lane);
+    dmc.init(scl, w, lane);
+    const int mlast = (L - 1) / 64 * 64;
+    const int nt = (mlast - ktile0) / 64;         // query tiles after the block; tile t starts at mlast - 64 t
+    float pf_lse = 0.f, pf_dh = 0.f, pf_dd = 0.f, pf_f = 0.f, pf_g = 0.f, pf_rowf = 0.f, pf_gm = 0.f;
+    auto fetch_scalars = [&](int m0) {
+        if (tid < 64) {
+            const int i = m0 + tid;
+            const bool ok = i < L;
+            const int ic = ok ? i : L - 1;
+            pf_lse = ok ? LSE[i] : __builtin_inff();
+            pf_dh = ok ? DELTA[i] : 0.f;
+            pf_dd = ok ? DDEL[i] : 0.f;
+            pf_f = (has_f && ok) ? FF[(int64_t)i * sfl] : 0.f;
+            pf_g = G[(int64_t)ic * sgl];
+            pf_rowf = ok ? ROWF[i] : 0.f;
+            pf_gm = G[(int64_t)m0 * sgl];           // start of the query block
+        }
+    };
+    auto issue_tile = [&](DkvLds<T>& d, int m0) {   // rows >= L read as zero
+        dma_issue<2>(dmq, Q, xq, (int)(m0 * sql * (int64_t)sizeof(T)), d.qs, w);
+        dma_issue<2>(dmd, DO, xd, (int)(m0 * sdl * (int64_t)sizeof(T)), d.ds, w);
+        dma_issue<2>(dmc, C, xc, (int)(m0 * scl * (int64_t)sizeof(T)), d.cs, w);
+        if (tid < 64) {
+            d.lse[tid] = pf_lse;
+            d.dhat[tid] = pf_dh;
+            d.ddel[tid] = pf_dd;
+            d.fq[tid] = pf_f;
+            d.gq[tid] = pf_g;
+            d.rq[tid] = pf_rowf * exp2_le0((pf_gm - ge) * LOG2E);
+            d.ftl[tid] = fmaf(pf_f - fe, LOG2E, -pf_lse);
+            d.ndh[tid] = -pf_dh;
+        }
+    };
+    auto advance = [&](int t) {
+        const int m0 = mlast - 64 * t;
+        if (NBUF == 2) {
+            if (t < nt) {
+                issue_tile(smb[(t + 1) & (NBUF - 1)], m0 - 64);
+                if (t + 1 < nt) fetch_scalars(m0 - 128);
+            }
+        } else if (t > 0) {
+            __syncthreads();
+            issue_tile(smb[0], m0);
+            __syncthreads();
+            if (t < nt) fetch_scalars(m0 - 64);
+        }
+    };
+    fetch_scalars(mlast);
+    issue_tile(smb[0], mlast);
+    if (nt > 0) fetch_scalars(mlast - 64);
+    __syncthreads();
+    for (int t = 0; t < nt; ++t) {
+        advance(t);
+        if (live) {
+            const DkvLds<T>& sm = smb[t & (NBUF - 1)];
+            dkv_tile<T, false>(sm, lane, mlast - 64 * t, k0, L, kf, vf, bfr, fk, nfe, rk, gk, dsd, lam, dgu, dfs, dva,
+                               dka, dba);
+        }
+        if (NBUF == 2) __syncthreads();
+    }
+    advance(nt);
+    if (live) {
+        // the block's own tile: apply the off-block column factors once, in fp32, then the pair path
+        const DkvLds<T>& sm = smb[nt & (NBUF - 1)];
+        dgu *= colf;
+        dba[0] *= rk;
+        dba[1] *= rk;
+        dkv_tile<T, true>(sm, lane, ktile0, k0, L, kf, vf, bfr, fk, nfe, rk, gk, dsd, lam, dgu, dfs, dva, dka, dba);
+    }
+    if (!live) return;
+    const float Dgu = group_sum(dgu), Dfs = group_sum(dfs);
+    const int kk = k0 + lc;
+    if (kk >= L) return;
+    T* dkp = (T*)a.dk.ptr + (int64_t)b * a.dk.sb + (int64_t)h * a.dk.sh + (int64_t)kk * a.dk.sl;
+    T* dvp = (T*)a.dv.ptr + (int64_t)b * a.dv.sb + (int64_t)h * a.dv.sh + (int64_t)kk * a.dv.sl;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+        const int d = db * 16 + 4 * grp;
+        store_row4<T, T>(dkp + d, dka[db] * QSCALE);
+        store_row4<T, T>(dvp + d, dva[db]);
+    }
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+        const int s0 = sb * 16 + 4 * grp;
+        if (a.dcb_dtype == SISA_F32) {
+            float* p = (float*)a.db.ptr + (int64_t)b * a.db.sb + (int64_t)h * a.db.sh + (int64_t)kk * a.db.sl;
+            *reinterpret_cast<f32x4*>(p + s0) = dba[sb];
+        } else {
+            T* p = (T*)a.db.ptr + (int64_t)b * a.db.sb + (int64_t)h * a.db.sh + (int64_t)kk * a.db.sl;
+            store_row4<T, T>(p + s0, dba[sb]);
+        }
+    }
+    if (grp == 0) {
+        const int64_t o = (int64_t)bh * L + kk;
+        a.dg[o] = WS[WS_RG * BHL + o] - lam * Dgu;
+        if (has_f) a.df[o] = WS[WS_RF * BHL + o] - Dfs;
+    }
+}
+
+}  // namespace
+
+namespace sisa {
+namespace detail {
+
+template <class T>
+static int launch_dq_dkv(const sisa_attn_bwd_args* a, hipStream_t st) {
+    const dim3 grid((unsigned)(sisa::cdiv(a->L, 64) * a->B * a->H));
+    attn_bwd_dq_kernel<T><<<grid, NTHB, 0, st>>>(*a);
+    const int rc = sisa::launch_status("sisa_attn_bwd (dq)");
+    if (rc) return rc;
+    attn_bwd_dkv_kernel<T><<<grid, NTHB, 0, st>>>(*a);
+    return sisa::launch_status("sisa_attn_bwd (dkv)");
+}
+
+int attn_bwd_dq_dkv(const sisa_attn_bwd_args* a, hipStream_t st) {
+    switch (a->dtype) {
+        case SISA_BF16: return launch_dq_dkv<__bf16>(a, st);
+        case SISA_F16: return launch_dq_dkv<_Float16>(a, st);
+        default: return launch_dq_dkv<float>(a, st);
+    }
+}
+
+}  // namespace detail
+}  // namespace sisa
