@@ -1,5 +1,5 @@
-// SISA attention for gfx950: decay factors, forward, exact-delta backward (query-owned and key-owned kernels) and
-// the deterministic fp64 dlambda reduction.
+// SISA attention for gfx950: decay factors, forward, exact-delta backward (query-owned and key-owned kernels, in
+// attention_bwd.hip) and the deterministic fp64 dlambda reduction, with the C entry points.
 //
 //   s_ij = q_i.k_j / 8 + lam * exp(g_i - g_j) * (c_i.b_j) + (F_i - F_j)        (j <= i)
 //   o_i  = sum_j softmax_j(s_ij) v_j
