@@ -3,7 +3,7 @@
 One step = the work of ``sisa_fused`` forward + backward on one batch: HIP prep forward (scans, factors, rotation),
 attention forward, exact-delta attention backward (dq kernel, dkv kernel, fp64 dlambda) and prep backward, at
 B=4, T=4096, H=8, d_head=64, d_state=32, bf16 (BASELINE.json metric; configs[1] is the T=2048 variant of it).
-Inputs are synthetic (oracle.reference.config_inputs('ns'), seeded on the CPU) and resident in HBM before timing.
+Inputs are synthetic (sisa_amd.workloads.config_inputs('ns'), seeded on the CPU) and resident in HBM before timing.
 sisa_fused's non-finite input guard (two small reductions and an asynchronous device assert per call in the default
 check mode) is left out of the timed step: it checks inputs and is not part of the attention arithmetic; on a fresh
 box its device-assert kernel was seen to slow the following attention launches of that process severalfold.
@@ -164,7 +164,7 @@ def bench_ce(steps: int, warmup: int) -> dict:
     in HBM, timed per phase with HIP events on the current stream."""
     import torch
 
-    from oracle.reference import config_inputs
+    from sisa_amd.workloads import config_inputs
     from sisa_amd.kernels import linear_ce as LC
 
     dev = torch.device("cuda:0")
@@ -472,7 +472,7 @@ def main():
         sys.exit(2)
     import torch
 
-    from oracle.reference import config_inputs
+    from sisa_amd.workloads import config_inputs
     from sisa_amd import backends
     from sisa_amd.kernels import attention as A
     from sisa_amd.kernels import fused_prep as FP
