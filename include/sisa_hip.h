@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SISA_ABI_VERSION 2
+#define SISA_ABI_VERSION 3
 
 enum sisa_dtype { SISA_F32 = 0, SISA_BF16 = 1, SISA_F16 = 2, SISA_F64 = 3 };
 
@@ -77,7 +77,7 @@ typedef struct {
 /* Workspace (bytes) of sisa_attn_bwd: six (B,H,L) fp32 row buffers. */
 int64_t sisa_attn_bwd_workspace_bytes(int32_t B, int32_t H, int32_t L);
 
-/* Exact-delta backward: dq, dk, dv, dc, db, dg, dF and dlambda.
+/* Backward: dq, dk, dv, dc, db, dg, dF and dlambda, exact-delta scheme by default (`exact`).
  * Replaces `_bwd_dq` (src/sisa/kernels/attention.py:300-491), `_bwd_dkv` (attention.py:495-663), the fp64 dlambda
  * reduction (attention.py:781-783) and the host core `attn_backward` (attention.py:730-784). */
 typedef struct {
@@ -99,6 +99,9 @@ typedef struct {
     float* df;                 /* (B,H,L) contiguous output, NULL when f.ptr is NULL */
     float* dlam;               /* (H,) output */
     void* workspace;           /* sisa_attn_bwd_workspace_bytes(B,H,L) bytes */
+    int32_t exact;             /* nonzero: exact-delta scheme (the public path); 0: FlashAttention-standard delta
+                                  o.do everywhere, diagonal included (comparison mode of the reference's kernels,
+                                  EXACT=False, attention.py:47-48); o32 is ignored when 0 */
 } sisa_attn_bwd_args;
 
 int sisa_factors(const sisa_factors_args* a, void* stream);

@@ -160,7 +160,122 @@ def analytic_grads64(q, k, v, c, b, g, lam, Fg, do):
     out = dict(o=P @ v, dq=(dSf @ k) * sc, dk=(dSf.T @ q) * sc, dv=P.T @ do, dc=lam * (dSE @ b),
                db=lam * (dSE.T @ c), dg=lam * (dSU.sum(1) - dSU.sum(0)), dlam=(dSf * U).sum())
     out["dF"] = (dS.sum(1) - dS.sum(0)) if Fg is not None else None
+    # sum over rows of |row part of dlam|: with |dlam| it gives the condition number of the dlam sum
+    out["dlam_abs"] = ((dS * U).sum(1) + dSd * torch.diagonal(CB)).abs().sum()
     return out
+
+
+def revcumsum(x: torch.Tensor) -> torch.Tensor:
+    """Reverse cumulative sum along the last axis in fp64: d log(decay) from dg, d log(forget) from dF."""
+    return x.double().flip(-1).cumsum(-1).flip(-1)
+
+
+def direct_grads_mp(q, k, v, c, b, g, lam, Fg, do, digits: int = 60) -> dict:
+    """The gradients of one (b, h) from the *direct* formula dS_tj = P_tj (dP_tj - T_t), diagonal included, evaluated
+    in ``digits``-digit mpmath arithmetic (tests/test_attention_diag.py:196-238 of the reference uses the same
+    check). A different formula from analytic_grads64's delta-free diagonal, and free of fp64 cancellation, so it
+    pins that function where P_tt rounds to 1 in fp64. 2-D fp64 CPU inputs, small L only. Returns fp64 tensors."""
+    import mpmath
+
+    ctx = mpmath.mp.clone()
+    ctx.dps = digits
+    mpf = ctx.mpf
+    L, D = q.shape
+    S = c.shape[1]
+
+    def rows(x):
+        return [[mpf(float(e)) for e in r] for r in x.tolist()]
+    Q, K, V, C, Bv, DO = rows(q), rows(k), rows(v), rows(c), rows(b), rows(do)
+    G = [mpf(float(e)) for e in g.tolist()]
+    FF = [mpf(float(e)) for e in Fg.tolist()] if Fg is not None else [mpf(0)] * L
+    lm = mpf(float(lam))
+    inv = 1 / ctx.sqrt(D)
+
+    def dot(x, y):
+        return ctx.fsum(a * bb for a, bb in zip(x, y))
+    dec = [[ctx.exp(G[i] - G[j]) if j <= i else mpf(0) for j in range(L)] for i in range(L)]
+    cb = [[dot(C[i], Bv[j]) for j in range(L)] for i in range(L)]
+    P = [[mpf(0)] * L for _ in range(L)]
+    for i in range(L):
+        sc = [dot(Q[i], K[j]) * inv + lm * dec[i][j] * cb[i][j] + (FF[i] - FF[j]) for j in range(i + 1)]
+        top = max(sc)
+        w = [ctx.exp(x - top) for x in sc]
+        tot = ctx.fsum(w)
+        for j in range(i + 1):
+            P[i][j] = w[j] / tot
+    dP = [[dot(DO[i], V[j]) for j in range(L)] for i in range(L)]
+    dS = [[mpf(0)] * L for _ in range(L)]
+    for i in range(L):
+        Ti = ctx.fsum(P[i][j] * dP[i][j] for j in range(i + 1))
+        for j in range(i + 1):
+            dS[i][j] = P[i][j] * (dP[i][j] - Ti)
+
+    def mat(f, n, m):
+        return torch.tensor([[float(f(i, j)) for j in range(m)] for i in range(n)], dtype=torch.float64)
+    o = mat(lambda i, d: ctx.fsum(P[i][j] * V[j][d] for j in range(L)), L, D)
+    dq = mat(lambda i, d: ctx.fsum(dS[i][j] * K[j][d] for j in range(L)) * inv, L, D)
+    dk = mat(lambda j, d: ctx.fsum(dS[i][j] * Q[i][d] for i in range(L)) * inv, L, D)
+    dv = mat(lambda j, d: ctx.fsum(P[i][j] * DO[i][d] for i in range(L)), L, D)
+    dc = mat(lambda i, d: lm * ctx.fsum(dS[i][j] * dec[i][j] * Bv[j][d] for j in range(L)), L, S)
+    db = mat(lambda j, d: lm * ctx.fsum(dS[i][j] * dec[i][j] * C[i][d] for i in range(L)), L, S)
+    term = [[dS[i][j] * dec[i][j] * cb[i][j] for j in range(L)] for i in range(L)]
+    dg = [lm * (ctx.fsum(term[t]) - ctx.fsum(term[i][t] for i in range(L))) for t in range(L)]
+    dF = [ctx.fsum(dS[t]) - ctx.fsum(dS[i][t] for i in range(L)) for t in range(L)]
+    dlam = ctx.fsum(ctx.fsum(r) for r in term)
+    vec = lambda xs: torch.tensor([float(x) for x in xs], dtype=torch.float64)   # noqa: E731
+    return dict(o=o, dq=dq, dk=dk, dv=dv, dc=dc, db=db, dg=vec(dg), dF=vec(dF),
+                dlam=torch.tensor(float(dlam), dtype=torch.float64))
+
+
+def diag_inputs(B: int, H: int, L: int, seed: int, dt=torch.bfloat16, forget=None, lam=0.31, decay: str = "model",
+                layout: str = "bhld", qk: float = 1.0, cbs: float = 0.6, k_of_q: float | None = None,
+                b_of_c: float | None = None, device="cpu") -> dict:
+    """Inputs of the strong-forgetting / diagonal judge (tests/test_attention_diag.py:242-275 of the reference),
+    drawn from a CPU generator.
+
+    forget: one mean increment c per head (F_t - F_{t-1} = min(c + 2 N(0,1), 0)) or None (no forget term).
+    decay: 'model' (g increments -softplus(N(-2.5, 1))), 'fast' (min(-20 + 2 N(0,1), 0)) or 'zero'.
+    k_of_q / b_of_c: k = q * k_of_q (diagonal dominated by q.k) / b = c * b_of_c (dominated by c.b).
+    layout 'blhd': tensors are (B,H,L,.) views of (B,L,H,.) memory (the model's layout)."""
+    gen = torch.Generator().manual_seed(seed)
+
+    def rn(*shape):
+        return torch.randn(*shape, generator=gen)
+    q, k, v = qk * rn(B, H, L, 64), qk * rn(B, H, L, 64), rn(B, H, L, 64)
+    c, b = cbs * rn(B, H, L, 32), cbs * rn(B, H, L, 32)
+    if k_of_q is not None:
+        k = q * k_of_q
+    if b_of_c is not None:
+        b = c * b_of_c
+    do = rn(B, H, L, 64)
+    if decay == "model":
+        inc = -F.softplus(rn(B, H, L) - 2.5)
+    elif decay == "fast":
+        inc = (2.0 * rn(B, H, L) - 20.0).clamp(max=0.0)
+    else:
+        inc = torch.zeros(B, H, L)
+    g = inc.cumsum(-1).float().contiguous()
+    Fg = None
+    if forget is not None:
+        steps = torch.stack([(mu + 2.0 * rn(B, L)).clamp(max=0.0) for mu in forget], 1)
+        Fg = steps.cumsum(-1).float().contiguous()
+    lams = list(lam) if isinstance(lam, (list, tuple)) else [lam] * H
+    lamt = torch.tensor(lams, dtype=torch.float32)
+
+    def place(x):
+        x = x.to(dt)
+        if layout == "blhd":
+            x = x.transpose(1, 2).contiguous().transpose(1, 2)
+        return x.contiguous() if layout == "bhld" else x
+    out = dict(q=place(q), k=place(k), v=place(v), c=place(c), b=place(b), g=g, lam=lamt, F=Fg, do=place(do))
+
+    def move(t):
+        if t is None:
+            return None
+        if layout == "blhd" and t.dim() == 4:   # keep the (B,L,H,.) memory order on the device
+            return t.transpose(1, 2).to(device).transpose(1, 2)
+        return t.to(device)
+    return {n: move(t) for n, t in out.items()}
 
 
 def fa_emulation(ins: dict, mode: str = "fa", rb: int | None = None) -> dict:

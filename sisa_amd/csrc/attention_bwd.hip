@@ -31,7 +31,7 @@ struct RowSums {
 template <class T, bool DIAG>
 SISA_DEV void dq_tile(const DqLds<T>& sm, int lane, int n0, int q0, int L, const frag8<T> (&qf)[2],
                       const frag8<T>& cfr, const frag8<T> (&dof)[2], float fq, float rs, float gq, float lse,
-                      float dhat, float lam, RowSums& R, f32x4 (&dqa)[4], f32x4 (&dca)[2]) {
+                      float dhat, float lam, bool exact, RowSums& R, f32x4 (&dqa)[4], f32x4 (&dca)[2]) {
     constexpr bool F16 = Anchor<T>::on;
     constexpr bool ANCH = F16 && !DIAG;
     const int grp = lane >> 4, lc = lane & 15;
@@ -70,16 +70,19 @@ SISA_DEV void dq_tile(const DqLds<T>& sm, int lane, int n0, int q0, int L, const
                     const float dpd = F16 ? dp[i] : dp[i] - dhat;   // dP - Delta
                     const float ds = pr * dpd;
                     const float dso = eye ? 0.f : ds;
+                    // exact: the diagonal enters the dq/dc products after the loop (delta-free dS_tt);
+                    // FlashAttention-standard mode keeps P_tt (dP_tt - delta) in the GEMM operands
+                    const float dsg = exact ? dso : ds;
                     R.ptt += eye ? pr : 0.f;
                     R.dptt += eye ? dpd : 0.f;
-                    R.xd += eye ? cbv : 0.f;
+                    R.xd += eye ? (exact ? cbv : ds * u) : 0.f;
                     const float po = eye ? 0.f : pr;
                     R.za += po;
                     R.ya += po * u;
                     R.wa += dso;
                     R.xa += dso * u;
-                    dsv[hb][i] = dso;
-                    wv[hb][i] = dso * (lam * dec);
+                    dsv[hb][i] = dsg;
+                    wv[hb][i] = dsg * (lam * dec);
                 }
             } else {
                 const f32x4 cf = lds4f(&cfm[j0]);
@@ -123,6 +126,8 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
     const int H = a.H, L = a.L;
     const int b = bh / H, h = bh % H;
     const bool has_f = a.f.ptr != nullptr;
+    const bool exact = a.exact != 0;
+    const float* O32 = exact ? a.o32 : nullptr;
     const T* Q = (const T*)a.q.ptr + (int64_t)b * a.q.sb + (int64_t)h * a.q.sh;
     const T* K = (const T*)a.k.ptr + (int64_t)b * a.k.sb + (int64_t)h * a.k.sh;
     const T* V = (const T*)a.v.ptr + (int64_t)b * a.v.sb + (int64_t)h * a.v.sh;
@@ -157,23 +162,23 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
             qf[st] = ok ? scale_frag<T>(load8<T>(Q + (int64_t)qq * a.q.sl + 32 * st + 8 * grp), QSCALE) : zero8<T>();
             dof[st] = ok ? load8<T>(DO + (int64_t)qq * a.dout.sl + 32 * st + 8 * grp) : zero8<T>();
             if (ok) {
-                const frag8<T> ov = load8<T>(O + (int64_t)qq * a.o.sl + 32 * st + 8 * grp);
-                f32x4 o32a = zero4(), o32b = zero4();
-                if (a.o32) {
-                    const float* p32 = a.o32 + ((int64_t)bh * L + qq) * DH + 32 * st + 8 * grp;
-                    o32a = *reinterpret_cast<const f32x4*>(p32);
-                    o32b = *reinterpret_cast<const f32x4*>(p32 + 4);
+                // exact mode: Delta'' = o''.do with the fp32 o'' as stored (no snapping to the DT o: a snapped element
+                // carries up to the snap threshold of error, not proportional to the non-dominant mass of the row)
+                f32x4 oa, ob;
+                if (O32) {
+                    const float* p32 = O32 + ((int64_t)bh * L + qq) * DH + 32 * st + 8 * grp;
+                    oa = *reinterpret_cast<const f32x4*>(p32);
+                    ob = *reinterpret_cast<const f32x4*>(p32 + 4);
+                } else {
+                    const frag8<T> ov = load8<T>(O + (int64_t)qq * a.o.sl + 32 * st + 8 * grp);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        oa[j] = (float)ov[j];
+                        ob[j] = (float)ov[j + 4];
+                    }
                 }
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    float o = (float)ov[j];
-                    if (a.o32) {
-                        // o'' agrees with the DT o to within 2^-15 relative: use the DT value (attention.py:341-349)
-                        const float o2 = j < 4 ? o32a[j] : o32b[j - 4];
-                        o = (fabsf(o2 - o) <= 3.0517578125e-05f * fabsf(o)) ? o : o2;
-                    }
-                    part += o * (float)dof[st][j];
-                }
+                for (int j = 0; j < 4; ++j) part += oa[j] * (float)dof[st][j] + ob[j] * (float)dof[st][j + 4];
             }
         }
         dhat = group_sum(part);
@@ -251,7 +256,7 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
         advance(t);
         if (live) {
             const DqLds<T>& sm = smb[t & (NBUF - 1)];
-            dq_tile<T, false>(sm, lane, 64 * t, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, R, dqa, dca);
+            dq_tile<T, false>(sm, lane, 64 * t, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, exact, R, dqa, dca);
         }
         if (NBUF == 2) __syncthreads();
     }
@@ -263,20 +268,23 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
         R.ya *= rowfq;
         dca[0] *= rs;
         dca[1] *= rs;
-        dq_tile<T, true>(sm, lane, tile0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, R, dqa, dca);
+        dq_tile<T, true>(sm, lane, tile0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, exact, R, dqa, dca);
     }
     if (!live) return;
     const float xat = group_sum(R.xa), yat = group_sum(R.ya), Wa = group_sum(R.wa), Za = group_sum(R.za);
     const float Ptt = group_sum(R.ptt), Dptt = group_sum(R.dptt), Xd = group_sum(R.xd);
     const int qq = q0 + lc;
     if (qq >= L) return;
-    // self-normalised exact delta and the delta-free diagonal (attention.py:453-463)
+    // Self-normalised exact delta T^ = Delta + ddel and the delta-free diagonal (attention.py:453-463). ddel is kept
+    // as its own quantity: forming T^ = Delta + ddel and taking T^ - Delta again would quantise ddel to the fp32 ulp
+    // of Delta, an absolute error that dominates every dS of rows whose mass sits on one key. The
+    // FlashAttention-standard mode keeps Delta (ddel = 0) and has the diagonal inside the products already.
     float ssum = Ptt + Za;
     ssum = ssum > 0.f ? ssum : 1.f;
     const float x0 = Dptt;   // dP_tt - Delta
-    const float tt = dhat + (Ptt * x0 + Wa) / ssum;
-    const float dstt = Ptt * (Za * x0 - Wa) / ssum;
-    const float dl_row = xat + (dhat - tt) * yat;
+    const float ddel = exact ? (Ptt * x0 + Wa) / ssum : 0.f;
+    const float dstt = exact ? Ptt * (Za * x0 - Wa) / ssum : 0.f;
+    const float dl_row = xat - ddel * yat;
     const float dsq = (float)cvt<T>(dstt);           // one DT rounding of the diagonal operands
     const float dsc = (float)cvt<T>(dstt * lam);
     const T* krow = K + (int64_t)qq * skl;
@@ -309,11 +317,11 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
     if (grp == 0) {
         const int64_t o = (int64_t)bh * L + qq;
         WS[WS_DELTA * BHL + o] = dhat;
-        WS[WS_DDEL * BHL + o] = tt - dhat;
+        WS[WS_DDEL * BHL + o] = ddel;
         WS[WS_DSD * BHL + o] = dstt;
         WS[WS_RG * BHL + o] = lam * dl_row;
-        WS[WS_RL * BHL + o] = dl_row + dstt * Xd;
-        WS[WS_RF * BHL + o] = Wa - Za * (tt - dhat);
+        WS[WS_RL * BHL + o] = exact ? dl_row + dstt * Xd : dl_row + Xd;   // FA: Xd = dS_tt cb_tt
+        WS[WS_RF * BHL + o] = Wa - Za * ddel;
     }
 }
 
@@ -337,7 +345,8 @@ struct __attribute__((aligned(16))) DkvLds {
 template <class T, bool PAIR>
 SISA_DEV void dkv_tile(const DkvLds<T>& sm, int lane, int m0, int k0, int L, const frag8<T> (&kf)[2],
                        const frag8<T> (&vf)[2], const frag8<T>& bfr, float fk, float nfe, float rk, float gk, float dsd,
-                       float lam, float& dgu, float& dfs, f32x4 (&dva)[4], f32x4 (&dka)[4], f32x4 (&dba)[2]) {
+                       float lam, bool exact, float& dgu, float& dfs, f32x4 (&dva)[4], f32x4 (&dka)[4],
+                       f32x4 (&dba)[2]) {
     constexpr bool F16 = Anchor<T>::on;
     constexpr bool ANCH = F16 && !PAIR;
     const int grp = lane >> 4, lc = lane & 15;
@@ -380,8 +389,11 @@ SISA_DEV void dkv_tile(const DkvLds<T>& sm, int lane, int m0, int k0, int L, con
                     dgu += dso * u;
                     dfs += dso;
                     pv[hb][i] = p;
-                    kv[hb][i] = eye ? dsd : dso;
-                    bv[hb][i] = (eye ? dsd : (strict ? dsh : 0.f)) * (lam * dec);
+                    // the diagonal: the dq kernel's delta-free dS_tt (exact) or P_tt (dP_tt - delta) (FA mode,
+                    // where T^ - delta = 0 makes dsx = dsh)
+                    const float dse = exact ? dsd : dsh;
+                    kv[hb][i] = eye ? dse : dso;
+                    bv[hb][i] = (eye ? dse : (strict ? dsh : 0.f)) * (lam * dec);
                 }
             } else {
                 const f32x4 rq = lds4f(&rqm[i0]);
@@ -431,6 +443,7 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
     const int H = a.H, L = a.L;
     const int b = bh / H, h = bh % H;
     const bool has_f = a.f.ptr != nullptr;
+    const bool exact = a.exact != 0;
     const T* Q = (const T*)a.q.ptr + (int64_t)b * a.q.sb + (int64_t)h * a.q.sh;
     const T* K = (const T*)a.k.ptr + (int64_t)b * a.k.sb + (int64_t)h * a.k.sh;
     const T* V = (const T*)a.v.ptr + (int64_t)b * a.v.sb + (int64_t)h * a.v.sh;
@@ -548,8 +561,8 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
         advance(t);
         if (live) {
             const DkvLds<T>& sm = smb[t & (NBUF - 1)];
-            dkv_tile<T, false>(sm, lane, mlast - 64 * t, k0, L, kf, vf, bfr, fk, nfe, rk, gk, dsd, lam, dgu, dfs, dva,
-                               dka, dba);
+            dkv_tile<T, false>(sm, lane, mlast - 64 * t, k0, L, kf, vf, bfr, fk, nfe, rk, gk, dsd, lam, exact, dgu,
+                               dfs, dva, dka, dba);
         }
         if (NBUF == 2) __syncthreads();
     }
@@ -560,7 +573,8 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
         dgu *= colf;
         dba[0] *= rk;
         dba[1] *= rk;
-        dkv_tile<T, true>(sm, lane, ktile0, k0, L, kf, vf, bfr, fk, nfe, rk, gk, dsd, lam, dgu, dfs, dva, dka, dba);
+        dkv_tile<T, true>(sm, lane, ktile0, k0, L, kf, vf, bfr, fk, nfe, rk, gk, dsd, lam, exact, dgu, dfs, dva, dka,
+                                 dba);
     }
     if (!live) return;
     const float Dgu = group_sum(dgu), Dfs = group_sum(dfs);

@@ -15,7 +15,7 @@ from ctypes import POINTER, Structure, c_char_p, c_float, c_int, c_int32, c_int6
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "libsisa_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 F32, BF16, F16, F64 = 0, 1, 2, 3
 _DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.float64: F64}
@@ -43,7 +43,8 @@ class AttnBwdArgs(Structure):
                 ("lam", c_void_p), ("s_lam", c_int64), ("rowf", c_void_p), ("colf", c_void_p),
                 ("o", View), ("o32", c_void_p), ("lse", c_void_p), ("dout", View),
                 ("dq", View), ("dk", View), ("dv", View), ("dc", View), ("db", View),
-                ("dg", c_void_p), ("df", c_void_p), ("dlam", c_void_p), ("workspace", c_void_p)]
+                ("dg", c_void_p), ("df", c_void_p), ("dlam", c_void_p), ("workspace", c_void_p),
+                ("exact", c_int32)]
 
 
 class PrepFwdArgs(Structure):

@@ -112,8 +112,6 @@ def attn_backward(q, k, v, c, b, g, fgate, rowf, colf, lam, o, lse, do, exact=Tr
     dc/db). ``o32`` is the self-normalised fp32 o'' of ``attn_forward(want32=True)`` (None: delta = o.do).
     Returns ``(dq, dk, dv, dc, db, dg, dlam (H,), dF or None)``. Reference: attention.py:730-784.
     """
-    if not exact:
-        raise NotImplementedError("the HIP backward implements the exact-delta scheme only (exact=True)")
     B, H, L, D = q.shape
     dev = q.device
     has_f = fgate is not None
@@ -135,7 +133,7 @@ def attn_backward(q, k, v, c, b, g, fgate, rowf, colf, lam, o, lse, do, exact=Tr
     dF = torch.empty((B, H, L), **f32) if has_f else None
     dlam = torch.empty((H,), **f32)
     ws = torch.empty((_lib.workspace_bytes("sisa_attn_bwd_workspace_bytes", B, H, L) // 4,), **f32)
-    has32 = o32 is not None and o32 is not o
+    has32 = bool(exact) and o32 is not None and o32 is not o
     if has32:
         assert o32.shape == (B, H, L, D) and o32.is_contiguous() and o32.dtype == torch.float32
     args = _lib.AttnBwdArgs(B, H, L, _lib.dtype_code(q.dtype), _lib.dtype_code(dc.dtype),
@@ -144,7 +142,7 @@ def attn_backward(q, k, v, c, b, g, fgate, rowf, colf, lam, o, lse, do, exact=Tr
                             rowf.data_ptr(), colf.data_ptr(), _lib.view(o), o32.data_ptr() if has32 else None,
                             lse.data_ptr(), _lib.view(do), _lib.view(dq), _lib.view(dk), _lib.view(dv),
                             _lib.view(dc), _lib.view(db), dg.data_ptr(), _lib.ptr(dF), dlam.data_ptr(),
-                            ws.data_ptr())
+                            ws.data_ptr(), 1 if exact else 0)
     _lib.call("sisa_attn_bwd", args, q)
     return dq, dk, dv, dc, db, dg, dlam, dF
 

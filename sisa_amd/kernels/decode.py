@@ -26,7 +26,9 @@ def sisa_decode_hip(q: Tensor, k: Tensor, v: Tensor, c: Tensor, b: Tensor, g_q: 
                     f_q: Tensor | None, f_k: Tensor | None, q_start: int) -> Tensor:
     """Exact SISA attention of the query rows ``q_start .. q_start+M-1`` against keys ``0 .. N-1``: ``q, c``
     ``(B,H,M,64|32)``, ``k, v, b`` ``(B,H,N,64|32)`` in one dtype, ``g_q, f_q`` ``(B,H,M)`` and ``g_k, f_k``
-    ``(B,H,N)`` float32, ``lam`` ``(H,)``. Returns ``(B,H,M,64)`` float32 (inference only: no autograd)."""
+    ``(B,H,N)`` float32, ``lam`` ``(H,)``. Returns ``(B,H,M,64)`` float32 (inference only: no autograd). Any M: a
+    launch takes fewer than 65,536 (batch, head, query) rows, so longer query blocks (chunked prefill into a filled
+    cache) run as several launches over row ranges."""
     B, H, M, D = q.shape
     N = k.shape[2]
     if D != 64 or c.shape[-1] != 32:
@@ -44,6 +46,22 @@ def sisa_decode_hip(q: Tensor, k: Tensor, v: Tensor, c: Tensor, b: Tensor, g_q: 
     f_q = None if f_q is None else f_q.float()
     f_k = None if f_k is None else f_k.float()
     lam = lam.float()
+    rows = ROWS_PER_LAUNCH // (B * H)
+    if rows < 1:
+        raise ValueError(f"sisa_decode_hip: B*H = {B * H} query heads exceed one launch ({ROWS_PER_LAUNCH})")
+    parts = []
+    for m0 in range(0, M, rows):       # the grid holds fewer than 65,536 query rows: longer blocks go in pieces
+        m1 = min(M, m0 + rows)
+        parts.append(_launch(q[:, :, m0:m1], k, v, c[:, :, m0:m1], b, g_q[:, :, m0:m1], g_k,
+                             None if f_q is None else f_q[:, :, m0:m1], f_k, lam, q_start + m0, N))
+    return parts[0] if len(parts) == 1 else torch.cat(parts, 2)
+
+
+ROWS_PER_LAUNCH = 65535
+
+
+def _launch(q, k, v, c, b, g_q, g_k, f_q, f_k, lam, q_start, N):
+    B, H, M, _ = q.shape
     out = torch.empty((B, H, M, 64), device=q.device, dtype=torch.float32)
     ws = torch.empty(_lib.workspace_bytes("sisa_decode_workspace_bytes", B, H, M, N) // 4, device=q.device,
                      dtype=torch.float32)

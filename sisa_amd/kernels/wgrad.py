@@ -11,7 +11,7 @@ from torch import Tensor
 
 from . import _lib
 
-__all__ = ["wgrad_hip", "linear_hip"]
+__all__ = ["wgrad_hip", "linear_hip", "row_pieces"]
 
 TM = 64
 
@@ -23,14 +23,39 @@ def _rows16(t: Tensor) -> Tensor:
     return t2
 
 
+# One launch addresses each operand through a 32-bit byte offset: a row range of an operand stays below 2 GiB.
+OPERAND_LIMIT = 1 << 31
+
+
+def row_pieces(M: int, lda: int, ldb: int, elem: int = 2) -> list[tuple[int, int]]:
+    """Row ranges [r0, r1) of the reduction axis, each small enough for one launch (both operands' ranges below
+    2 GiB), every range but the last a multiple of 64 rows."""
+    per_row = max(lda, ldb) * elem
+    cap = (OPERAND_LIMIT - 1) // per_row
+    cap = max(TM, cap // TM * TM)
+    return [(r, min(M, r + cap)) for r in range(0, M, cap)] if M > 0 else []
+
+
 def wgrad_hip(dy: Tensor, x: Tensor, out: Tensor | None = None, nsplit: int | None = None) -> Tensor:
     """``dy^T x`` in fp32 for ``dy`` ``(..., N)`` and ``x`` ``(..., K)`` of one 16-bit dtype (the leading dims are
-    the reduction); returns ``(N, K)`` float32 (written into ``out`` when given)."""
+    the reduction); returns ``(N, K)`` float32 (written into ``out`` when given). Operands of 2 GiB or more are
+    reduced in row ranges (see :func:`row_pieces`) whose fp32 results are added in range order."""
     if dy.dtype != x.dtype or dy.dtype not in (torch.bfloat16, torch.float16):
         raise TypeError(f"wgrad_hip: dy {dy.dtype} and x {x.dtype} must be one of bf16/fp16")
     a, b = _rows16(dy), _rows16(x)
     if a.shape[0] != b.shape[0]:
         raise ValueError(f"wgrad_hip: {a.shape[0]} rows of dy vs {b.shape[0]} of x")
+    pieces = row_pieces(a.shape[0], a.stride(0), b.stride(0), a.element_size())
+    if len(pieces) > 1:
+        out = _wgrad_launch(a[pieces[0][0]:pieces[0][1]], b[pieces[0][0]:pieces[0][1]], out, nsplit)
+        part = torch.empty_like(out)
+        for r0, r1 in pieces[1:]:
+            out += _wgrad_launch(a[r0:r1], b[r0:r1], part, nsplit)
+        return out
+    return _wgrad_launch(a, b, out, nsplit)
+
+
+def _wgrad_launch(a: Tensor, b: Tensor, out: Tensor | None, nsplit: int | None) -> Tensor:
     M, N = a.shape
     K = b.shape[1]
     lib = _lib.load()
@@ -38,14 +63,14 @@ def wgrad_hip(dy: Tensor, x: Tensor, out: Tensor | None = None, nsplit: int | No
     per = -(-M // s)
     per = -(-per // TM) * TM
     if out is None:
-        out = torch.empty((N, K), device=dy.device, dtype=torch.float32)
+        out = torch.empty((N, K), device=a.device, dtype=torch.float32)
     elif out.shape != (N, K) or out.dtype != torch.float32 or out.stride(1) != 1:
         raise ValueError("wgrad_hip: out must be an (N, K) float32 tensor with unit column stride")
     ws_bytes = int(lib.sisa_wgrad_workspace_bytes(M, N, K, s))
-    ws = torch.empty(max(ws_bytes // 4, 1), device=dy.device, dtype=torch.float32) if ws_bytes else None
-    args = _lib.WgradArgs(M, N, K, _lib.dtype_code(dy.dtype), s, per, a.data_ptr(), a.stride(0), b.data_ptr(),
+    ws = torch.empty(max(ws_bytes // 4, 1), device=a.device, dtype=torch.float32) if ws_bytes else None
+    args = _lib.WgradArgs(M, N, K, _lib.dtype_code(a.dtype), s, per, a.data_ptr(), a.stride(0), b.data_ptr(),
                           b.stride(0), out.data_ptr(), out.stride(0), _lib.ptr(ws))
-    _lib.call("sisa_wgrad", args, dy)
+    _lib.call("sisa_wgrad", args, a)
     return out
 
 

@@ -269,13 +269,21 @@ def test_north_star_shape_properties():
     o2, g2 = call(leaves(ins), do)
     assert all(torch.equal(g1[n], g2[n]) for n in g1) and torch.equal(o1, o2)
     assert all(bool(torch.isfinite(t).all()) for t in [o1, *g1.values()])
-    # fp64 truth on batch row 0 (all heads): rows are independent across the batch
-    sub = {n: (t[:1] if (t is not None and n != "lam") else t) for n, t in ins.items()}
-    T = R.truth64(sub)
-    for n in ("o", "dq", "dk", "dv", "dc", "db", "dg", "dF"):
-        x = o1 if n == "o" else g1[n]
-        e = R.rel(x[:1], T[n])
-        assert e < 2e-2, f"{n}: {e:.3e}"
+    # fp64 truth one batch row at a time (all heads; rows are independent, dlambda is their sum)
+    dlam64 = torch.zeros(H, dtype=torch.float64, device=DEV)
+    for r in range(B):
+        sub = {n: (t[r:r + 1] if (t is not None and n != "lam") else t) for n, t in ins.items()}
+        T = R.truth64(sub)
+        dlam64 += T["dlam"].double()
+        if r == 0:
+            for n in ("o", "dq", "dk", "dv", "dc", "db", "dg", "dF"):
+                x = o1 if n == "o" else g1[n]
+                e = R.rel(x[:1], T[n])
+                assert e < 2e-2, f"{n}: {e:.3e}"
+        del T
+    for h in range(H):
+        e = R.rel(g1["dlam"][h:h + 1], dlam64[h:h + 1])
+        assert e < 2e-2, f"dlam head {h}: {e:.3e}"
 
 
 def test_config2_long_context_head_subset():

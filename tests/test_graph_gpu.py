@@ -38,7 +38,7 @@ def _step(proj, z, lam, dy, H):
     return o, DP, dlam, DZ
 
 
-@pytest.mark.parametrize("B,L,H", [(1, 1000, 4), (2, 2048, 8)])
+@pytest.mark.parametrize("B,L,H", [(1, 1000, 4), (4, 2048, 8)])   # (4, 2048, 8): config 1
 def test_layer_step_graph_replays(B, L, H):
     from sisa_amd import backends
     print(f"[graph] B={B} L={L} H={H}", flush=True)

@@ -305,3 +305,16 @@ def test_hip_attention_refuses_cpu_tensors():
     with pytest.raises((ValueError, RuntimeError)):
         sisa_attention_hip(*(ins[n] for n in R.IN_NAMES))
     assert math.isfinite(float(ins["q"].float().sum()))
+
+
+def test_wgrad_row_pieces():
+    """The weight-gradient launches keep each operand's row range below 2 GiB (32-bit buffer offsets)."""
+    from sisa_amd.kernels.wgrad import OPERAND_LIMIT, row_pieces
+    assert row_pieces(16384, 3280, 768) == [(0, 16384)]
+    M, lda = 400_000, 3280                      # 2.6 GB of dy: beyond one launch
+    pieces = row_pieces(M, lda, 768)
+    assert len(pieces) == 2 and pieces[0][0] == 0 and pieces[-1][1] == M
+    assert all(a1 == b0 for (_, a1), (b0, _) in zip(pieces, pieces[1:]))
+    assert all((r1 - r0) * lda * 2 < OPERAND_LIMIT and (r1 - r0) % 64 == 0 for r0, r1 in pieces[:-1])
+    assert (pieces[-1][1] - pieces[-1][0]) * lda * 2 < OPERAND_LIMIT
+    assert row_pieces(0, 8, 8) == []

@@ -175,7 +175,8 @@ def _decode_inputs(B, H, M, N, dtype, seed, has_f=True):
 
 @pytest.mark.parametrize("B,H,M,N,dtype,has_f", [(1, 12, 1, 1, torch.bfloat16, True), (2, 3, 1, 257, torch.bfloat16, True),
                                                  (1, 2, 5, 1000, torch.float32, True), (3, 2, 1, 4097, torch.float16, False),
-                                                 (1, 16, 2, 16384, torch.bfloat16, True)])
+                                                 (1, 16, 2, 16384, torch.bfloat16, True),
+                                                 (8, 12, 1024, 2048, torch.bfloat16, True)])   # 2 launches
 def test_decode_kernel(B, H, M, N, dtype, has_f):
     from sisa_amd.functional import _attend_rows
     from sisa_amd.kernels.decode import sisa_decode_hip

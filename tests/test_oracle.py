@@ -131,6 +131,76 @@ def test_analytic_grads_vs_autograd():
         assert abs(tot.item() - T["dlam"][h].item()) < 1e-10
 
 
+def _head(ins, bb, h):
+    return [ins[n][bb, h].double().cpu() for n in ("q", "k", "v", "c", "b", "g")] + [
+        ins["lam"][h].double(), None if ins["F"] is None else ins["F"][bb, h].double().cpu(),
+        ins["do"][bb, h].double().cpu()]
+
+
+def _worst_vs(A, M, names=("o", "dq", "dk", "dv", "dc", "db", "dg", "dF", "dlam")):
+    worst = 0.0
+    for n in names:
+        a, m = A[n].reshape(-1), M[n].reshape(-1)
+        worst = max(worst, ((a - m).norm() / m.norm()).item())
+    return worst
+
+
+@pytest.mark.parametrize("forget", [-3.0, -20.0, -40.0, -60.0])
+def test_analytic_grads_vs_mpmath_strong_forgetting(forget):
+    """The delta-free analytic gradients against a 60-digit evaluation of the direct formula (dS = P (dP - T),
+    diagonal included) at L = 10, where P_tt rounds to 1 in fp64 beyond about -30 nats per token: <= 1e-12."""
+    ins = R.diag_inputs(1, 1, 10, seed=7, forget=[forget], lam=0.9)
+    args = _head(ins, 0, 0)
+    A = R.analytic_grads64(*args)
+    M = R.direct_grads_mp(*args)
+    assert _worst_vs(A, M) <= 1e-12
+
+
+def test_mpmath_check_detects_a_dropped_diagonal():
+    """Planted mistake: dq without its diagonal term dS_tt k_t / 8 fails the mpmath check that the oracle passes."""
+    ins = R.diag_inputs(1, 1, 10, seed=7, forget=[-3.0], lam=0.9)
+    args = _head(ins, 0, 0)
+    q, k, v, c, b, g, lam, Fg, do = args
+    M = R.direct_grads_mp(*args)
+    A = R.analytic_grads64(*args)
+    i = torch.arange(q.shape[0])
+    dec = torch.exp((g[:, None] - g[None, :]).clamp(max=0))
+    s = (q @ k.T) / 8 + lam * dec * (c @ b.T) + (Fg[:, None] - Fg[None, :])
+    P = torch.softmax(s.masked_fill(i[:, None] < i[None, :], -math.inf), -1)
+    dP = do @ v.T
+    dS_tt = torch.diagonal(P) * (torch.diagonal(dP) - (P * dP).sum(1))
+    planted = dict(A, dq=A["dq"] - dS_tt[:, None] * k / 8)
+    assert _worst_vs(A, M, ("dq",)) <= 1e-12
+    assert _worst_vs(planted, M, ("dq",)) > 1e-6
+
+
+def test_analytic_grads_vs_autograd_mild_forgetting():
+    """The delta-free analytic gradients against fp64 autograd at mild forgetting, L = 512, lam including 0:
+    <= 1e-10 (the reference's refcheck, tests/test_attention_diag.py:383-388)."""
+    ins = R.diag_inputs(1, 4, 512, seed=8, forget=[-0.05, -1.0, -3.0, -6.0], lam=[0.31, 3.0, 0.0, 0.8],
+                        dt=torch.float64)
+    T = R.truth64(ins)
+    worst = 0.0
+    for h in range(4):
+        A = R.analytic_grads64(*_head(ins, 0, h))
+        for n in ("o", "dq", "dk", "dv", "dc", "db", "dg", "dF"):
+            worst = max(worst, R.rel(A[n], T[n][0, h]))
+        worst = max(worst, abs(A["dlam"].item() - T["dlam"][h].item()) / abs(T["dlam"][h].item()))
+        for n, src in (("dloga", "dg"), ("dlogf", "dF")):
+            worst = max(worst, R.rel(R.revcumsum(A[src]), R.revcumsum(T[src][0, h])))
+    assert worst <= 1e-10
+
+
+def test_diag_inputs_layouts():
+    """The model layout holds the same values as the head-major one, as (B,L,H,.) memory."""
+    a = R.diag_inputs(2, 3, 17, seed=3, forget=[-20.0, -3.0, -1.0])
+    b = R.diag_inputs(2, 3, 17, seed=3, forget=[-20.0, -3.0, -1.0], layout="blhd")
+    for n in ("q", "k", "v", "c", "b", "do"):
+        assert torch.equal(a[n], b[n])
+        assert b[n].transpose(1, 2).is_contiguous() and not b[n].is_contiguous()
+    assert bool((a["F"].diff(dim=-1) <= 0).all()) and bool((a["g"].diff(dim=-1) <= 0).all())
+
+
 @pytest.mark.parametrize("block_q", [1, 7, 64])
 def test_blocked_vs_dense(block_q):
     ins = _rand_ins(H=2, L=70, D=16, S=8, seed=6)

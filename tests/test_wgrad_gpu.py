@@ -72,3 +72,19 @@ def test_linear_hip_bias_columns():
         full = torch.autograd.grad(linear_hip(x, w, b), (b,), dy)[0]
         part = torch.autograd.grad(linear_hip(x, w, b, (40, 52)), (b,), dy)[0]
     assert torch.equal(part[40:52], full[40:52]) and not part[:40].any() and not part[52:].any()
+
+
+def test_wgrad_row_ranges(monkeypatch):
+    """Operands past the one-launch limit are reduced in row ranges and summed in range order: with the limit
+    lowered to a few hundred rows the result matches one launch to fp32 summation order, and fp64 to 2e-6."""
+    from sisa_amd.kernels import wgrad as W
+    gen = torch.Generator().manual_seed(6)
+    M, N, K = 1000, 320, 192
+    dy = torch.randn(M, N, generator=gen).to(DEV).bfloat16()
+    x = torch.randn(M, K, generator=gen).to(DEV).bfloat16()
+    whole = W.wgrad_hip(dy, x)
+    monkeypatch.setattr(W, "OPERAND_LIMIT", 256 * N * 2 + 1)     # 256 rows of dy per launch
+    assert len(W.row_pieces(M, N, K)) == 4
+    pieces = W.wgrad_hip(dy, x)
+    ref = dy.double().t() @ x.double()
+    assert rel_err(pieces, ref) < 2e-6 and rel_err(pieces, whole) < 2e-6
