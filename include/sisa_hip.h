@@ -108,6 +108,18 @@ int sisa_factors(const sisa_factors_args* a, void* stream);
 int sisa_attn_fwd(const sisa_attn_fwd_args* a, void* stream);
 int sisa_attn_bwd(const sisa_attn_bwd_args* a, void* stream);
 
+/* Largest B*H*L that sisa_attn_bwd_noalloc takes: its scratch holds six (B,H,L) fp32 row buffers (24 MiB). */
+#define SISA_NOALLOC_MAX_BHL (1 << 20)
+
+/* sisa_attn_bwd without a caller workspace and without any allocation: `workspace` must be NULL, and the six row
+ * buffers live in the library's static device scratch (one 24 MiB copy per GPU, held until the process ends).
+ * No counterpart in the reference: for callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Limits: B*H*L <= SISA_NOALLOC_MAX_BHL (else SISA_ERR_INVALID); the stream
+ * must belong to the current device. All calls on one GPU share its scratch: calls that overlap on one GPU (on
+ * different streams, or from different threads) race; calls ordered on one stream do not. Results are bitwise those
+ * of sisa_attn_bwd. */
+int sisa_attn_bwd_noalloc(const sisa_attn_bwd_args* a, void* stream);
+
 /* ------------------------------------------------------------------------------------------------ fused prep */
 
 /* proj column layout (src/sisa/kernels/fused_prep.py:71-96): [Q H*64 | K H*64 | V H*64 | B H*32 | C H*32 |

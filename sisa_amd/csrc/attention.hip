@@ -20,6 +20,8 @@
 //   Operands of the sequence-contracted products (P V, dS K, ...) are read from the row-major tiles with the gfx950
 //   LDS transpose read, so no transposed copy is ever stored.
 //   Ownership is exclusive: dq/dc by query blocks, dk/dv/db/dg/dF by key blocks.
+#include <mutex>
+
 #include "attention_common.h"
 
 namespace {
@@ -428,8 +430,8 @@ extern "C" int64_t sisa_attn_bwd_workspace_bytes(int32_t B, int32_t H, int32_t L
     return (int64_t)WS_N * B * H * L * (int64_t)sizeof(float);
 }
 
-extern "C" int sisa_attn_bwd(const sisa_attn_bwd_args* a, void* stream) {
-    SISA_REQUIRE(a != nullptr, "sisa_attn_bwd: null args");
+// Argument checks shared by sisa_attn_bwd and sisa_attn_bwd_noalloc (the workspace pointer included).
+static int check_bwd(const sisa_attn_bwd_args* a) {
     SISA_REQUIRE(a->B >= 1 && a->H >= 1 && a->L >= 1, "sisa_attn_bwd: bad shape B=%d H=%d L=%d", a->B, a->H, a->L);
     SISA_REQUIRE((int64_t)a->B * a->H * sisa::cdiv(a->L, 64) * 512 < ((int64_t)1 << 31),
                  "sisa_attn_bwd: B*H*L too large for one launch");
@@ -452,10 +454,77 @@ extern "C" int sisa_attn_bwd(const sisa_attn_bwd_args* a, void* stream) {
                  "sisa_attn_bwd: a (batch, head) slice of q/k/v/do/c/b spans 2 GiB or more");
     SISA_REQUIRE((a->f.ptr == nullptr) == (a->df == nullptr), "sisa_attn_bwd: f and df must both be given or null");
     SISA_REQUIRE(a->o32 == nullptr || (sisa::aligned16(a->o32) && dt != SISA_F32), "sisa_attn_bwd: bad o32");
-    hipStream_t st = (hipStream_t)stream;
-    switch (dt) {
+    return SISA_OK;
+}
+
+static int launch_bwd_any(const sisa_attn_bwd_args* a, hipStream_t st) {
+    switch (a->dtype) {
         case SISA_BF16: return launch_bwd<__bf16>(a, st);
         case SISA_F16: return launch_bwd<_Float16>(a, st);
         default: return launch_bwd<float>(a, st);
     }
+}
+
+extern "C" int sisa_attn_bwd(const sisa_attn_bwd_args* a, void* stream) {
+    SISA_REQUIRE(a != nullptr, "sisa_attn_bwd: null args");
+    const int rc = check_bwd(a);
+    return rc ? rc : launch_bwd_any(a, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------------------------------------------ no-alloc backward
+// The backward's six (B,H,L) fp32 row buffers in a file-scope device array, for callers that cannot allocate. Every
+// GPU the library runs on holds its own copy (24 MiB) until the process ends. In host code `scratch` names a host-side
+// stand-in, not device memory: its device address is looked up once per device (hipGetSymbolAddress, with that
+// device current) and only that address is ever handed to kernels.
+static __device__ __align__(256) float scratch[WS_N * (int64_t)SISA_NOALLOC_MAX_BHL];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_dev[MAX_DEVICES] = {};   // device address of `scratch`, per device ordinal
+
+// The device address of `scratch` on the current device (looked up on the first call on that device). The stream
+// must belong to the current device.
+int scratch_address(hipStream_t st, float** out) {
+    int dev = -1;
+    SISA_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < MAX_DEVICES,
+                 "sisa_attn_bwd_noalloc: no current device (or ordinal %d >= %d)", dev, MAX_DEVICES);
+    if (st != nullptr) {
+        hipDevice_t sdev = -1;
+        SISA_REQUIRE(hipStreamGetDevice(st, &sdev) == hipSuccess && sdev == dev,
+                     "sisa_attn_bwd_noalloc: the stream belongs to device %d, the current device is %d", (int)sdev,
+                     dev);
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_dev[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            sisa::set_error("sisa_attn_bwd_noalloc: hipGetSymbolAddress of the scratch array failed on device %d: %s",
+                            dev, hipGetErrorString(e));
+            return SISA_ERR_LAUNCH;
+        }
+        g_scratch_dev[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_dev[dev];
+    return SISA_OK;
+}
+}  // namespace
+
+extern "C" int sisa_attn_bwd_noalloc(const sisa_attn_bwd_args* a, void* stream) {
+    SISA_REQUIRE(a != nullptr, "sisa_attn_bwd_noalloc: null args");
+    SISA_REQUIRE(a->workspace == nullptr, "sisa_attn_bwd_noalloc: workspace must be NULL (the library's scratch is "
+                                          "used)");
+    SISA_REQUIRE(a->B >= 1 && a->H >= 1 && a->L >= 1 &&
+                     (int64_t)a->B * a->H * a->L <= (int64_t)SISA_NOALLOC_MAX_BHL,
+                 "sisa_attn_bwd_noalloc: B*H*L = %lld exceeds the scratch limit SISA_NOALLOC_MAX_BHL = %d",
+                 (long long)a->B * a->H * a->L, SISA_NOALLOC_MAX_BHL);
+    hipStream_t st = (hipStream_t)stream;
+    float* ws = nullptr;
+    int rc = scratch_address(st, &ws);
+    if (rc) return rc;
+    sisa_attn_bwd_args b = *a;
+    b.workspace = ws;      // every entry the kernels read is written earlier in the same call: nothing to clear
+    rc = check_bwd(&b);
+    return rc ? rc : launch_bwd_any(&b, st);
 }

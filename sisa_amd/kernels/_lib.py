@@ -113,6 +113,7 @@ SIGNATURES = {
     "sisa_attn_fwd": ([POINTER(AttnFwdArgs), c_void_p], c_int),
     "sisa_attn_bwd_workspace_bytes": ([c_int32, c_int32, c_int32], c_int64),
     "sisa_attn_bwd": ([POINTER(AttnBwdArgs), c_void_p], c_int),
+    "sisa_attn_bwd_noalloc": ([POINTER(AttnBwdArgs), c_void_p], c_int),
     "sisa_prep_fwd": ([POINTER(PrepFwdArgs), c_void_p], c_int),
     "sisa_prep_bwd_workspace_bytes": ([c_int32, c_int32, c_int32], c_int64),
     "sisa_finite_sum": ([c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p], c_int),

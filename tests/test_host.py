@@ -39,7 +39,7 @@ def _header_functions():
 def test_library_exports_every_header_function(lib):
     from sisa_amd.kernels import _lib
     declared = _header_functions()
-    assert len(declared) == 24
+    assert len(declared) == 25
     assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
     out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True, check=True)
     exported = set(re.findall(r"\bT (sisa_\w+)$", out.stdout, re.M))
