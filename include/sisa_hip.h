@@ -108,11 +108,11 @@ int sisa_factors(const sisa_factors_args* a, void* stream);
 int sisa_attn_fwd(const sisa_attn_fwd_args* a, void* stream);
 int sisa_attn_bwd(const sisa_attn_bwd_args* a, void* stream);
 
-/* Largest B*H*L that sisa_attn_bwd_noalloc takes: its scratch holds six (B,H,L) fp32 row buffers (24 MiB). */
+/* Largest B*H*L that sisa_attn_bwd_noalloc takes: its scratch holds the backward workspace for it (32 MiB). */
 #define SISA_NOALLOC_MAX_BHL (1 << 20)
 
 /* sisa_attn_bwd without a caller workspace and without any allocation: `workspace` must be NULL, and the six row
- * buffers live in the library's static device scratch (one 24 MiB copy per GPU, held until the process ends).
+ * buffers live in the library's static device scratch (one 32 MiB copy per GPU, held until the process ends).
  * No counterpart in the reference: for callers that cannot allocate (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). Limits: B*H*L <= SISA_NOALLOC_MAX_BHL (else SISA_ERR_INVALID); the stream
  * must belong to the current device. All calls on one GPU share its scratch: calls that overlap on one GPU (on

@@ -280,11 +280,11 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
     };
     // Advance to tile t (key offset 64 t): afterwards (and after the caller's barrier for two buffers) the tile is in
     // LDS buffer t & (NBUF-1).
-    auto advance = [&](int t) {
+    auto advance_into = [&](int t, FwdLds<T>& nxt) {   // nxt: the buffer that is idle during tile t
         const int n0 = 64 * t;
         if (NBUF == 2) {
             if (n0 + 64 < kend) {
-                issue_tile(smb[(t + 1) & (NBUF - 1)], n0 + 64);
+                issue_tile(nxt, n0 + 64);
                 if (n0 + 128 < kend) fetch_scalars(n0 + 128);
             }
         } else if (t > 0) {
@@ -294,19 +294,30 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
             if (n0 + 64 < kend) fetch_scalars(n0 + 64);
         }
     };
+    auto advance = [&](int t) { advance_into(t, smb[(t + 1) & (NBUF - 1)]); };
     fetch_scalars(0);
     issue_tile(smb[0], 0);
     if (64 < kend) fetch_scalars(64);
     __syncthreads();
     // tiles before the workgroup's first query block: off-block for every wave (one code path in the loop)
     const int nfull = tile0 / 64;
-    for (int t = 0; t < nfull; ++t) {
-        advance(t);
+    auto off_tile = [&](int t, const FwdLds<T>& sm, FwdLds<T>& nxt) {
+        advance_into(t, nxt);
         if (live) {
-            const FwdLds<T>& sm = smb[t & (NBUF - 1)];
             fwd_tile<T, false>(sm, qblk, lane, 64 * t, q0, L, qf, cx0, cx1, onesf, fq, rs, gq, lam, m, l, acc);
         }
         if (NBUF == 2) __syncthreads();
+    };
+    if constexpr (NBUF == 2) {
+        // two tiles per iteration, so that each names its LDS buffers statically (no per-tile address arithmetic)
+        int t = 0;
+        for (; t + 2 <= nfull; t += 2) {
+            off_tile(t, smb[0], smb[NBUF - 1]);
+            off_tile(t + 1, smb[NBUF - 1], smb[0]);
+        }
+        if (t < nfull) off_tile(t, smb[0], smb[NBUF - 1]);
+    } else {
+        for (int t = 0; t < nfull; ++t) off_tile(t, smb[0], smb[0]);
     }
     // the workgroup's own tiles: block 0's (off-block for block 1's waves), then block 1's
     advance(nfull);
@@ -344,20 +355,21 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
     if (grp == 0) a.lse[(int64_t)bh * L + qq] = m + __builtin_amdgcn_logf(ls);
 }
 
-// dlambda_h = sum over (b, t) of the per-row parts, in fp64 with a fixed reduction order (attention.py:781-783).
-__global__ __launch_bounds__(1024) void dlam_kernel(const float* __restrict__ rl, float* __restrict__ dlam, int B,
-                                                   int H, int L) {
-    __shared__ double red[1024];
+// dlambda_h = sum over (b, t) of the per-row parts, in fp64 with a fixed reduction order (attention.py:781-783): the
+// dkv kernel sums each 64-row block; this kernel sums the B * ceil(L/64) block sums of head h.
+__global__ __launch_bounds__(256) void dlam_kernel(const double* __restrict__ blk, float* __restrict__ dlam, int B,
+                                                   int H, int nkt) {
+    __shared__ double red[256];
     const int h = blockIdx.x;
-    const int64_t n = (int64_t)B * L;
+    const int64_t n = (int64_t)B * nkt;
     double s = 0.0;
-    for (int64_t t = threadIdx.x; t < n; t += 1024) {
-        const int64_t bb = t / L, l = t % L;
-        s += (double)rl[(bb * H + h) * (int64_t)L + l];
+    for (int64_t t = threadIdx.x; t < n; t += 256) {
+        const int64_t bb = t / nkt, kt = t % nkt;
+        s += blk[(bb * H + h) * nkt + kt];
     }
     red[threadIdx.x] = s;
     __syncthreads();
-    for (int o = 512; o > 0; o >>= 1) {
+    for (int o = 128; o > 0; o >>= 1) {
         if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
         __syncthreads();
     }
@@ -376,7 +388,7 @@ int launch_bwd(const sisa_attn_bwd_args* a, hipStream_t st) {
     const int rc = sisa::detail::attn_bwd_dq_dkv(a, st);   // the dq and dkv kernels (attention_bwd.hip)
     if (rc) return rc;
     const int64_t BHL = (int64_t)a->B * a->H * a->L;
-    dlam_kernel<<<a->H, 1024, 0, st>>>((const float*)a->workspace + WS_RL * BHL, a->dlam, a->B, a->H, a->L);
+    dlam_kernel<<<a->H, 256, 0, st>>>(ws_block_dlam(a->workspace, BHL), a->dlam, a->B, a->H, (a->L + 63) / 64);
     return sisa::launch_status("sisa_attn_bwd (dlam)");
 }
 
@@ -426,8 +438,14 @@ extern "C" int sisa_attn_fwd(const sisa_attn_fwd_args* a, void* stream) {
     }
 }
 
+// Six (B,H,L) fp32 row buffers, then (B*H, ceil(L/64)) fp64 block sums of dlambda (8-byte aligned).
+static int64_t bwd_workspace_bytes(int64_t B, int64_t H, int64_t L) {
+    const int64_t BHL = B * H * L;
+    return (WS_N * BHL + (BHL & 1)) * (int64_t)sizeof(float) + B * H * ((L + 63) / 64) * (int64_t)sizeof(double);
+}
+
 extern "C" int64_t sisa_attn_bwd_workspace_bytes(int32_t B, int32_t H, int32_t L) {
-    return (int64_t)WS_N * B * H * L * (int64_t)sizeof(float);
+    return bwd_workspace_bytes(B, H, L);
 }
 
 // Argument checks shared by sisa_attn_bwd and sisa_attn_bwd_noalloc (the workspace pointer included).
@@ -472,11 +490,12 @@ extern "C" int sisa_attn_bwd(const sisa_attn_bwd_args* a, void* stream) {
 }
 
 // ------------------------------------------------------------------------------------------------ no-alloc backward
-// The backward's six (B,H,L) fp32 row buffers in a file-scope device array, for callers that cannot allocate. Every
-// GPU the library runs on holds its own copy (24 MiB) until the process ends. In host code `scratch` names a host-side
+// The backward's workspace (six (B,H,L) fp32 row buffers and the fp64 dlambda block sums; for B*H*L <= 2^20 at most
+// 2^20 blocks) in a file-scope device array, for callers that cannot allocate. Every GPU the library runs on holds its
+// own copy (32 MiB) until the process ends. In host code `scratch` names a host-side
 // stand-in, not device memory: its device address is looked up once per device (hipGetSymbolAddress, with that
 // device current) and only that address is ever handed to kernels.
-static __device__ __align__(256) float scratch[WS_N * (int64_t)SISA_NOALLOC_MAX_BHL];
+static __device__ __align__(256) float scratch[(WS_N + 2) * (int64_t)SISA_NOALLOC_MAX_BHL];   // 32 MiB
 
 namespace {
 constexpr int MAX_DEVICES = 64;

@@ -576,6 +576,14 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
         dkv_tile<T, true>(sm, lane, ktile0, k0, L, kf, vf, bfr, fk, nfe, rk, gk, dsd, lam, exact, dgu, dfs, dva, dka,
                                  dba);
     }
+    if (w == 0) {
+        // the block's 64 per-row dlambda parts (written by the dq kernel) summed in fp64 in a fixed butterfly order
+        const int r = ktile0 + lane;
+        double v = r < L ? (double)WS[WS_RL * BHL + (int64_t)bh * L + r] : 0.0;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+        if (lane == 0) ws_block_dlam(a.workspace, BHL)[(int64_t)bh * ((L + 63) / 64) + ktile] = v;
+    }
     if (!live) return;
     const float Dgu = group_sum(dgu), Dfs = group_sum(dfs);
     const int kk = k0 + lc;
