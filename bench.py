@@ -4,9 +4,10 @@ One step = the work of ``sisa_fused`` forward + backward on one batch: HIP prep 
 attention forward, exact-delta attention backward (dq kernel, dkv kernel, fp64 dlambda) and prep backward, at
 B=4, T=4096, H=8, d_head=64, d_state=32, bf16 (BASELINE.json metric; configs[1] is the T=2048 variant of it).
 Inputs are synthetic (sisa_amd.workloads.config_inputs('ns'), seeded on the CPU) and resident in HBM before timing.
-sisa_fused's non-finite input guard (two small reductions and an asynchronous device assert per call in the default
-check mode) is left out of the timed step: it checks inputs and is not part of the attention arithmetic; on a fresh
-box its device-assert kernel was seen to slow the following attention launches of that process severalfold.
+The headline step is the kernels of the path (check mode "off": sisa_fused's non-finite input guard checks inputs
+and is not part of the attention arithmetic). fused_layer_async times the same work as users call it -- sisa_fused
+forward and backward through autograd, eager launches, in the default "async" check mode (guard included) -- and the
+model step runs in the default mode too, with its "off" figure beside it.
 
 Reported (one JSON line on rank 0):
   value      algorithmic attention TFLOP/s of the step: 1152 * P flop (P = B*H*T^2/2 causal pairs; fwd 320 P,
@@ -20,10 +21,14 @@ Reported (one JSON line on rank 0):
              same number of bytes (half read, half written), timed the same way, as the ceiling HBM offers to a
              transfer of this size (copy_same_bytes_gbs, frac_of_copy); the prep backward likewise (backward).
              phases_ms are the step's own event phases, host gaps included.
-  lmce       the linear cross-entropy at config 3 (N=16384, d=768, V=50277): step time, TFLOP/s of its three GEMMs
-             (6 N V d), hipBLASLt GEMM roofline and the HIP row pass against HBM peak.
+  lmce       the linear cross-entropy at config 3 (N=16384, d=768, V=50277): the gradient step (token chunks of at
+             most 1 GiB of logits; TFLOP/s of its three GEMMs, 6 N V d; library GEMM roofline; the HIP row pass
+             against HBM peak) and the loss without gradients on the fused HIP kernel (MFMA roofline, no logits
+             buffer) beside the unfused GEMM + row pass it replaces.
+  fused_layer_async  sisa_fused forward + backward through autograd in the default "async" check mode (guard
+             included, eager launches): ms and TFLOP/s, beside the same calls in "off" mode.
   model_step the full decoder training step at config 4 (sisa-152m, B=8, T=2048, bf16 autocast, fused attention,
-             HIP RMSNorm/SwiGLU, fused linear CE, AdamW): tokens/s.
+             HIP RMSNorm/SwiGLU, fused linear CE, AdamW): tokens/s in the default "async" check mode, and in "off".
   block_kernels  RMSNorm, SwiGLU activation and decode-attention kernels against HBM peak (config-4 shapes).
   projection_gemms  the library GEMMs of one config-4 layer (fwd, dx, dW of W_cat, W_O, gate/up, down) against
              the bf16 MFMA peak.
@@ -61,12 +66,51 @@ def _quiet_host():
 
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
-# HBM bytes per step measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, each scaled by what the same counter
-# reads for a plain 1 GiB copy (fetch x2.0, write x1.0); per-kernel figures in profiles/hbm_traffic_ns_ce.txt.
-# They belong to the kernels of this build: re-measure after a kernel change.
-TRAFFIC_ATTN_NS = 636.0e6        # attn_fwd + attn_bwd_dq + attn_bwd_dkv + dlam, north-star shape
-TRAFFIC_PREP_FWD_NS = 50.8e6     # prep_sums + prep_fwd
-TRAFFIC_LMCE_ROWS_C3 = 3299.8e6  # lmce_rows on the 16384 x 50304 chunk
+# Profiles of this build's kernels (rocprofv3 under the commands the files name), read at run time so that the bench
+# line quotes the committed measurements: HBM bytes per dispatch (FETCH_SIZE / WRITE_SIZE, each scaled by what the
+# counter reads for a plain 1 GiB copy) and the counter-measured MFMA busy fraction of the attention kernels.
+PROFILES = os.path.join(ROOT, "profiles")
+ATTN_KERNELS = ("attn_fwd_kernelIDF16b", "attn_bwd_dq_kernelIDF16b", "attn_bwd_dkv_kernelIDF16b", "dlam_kernel")
+PREP_FWD_KERNELS = ("prep_sums_kernelIDF16b", "prep_fwd_kernelIDF16b")
+
+
+def profiled_traffic(kernels, name: str = "hbm_traffic_ns_ce.txt") -> float | None:
+    """Sum of read + written MB per dispatch (calibrated, 1 MB = 1e6 B) of the named kernels in a committed traffic
+    profile (its table rows: calls FETCH_KiB WRITE_KiB read_MB written_MB kernel), in bytes; None when absent."""
+    found = {}
+    try:
+        with open(os.path.join(PROFILES, name)) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) < 6 or not parts[0].isdigit():
+                    continue
+                for k in kernels:
+                    if k in parts[5] and k not in found:
+                        found[k] = (float(parts[3]) + float(parts[4])) * 1e6
+    except (OSError, ValueError):
+        return None
+    return sum(found.values()) if len(found) == len(kernels) else None
+
+
+def profiled_mfma_busy(name: str = "counters_attention_ns.txt") -> dict | None:
+    """Per-kernel and time-weighted MFMA busy percentages of the attention kernels from the committed counter profile
+    (rows: kernel  us  valu_busy_pct  mfma_busy_pct ...); None when absent."""
+    rows = {}
+    try:
+        with open(os.path.join(PROFILES, name)) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) >= 4 and parts[0] in ("attn_fwd", "attn_bwd_dq", "attn_bwd_dkv"):
+                    rows[parts[0]] = (float(parts[1]), float(parts[3]))
+    except (OSError, ValueError):
+        return None
+    if len(rows) != 3:
+        return None
+    t = sum(us for us, _ in rows.values())
+    out = {k: v[1] for k, v in rows.items()}
+    out["time_weighted"] = round(sum(us * b for us, b in rows.values()) / t, 2)
+    out["source"] = f"profiles/{name}"
+    return out
 
 
 def parse():
@@ -159,9 +203,13 @@ def prep_kernel_rates(proj, z, H: int) -> dict:
 
 
 def bench_ce(steps: int, warmup: int) -> dict:
-    """Linear cross-entropy at config 3 (N=16,384 tokens, d=768, V=50,277, bf16): one step = the work of
-    linear_cross_entropy forward with both gradients (logits GEMM, HIP row pass, dx GEMM, dW GEMM), inputs resident
-    in HBM, timed per phase with HIP events on the current stream."""
+    """Linear cross-entropy at config 3 (N=16,384 tokens, d=768, V=50,277, bf16), inputs resident in HBM.
+
+    train: one forward with both gradients as linear_cross_entropy runs it (per token chunk of at most 1 GiB of logits:
+    logits GEMM, HIP row pass writing G over the logits, dx GEMM, dW GEMM), timed per phase with HIP events.
+    fused_forward: the loss without gradients on the fused HIP kernel (sisa_lmce_fwd: MFMA GEMM reduced to lse and
+    the label logit on the fly, no logits buffer), against the bf16 dense MFMA peak; beside it the unfused no-gradient
+    forward (logits GEMM + row pass without G) that it replaces."""
     import torch
 
     from sisa_amd.workloads import config_inputs
@@ -172,9 +220,9 @@ def bench_ce(steps: int, warmup: int) -> dict:
     x, w, lab = c["hidden"], c["weight"], c["labels"]
     N, D = x.shape
     V = w.shape[0]
-    wp = LC._padded_lowp_weight(w, torch.bfloat16)
+    wp = LC.padded_weight(w, torch.bfloat16)
     Vp = wp.shape[0]
-    rows = LC._pick_chunk(N, Vp, None, 2)
+    rows = LC.chunk_rows(N, Vp, None, 2)
     buf = torch.empty((rows, Vp), dtype=torch.bfloat16, device=dev)
     loss_rows = torch.empty(N, device=dev)
     dx = torch.empty((N, D), device=dev)
@@ -223,21 +271,75 @@ def bench_ce(steps: int, warmup: int) -> dict:
     fl = LC.flops(N, V, D)
     gemm_ms = ph["logits_gemm"] + ph["dx_gemm"] + ph["dw_gemm"]
     row_bytes = N * Vp * 2 * 2 + N * 12
-    return {"workload": "linear cross-entropy fwd with dx, dW (config 3)", "N": N, "d": D, "V": V, "Vp": Vp,
-            "chunk_rows": rows, "ms_per_step": round(ms, 4), "tflops": round(fl["total"] / (ms * 1e-3) / 1e12, 2),
-            "tokens_per_s": round(N / (ms * 1e-3), 1), "phases_ms": {k: round(v, 4) for k, v in ph.items()},
-            "roofline_gemm": {"bound": "mfma", "achieved": round(fl["total"] / (gemm_ms * 1e-3) / 1e12, 1),
-                              "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                              "frac": round(fl["total"] / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-                              "algorithmic": "3 GEMMs x 2*N*V*d flop"},
-            "roofline_rows": {"bound": "hbm", "achieved": round(row_bytes / (ph["rows"] * 1e-3) / 1e9, 1),
-                              "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                              "frac": round(row_bytes / (ph["rows"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                              "traffic": TRAFFIC_LMCE_ROWS_C3,
-                              "algorithmic": "N*Vp*2 B read + N*Vp*2 B written (+12 B per row)"}}
+
+    # the loss without gradients: fused kernel, and the unfused pair it replaces
+    def fused():
+        LC.lmce_fused_loss_rows(x, wp, lab, V, -100)
+
+    def unfused():
+        for s in range(0, N, rows):
+            lg = buf[:min(N, s + rows) - s]
+            torch.mm(x[s:s + lg.shape[0]], wp.t(), out=lg)
+            LC.lmce_rows(lg, lab[s:s + lg.shape[0]], loss_rows[s:s + lg.shape[0]], V, -100, None, 1.0)
+
+    fused_s = queued_seconds(fused, reps=10)
+    unfused_s = queued_seconds(unfused, reps=10)
+    fwd_tf = fl["forward"] / fused_s / 1e12
+    return {"workload": "linear cross-entropy (config 3): N=16384, d=768, V=50277, bf16", "N": N, "d": D, "V": V,
+            "Vp": Vp,
+            "train": {"what": "forward with dx, dW (token chunks of <= 1 GiB of logits)", "chunk_rows": rows,
+                      "ms_per_step": round(ms, 4), "tflops": round(fl["total"] / (ms * 1e-3) / 1e12, 2),
+                      "tokens_per_s": round(N / (ms * 1e-3), 1), "phases_ms": {k: round(v, 4) for k, v in ph.items()},
+                      "roofline_gemm": {"bound": "mfma", "achieved": round(fl["total"] / (gemm_ms * 1e-3) / 1e12, 1),
+                                        "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                                        "frac": round(fl["total"] / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                                        "algorithmic": "3 GEMMs x 2*N*V*d flop"},
+                      "roofline_rows": {"bound": "hbm", "achieved": round(row_bytes / (ph["rows"] * 1e-3) / 1e9, 1),
+                                        "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                        "frac": round(row_bytes / (ph["rows"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                                        "algorithmic": "N*Vp*2 B read + N*Vp*2 B written (+12 B per row)"}},
+            "fused_forward": {"what": "loss without gradients, sisa_lmce_fwd (no logits buffer)",
+                              "ms": round(fused_s * 1e3, 4), "tokens_per_s": round(N / fused_s, 1),
+                              "roofline": {"bound": "mfma", "achieved": round(fwd_tf, 1), "peak": PEAK_BF16_TFLOPS,
+                                           "unit": "TFLOP/s", "frac": round(fwd_tf / PEAK_BF16_TFLOPS, 4),
+                                           "algorithmic": "2*N*V*d flop"},
+                              "unfused_ms": round(unfused_s * 1e3, 4),
+                              "unfused_logits_bytes": int(rows * Vp * 2)}}
 
 
-def bench_model(steps: int, warmup: int) -> dict:
+def bench_fused_layer(proj, z, lam, dy, H, steps: int, mode: str, flop: float) -> dict:
+    """sisa_fused forward + backward through autograd as a user calls it (eager launches, fresh outputs each call),
+    in check mode ``mode`` (the default "async": the non-finite guard and its device assert included) and in "off"."""
+    import torch
+
+    from sisa_amd import backends
+    from sisa_amd.kernels.fused_prep import sisa_fused
+
+    P, Z, LM = (t.detach().clone().requires_grad_(True) for t in (proj, z, lam))
+
+    def call():
+        y = sisa_fused(P, Z, LM, H)
+        torch.autograd.grad(y, (P, Z, LM), dy)
+
+    res = {}
+    for m in (mode, "off"):
+        backends.set_check_mode(m)
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        with _quiet_host():
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                call()
+            torch.cuda.synchronize()
+            res[m] = (time.perf_counter() - t0) * 1e3 / steps
+    backends.set_check_mode(mode)
+    return {"what": "sisa_fused forward + backward (autograd, eager launches)", "check_mode": mode,
+            "ms_per_step": round(res[mode], 4), "tflops": round(flop / (res[mode] * 1e-3) / 1e12, 2),
+            "ms_per_step_check_off": round(res["off"], 4)}
+
+
+def bench_model(steps: int, warmup: int, brief: bool = False) -> dict:
     """Full decoder training step at config 4: sisa-152m (12 layers, d=768, H=12, d_head=64, d_state=32, SwiGLU,
     tied embedding, vocabulary 50277, README init), B=8 x T=2048 uniform random token ids, bf16 autocast; one step =
     forward with the fused HIP attention path and the chunked HIP linear cross-entropy, backward, AdamW update."""
@@ -273,8 +375,13 @@ def bench_model(steps: int, warmup: int) -> dict:
             loss = step()
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) * 1e3 / steps
+    if brief:
+        return {"ms_per_step": round(ms, 3), "tokens_per_s": round(B * T / (ms * 1e-3), 1)}
+    from sisa_amd import backends
+
     return {"workload": "full decoder training step (config 4): sisa-152m, B=8, T=2048, bf16 autocast, hip_fused "
                         "attention + HIP RMSNorm/SwiGLU + fused linear CE + AdamW", "B": B, "T": T,
+            "check_mode": backends.get_check_mode(),
             "params": model.num_parameters(), "steps": steps, "ms_per_step": round(ms, 3),
             "tokens_per_s": round(B * T / (ms * 1e-3), 1), "loss": round(float(loss.detach()), 4), "tuned_gemms": tuned}
 
@@ -482,7 +589,8 @@ def main():
     from sisa_amd.gemm_tuning import enable_tuned_gemms
 
     enable_tuned_gemms()          # library GEMM choices for the CE and model legs (the attention leg has none)
-    backends.set_check_mode("off")    # the guard is an input check, not part of the measured arithmetic (see below)
+    default_mode = backends.get_check_mode()
+    backends.set_check_mode("off")    # headline: the path's kernels (the guard is an input check; timed separately)
     cfg = {"ns": "ns", "1": 1, "2": 2}[args.config]
     inp = config_inputs(cfg, device=dev)
     proj, z, dy, H = inp["proj"], inp["z"], inp["dy"], inp["H"]
@@ -599,26 +707,32 @@ def main():
         "tokens_per_s": round(B * L / (ms_step * 1e-3), 1),
         "timing": timing,
         "eager_ms_per_step": round(ms_eager, 4),
-        "mfma_util_pct": round(100 * value / PEAK_BF16_TFLOPS, 2),
+        "algorithmic_peak_pct": round(100 * value / PEAK_BF16_TFLOPS, 2),
+        "mfma_busy_pct": profiled_mfma_busy(),
         "phases_ms": {k: round(v, 4) for k, v in phases.items()},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": TRAFFIC_ATTN_NS if cfg == "ns" else None,
+                     "traffic": profiled_traffic(ATTN_KERNELS) if cfg == "ns" else None,
                      "kernel": "attention fwd + bwd launches (attn_fwd, attn_bwd_dq, attn_bwd_dkv, dlam)",
                      "algorithmic": f"1152 flop per causal pair x {fl['pairs']:.4g} pairs per step"},
         "roofline_prep": {"bound": "hbm", "achieved": round(prep_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": round(prep_gbs / PEAK_HBM_GBS, 4),
-                          "traffic": TRAFFIC_PREP_FWD_NS if cfg == "ns" else None,
+                          "traffic": profiled_traffic(PREP_FWD_KERNELS) if cfg == "ns" else None,
                           "algorithmic": f"{pb['total'] / 1e6:.1f} MB per prep forward (310 B per token-head)",
                           "kernels": "prep_sums + prep_fwd, queued behind a GPU spin (HIP events)",
                           "copy_same_bytes_gbs": prk["prep_fwd"]["copy_same_bytes_gbs"],
                           "frac_of_copy": prk["prep_fwd"]["frac_of_copy"],
                           "backward": prk["prep_bwd"]},
     }
+    out["fused_layer_async"] = bench_fused_layer(proj, z, lam, dy, H, args.steps, default_mode, total_flop)
+    backends.set_check_mode(default_mode)
     if not args.no_ce:
         out["lmce"] = bench_ce(max(3, args.steps // 2), 2)
     if not args.no_model:
         out["model_step"] = bench_model(max(3, args.steps // 4), 2)
+        backends.set_check_mode("off")
+        out["model_step"]["check_mode_off"] = bench_model(max(3, args.steps // 4), 2, brief=True)
+        backends.set_check_mode(default_mode)
         out["block_kernels"] = bench_block_kernels()
         out["projection_gemms"] = bench_projection_gemms()
     if not args.no_cpu_baseline:

@@ -206,6 +206,32 @@ typedef struct {
 
 int sisa_lmce_rows(const sisa_lmce_rows_args* a, void* stream);
 
+/* Fused forward of the linear cross-entropy: lse_r = log sum_{c<V} exp(x_r . w_c) and loss_r = lse_r - x_r . w_{label_r}
+ * (0 for ignore_index, NaN for a label outside [0, V)) from x (N, D) and the padded weight w (Vp, D) on MFMA, without
+ * a logits buffer: the logits are fp32 MFMA accumulations reduced tile by tile (online max / sum-exp over vocabulary
+ * splits, combined in a fixed order). Replaces the forward of the reference's chunk loop for callers that need no
+ * gradient -- the logits GEMM + `_lmce_row_kernel` pass of `_LinearCrossEntropyFn.forward`
+ * (src/sisa/kernels/linear_ce.py:138-191, 60-96). */
+typedef struct {
+    int64_t N;                 /* rows (0 is a no-op) */
+    int64_t V;                 /* real vocabulary rows of w, >= 1 */
+    int64_t Vp;                /* rows of w, >= V (rows >= V are ignored) */
+    int32_t D;                 /* hidden size, a positive multiple of 64 */
+    int32_t dtype;             /* of x and w: SISA_BF16 or SISA_F16 */
+    const void* x;             /* (N, D), 16-byte aligned, row stride ldx (multiple of 8) */
+    int64_t ldx;
+    const void* w;             /* (Vp, D), 16-byte aligned, row stride ldw (multiple of 8) */
+    int64_t ldw;
+    const int64_t* labels;     /* (N,) */
+    int64_t ignore_index;
+    float* lse;                /* (N,) fp32 output, natural log, or NULL */
+    float* loss_rows;          /* (N,) fp32 output */
+    float* workspace;          /* sisa_lmce_fwd_workspace_bytes(N, Vp) bytes */
+} sisa_lmce_fwd_args;
+
+int64_t sisa_lmce_fwd_workspace_bytes(int64_t N, int64_t Vp);
+int sisa_lmce_fwd(const sisa_lmce_fwd_args* a, void* stream);
+
 /* ------------------------------------------------------------------------------------------------ decoder block */
 
 /* RMSNorm over the last axis: y = (x * rsqrt(mean(x^2) + eps)) * w in fp32, stored in the input dtype; rstd (N) fp32

@@ -1,0 +1,269 @@
+// Fused forward of the linear cross-entropy for gfx950: logits = x W_pad^T computed tile by tile on bf16/fp16 MFMA
+// and reduced on the fly to each row's log-sum-exp and label logit. The (N x Vp) logits never exist in memory.
+//
+// Reference: the forward of `_LinearCrossEntropyFn` (src/sisa/kernels/linear_ce.py:138-191: logits chunk GEMM, then
+// `_lmce_row_kernel`'s online max / sum-exp and the label pick, linear_ce.py:60-96). The reference materialises a
+// (chunk, Vp) logits buffer; here the GEMM's output tiles never leave registers. The logits are the MFMA's fp32
+// accumulations (the unfused path rounds them to the compute dtype before the row pass).
+//
+// Decomposition: a workgroup of 2 x 4 waves owns 256 rows of x and walks a range of 256-column vocabulary tiles (one
+// of S vocabulary splits). Per tile, K = D is streamed through LDS in 64-wide stages (buffer loads straight into
+// LDS, double-buffered, XOR-swizzled 16-byte chunks); a wave computes a 128 (vocabulary) x 64 (rows) block as 8 x 4
+// v_mfma_f32_16x16x32 blocks with W as the A operand, so that a lane holds 32 logits of one row per block column
+// (12 operand fragments per 32 MFMAs, to keep the LDS reads below the matrix rate). After a tile's last stage each
+// lane folds its 32 logits per row into a running (max, sum of exponentials) in log2 units and, when the tile holds
+// a row's label, keeps that logit. At the end the lane groups and the two waves
+// sharing rows combine their partials; a second launch combines the S splits of each row in a fixed order.
+// Deterministic: no atomics. Workgroup i runs on XCD i % 8; each XCD takes a set of row blocks with all their
+// splits, so its L2 keeps those rows of x for every vocabulary tile.
+#include "common.h"
+#include "host.h"
+
+namespace {
+
+constexpr int NWC = 8;            // waves per workgroup: 2 along the vocabulary x 4 along the rows
+constexpr int TR = 256;           // rows of x per workgroup
+constexpr int TV = 256;           // vocabulary columns per tile
+constexpr int WV = 128;           // vocabulary columns of a wave (8 MFMA blocks)
+constexpr int WR = 64;            // rows of a wave (4 MFMA blocks)
+constexpr int IB = WV / 16, JB = WR / 16;
+constexpr int TK = 64;            // hidden elements per LDS stage
+constexpr float M_FLOOR_CE = -1e30f;
+constexpr float LN2 = 0.69314718055994531f;
+
+template <class T>
+struct __attribute__((aligned(16))) CeLds {
+    T x[2][TR * TK];
+    T w[2][TV * TK];
+    float red_m[TR], red_s[TR];   // the second wave of each row pair hands over its row partials
+};
+
+// The vocabulary splits of one problem: S splits of `per` consecutive tiles (the last ones may be shorter or empty).
+struct Split {
+    int64_t tiles, S, per;
+};
+inline Split ce_split(int64_t N, int64_t Vp) {
+    const int64_t nrb = sisa::cdiv(N, TR), tiles = sisa::cdiv(Vp, TV);
+    int64_t S = sisa::cdiv(512, nrb);            // about 512 workgroups: two rounds of one per CU
+    S = S < 1 ? 1 : (S > tiles ? tiles : S);
+    return {tiles, S, sisa::cdiv(tiles, S)};
+}
+
+template <class T>
+__global__ __launch_bounds__(64 * NWC) void lmce_fwd_kernel(sisa_lmce_fwd_args a, int S, int per) {
+    __shared__ CeLds<T> sm;
+    const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t N = a.N, V = a.V;
+    const int nrb = (int)((N + TR - 1) / TR), rbx = (nrb + 7) / 8;
+    const int xcd = blockIdx.x % 8, q = blockIdx.x / 8;
+    const int split = q % S, rb = xcd * rbx + q / S;
+    if (rb >= nrb) return;
+    const int tiles = (int)((a.Vp + TV - 1) / TV);
+    const int t_begin = split * per;
+    const int t_end = t_begin + per < tiles ? t_begin + per : tiles;
+    const int ntiles = t_end > t_begin ? t_end - t_begin : 0;
+    const int nks = a.D / TK;
+    const int64_t row0 = (int64_t)rb * TR;
+    const int wv = WV * (w & 1), wn = WR * (w >> 1);   // the wave's vocabulary and row offsets in the tile
+
+    // staging: a 256-row tile is four 64-row DMA groups; rows past the data read as zero
+    DmaStage<T, TK, NWC> sx, sw;
+    sx.init(a.ldx, w, lane);
+    sw.init(a.ldw, w, lane);
+    const int64_t xbytes = ((N - 1) * a.ldx + a.D) * (int64_t)sizeof(T);
+    const int64_t wbytes = ((a.Vp - 1) * a.ldw + a.D) * (int64_t)sizeof(T);
+    const T* X = (const T*)a.x;
+    const T* W = (const T*)a.w;
+    auto issue = [&](int g, int buf) {   // stage g of the workgroup: vocabulary tile g / nks, K block g % nks
+        const int64_t v0 = (int64_t)(t_begin + g / nks) * TV;
+        const int k0 = (g % nks) * TK;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            dma_issue<4>(sx, X, xbytes, (int)(((row0 + 64 * h) * a.ldx + k0) * (int64_t)sizeof(T)),
+                         sm.x[buf] + 64 * h * TK, w);
+            dma_issue<5>(sw, W, wbytes, (int)(((v0 + 64 * h) * a.ldw + k0) * (int64_t)sizeof(T)),
+                         sm.w[buf] + 64 * h * TK, w);
+        }
+    };
+
+    // the label of each of the lane's 4 rows: which tile, and whether this lane holds it (and where)
+    int lab_tile[JB], lab_idx[JB];
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+        const int64_t n = row0 + wn + 16 * j + lc;
+        lab_tile[j] = -1;
+        lab_idx[j] = 0;
+        if (n < N) {
+            const int64_t y = a.labels[n];
+            if (y != a.ignore_index && y >= 0 && y < V) {
+                const int pos = (int)(y % TV);
+                const bool mine = (pos / WV) * WV == wv && ((pos % 16) >> 2) == grp;
+                lab_tile[j] = mine ? (int)(y / TV) : -1;
+                lab_idx[j] = ((pos % WV) >> 4) * 4 + (pos & 3);   // block i, register r
+            }
+        }
+    }
+    float m[JB], s[JB], zlab[JB];
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+        m[j] = M_FLOOR_CE;
+        s[j] = 0.f;
+        zlab[j] = 0.f;
+    }
+    bool got[JB] = {false, false, false, false};
+
+    f32x4 acc[IB][JB];
+#pragma unroll
+    for (int i = 0; i < IB; ++i)
+#pragma unroll
+        for (int j = 0; j < JB; ++j) acc[i][j] = zero4();
+
+    const int total = ntiles * nks;
+    if (total > 0) issue(0, 0);
+    __syncthreads();
+    for (int g = 0; g < total; ++g) {
+        const int buf = g & 1;
+        if (g + 1 < total) issue(g + 1, buf ^ 1);
+#pragma unroll
+        for (int step = 0; step < TK / 32; ++step) {
+            frag8<T> xf[JB];
+#pragma unroll
+            for (int j = 0; j < JB; ++j) xf[j] = frag_rows<T, TK>(sm.x[buf], wn + 16 * j, step, lane);
+#pragma unroll
+            for (int i = 0; i < IB; ++i) {
+                const frag8<T> wf = frag_rows<T, TK>(sm.w[buf], wv + 16 * i, step, lane);
+#pragma unroll
+                for (int j = 0; j < JB; ++j) acc[i][j] = mma(wf, xf[j], acc[i][j]);
+            }
+        }
+        if (g % nks == nks - 1) {
+            // the tile is complete: lane holds logits of rows wn + 16 j + lc at columns v0 + wv + 16 i + 4 grp + r
+            const int vt = t_begin + g / nks;
+            const int64_t vbase = (int64_t)vt * TV + wv + 4 * grp;
+#pragma unroll
+            for (int j = 0; j < JB; ++j) {
+                float mt = -__builtin_inff();
+#pragma unroll
+                for (int i = 0; i < IB; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const bool in = vbase + 16 * i + r < V;   // padding columns do not enter the sum
+                        acc[i][j][r] = in ? acc[i][j][r] * LOG2E : -__builtin_inff();
+                        mt = fmaxf(mt, acc[i][j][r]);
+                    }
+                if (mt > m[j]) {
+                    s[j] *= fast_exp2(m[j] - mt);
+                    m[j] = mt;
+                }
+                float ls = 0.f;
+#pragma unroll
+                for (int i = 0; i < IB; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) ls += fast_exp2(acc[i][j][r] - m[j]);
+                s[j] += ls;
+                if (lab_tile[j] == vt) {   // rare: pick the label's logit (log2 units)
+                    float z = 0.f;
+#pragma unroll
+                    for (int i = 0; i < IB; ++i)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) z = (lab_idx[j] == 4 * i + r) ? acc[i][j][r] : z;
+                    zlab[j] = z;
+                    got[j] = true;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < IB; ++i)
+#pragma unroll
+                for (int j = 0; j < JB; ++j) acc[i][j] = zero4();
+        }
+        __syncthreads();
+    }
+
+    // combine the four lane groups of each row, then the two waves sharing the rows (w and w ^ 1)
+    float rm[JB], rsum[JB];
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+        rm[j] = group_max(m[j]);
+        rsum[j] = group_sum(s[j] * fast_exp2(m[j] - rm[j]));
+        if (got[j]) a.workspace[2 * (int64_t)S * N + row0 + wn + 16 * j + lc] = zlab[j] * LN2;
+    }
+    if ((w & 1) && grp == 0) {
+#pragma unroll
+        for (int j = 0; j < JB; ++j) {
+            sm.red_m[wn + 16 * j + lc] = rm[j];
+            sm.red_s[wn + 16 * j + lc] = rsum[j];
+        }
+    }
+    __syncthreads();
+    if ((w & 1) == 0 && grp == 0) {
+#pragma unroll
+        for (int j = 0; j < JB; ++j) {
+            const int64_t n = row0 + wn + 16 * j + lc;
+            if (n >= N) continue;
+            const float m2 = sm.red_m[wn + 16 * j + lc], s2 = sm.red_s[wn + 16 * j + lc];
+            const float mm = fmaxf(rm[j], m2);
+            a.workspace[(int64_t)split * N + n] = mm;
+            a.workspace[(int64_t)(S + split) * N + n] = rsum[j] * fast_exp2(rm[j] - mm) + s2 * fast_exp2(m2 - mm);
+        }
+    }
+}
+
+// Per row: the S split partials combined in split order; lse (natural log) and the loss row.
+__global__ __launch_bounds__(256) void lmce_combine_kernel(sisa_lmce_fwd_args a, int S) {
+    const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (n >= a.N) return;
+    const int64_t N = a.N;
+    float mm = M_FLOOR_CE;
+    for (int sp = 0; sp < S; ++sp) mm = fmaxf(mm, a.workspace[(int64_t)sp * N + n]);
+    float ss = 0.f;
+    for (int sp = 0; sp < S; ++sp)
+        ss += a.workspace[(int64_t)(S + sp) * N + n] * fast_exp2(a.workspace[(int64_t)sp * N + n] - mm);
+    const float lse = (mm + __builtin_amdgcn_logf(ss)) * LN2;
+    const int64_t y = a.labels[n];
+    float loss;
+    if (y == a.ignore_index) loss = 0.f;
+    else if (y < 0 || y >= a.V) loss = __builtin_nanf("");
+    else loss = lse - a.workspace[2 * (int64_t)S * N + n];
+    a.loss_rows[n] = loss;
+    if (a.lse) a.lse[n] = lse;
+}
+
+template <class T>
+int launch_lmce_fwd(const sisa_lmce_fwd_args* a, hipStream_t st) {
+    const Split sp = ce_split(a->N, a->Vp);
+    const int64_t nrb = sisa::cdiv(a->N, TR), rbx = sisa::cdiv(nrb, 8);
+    const unsigned grid = (unsigned)(8 * rbx * sp.S);
+    lmce_fwd_kernel<T><<<grid, 64 * NWC, 0, st>>>(*a, (int)sp.S, (int)sp.per);
+    const int rc = sisa::launch_status("sisa_lmce_fwd");
+    if (rc) return rc;
+    lmce_combine_kernel<<<(unsigned)sisa::cdiv(a->N, 256), 256, 0, st>>>(*a, (int)sp.S);
+    return sisa::launch_status("sisa_lmce_fwd (combine)");
+}
+
+}  // namespace
+
+extern "C" int64_t sisa_lmce_fwd_workspace_bytes(int64_t N, int64_t Vp) {
+    if (N < 1 || Vp < 1) return 0;
+    return (2 * ce_split(N, Vp).S + 1) * N * (int64_t)sizeof(float);
+}
+
+extern "C" int sisa_lmce_fwd(const sisa_lmce_fwd_args* a, void* stream) {
+    SISA_REQUIRE(a != nullptr, "sisa_lmce_fwd: null args");
+    if (a->N == 0) return SISA_OK;
+    SISA_REQUIRE(a->N >= 1 && a->V >= 1 && a->Vp >= a->V, "sisa_lmce_fwd: bad shape N=%lld V=%lld Vp=%lld",
+                 (long long)a->N, (long long)a->V, (long long)a->Vp);
+    SISA_REQUIRE(a->D >= TK && a->D % TK == 0, "sisa_lmce_fwd: hidden size %d must be a positive multiple of %d", a->D,
+                 TK);
+    SISA_REQUIRE(a->dtype == SISA_BF16 || a->dtype == SISA_F16, "sisa_lmce_fwd: dtype %d (bf16 or fp16)", a->dtype);
+    SISA_REQUIRE(a->x && a->w && a->labels && a->loss_rows && a->workspace && sisa::aligned16(a->x) &&
+                     sisa::aligned16(a->w) && a->ldx >= a->D && a->ldw >= a->D && a->ldx % 8 == 0 && a->ldw % 8 == 0,
+                 "sisa_lmce_fwd: x, w must be 16-byte aligned with row strides >= D (multiples of 8); labels, "
+                 "loss_rows, workspace given");
+    // one buffer resource per operand: both extents below 2 GiB
+    SISA_REQUIRE(((sisa::cdiv(a->N, TR) * TR - 1) * a->ldx + a->D) * 2 < ((int64_t)1 << 31) &&
+                     ((sisa::cdiv(a->Vp, TV) * TV - 1) * a->ldw + a->D) * 2 < ((int64_t)1 << 31),
+                 "sisa_lmce_fwd: x or w spans 2 GiB or more");
+    hipStream_t st = (hipStream_t)stream;
+    return a->dtype == SISA_BF16 ? launch_lmce_fwd<__bf16>(a, st) : launch_lmce_fwd<_Float16>(a, st);
+}

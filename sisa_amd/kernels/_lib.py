@@ -98,6 +98,12 @@ class WgradArgs(Structure):
                 ("c", c_void_p), ("ldc", c_int64), ("workspace", c_void_p)]
 
 
+class LmceFwdArgs(Structure):
+    _fields_ = [("N", c_int64), ("V", c_int64), ("Vp", c_int64), ("D", c_int32), ("dtype", c_int32),
+                ("x", c_void_p), ("ldx", c_int64), ("w", c_void_p), ("ldw", c_int64), ("labels", c_void_p),
+                ("ignore_index", c_int64), ("lse", c_void_p), ("loss_rows", c_void_p), ("workspace", c_void_p)]
+
+
 class DecodeArgs(Structure):
     _fields_ = [("B", c_int32), ("H", c_int32), ("M", c_int32), ("N", c_int32), ("dtype", c_int32),
                 ("q_start", c_int32), ("q", View), ("k", View), ("v", View), ("c", View), ("b", View),
@@ -114,6 +120,8 @@ SIGNATURES = {
     "sisa_attn_bwd_workspace_bytes": ([c_int32, c_int32, c_int32], c_int64),
     "sisa_attn_bwd": ([POINTER(AttnBwdArgs), c_void_p], c_int),
     "sisa_attn_bwd_noalloc": ([POINTER(AttnBwdArgs), c_void_p], c_int),
+    "sisa_lmce_fwd_workspace_bytes": ([c_int64, c_int64], c_int64),
+    "sisa_lmce_fwd": ([POINTER(LmceFwdArgs), c_void_p], c_int),
     "sisa_prep_fwd": ([POINTER(PrepFwdArgs), c_void_p], c_int),
     "sisa_prep_bwd_workspace_bytes": ([c_int32, c_int32, c_int32], c_int64),
     "sisa_finite_sum": ([c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p], c_int),

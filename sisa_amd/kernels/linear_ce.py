@@ -1,21 +1,27 @@
-"""Chunked linear + cross-entropy for a tied LM head on MI355X, without materialising the full logits.
+"""Linear layer + cross-entropy for a tied LM head on MI355X without the full (tokens x vocabulary) logits.
 
-Mirrors ``src/sisa/kernels/linear_ce.py`` of the reference: the same public functions (``linear_cross_entropy``,
-``reference_linear_cross_entropy``), arguments, loss/gradient definitions, ``grad_scale`` promise, eager fallback for
-CPU tensors or an fp32 compute dtype, and error behaviour (``ValueError`` for a bad weight shape or label count).
+Interface of the reference's ``sisa.kernels.linear_ce`` (src/sisa/kernels/linear_ce.py:220-259):
+``linear_cross_entropy(hidden, weight, labels, ignore_index=-100, *, chunk_tokens=None, grad_scale=None)`` -> the mean
+loss over the non-ignored rows, differentiable in ``hidden`` and ``weight``, and the eager formula
+``reference_linear_cross_entropy``. Labels are not shifted. A label outside [0, V) makes the loss NaN. A ``weight`` of
+the wrong shape or a label count that does not match the hidden rows raises ``ValueError``. CPU tensors and an fp32
+compute dtype take the eager formula.
 
-Per token chunk (gradients are produced during forward, as in the reference, linear_ce.py:167-191):
+How the work is arranged here (every kernel is HIP, ``libsisa_hip.so``):
 
-  1. ``logits = x_c @ W_pad^T`` -- hipBLASLt through ``torch.mm``, compute-dtype output with fp32 accumulation
-     (the autocast formula). W is padded with zero rows to a multiple of 128 (50,277 -> 50,304).
-  2. ``sisa_lmce_rows`` (HIP, ``csrc/lmce.hip``): per row lse, loss row and, when a gradient is needed,
-     G = (softmax - onehot) * (1/N_valid) * gscale rounded once to the compute dtype, written over the logits. A
-     row of up to 65,536 columns is read from HBM once and written once.
-  3. ``dx_c = G @ W_pad`` with fp32 output; 4. ``dW (+)= G^T @ x_c`` with fp32 output and accumulation.
+* No gradient wanted (``torch.no_grad``, evaluation, or neither input requires grad): one fused launch,
+  ``sisa_lmce_fwd`` (csrc/lmce_fwd.hip). An MFMA GEMM whose tiles are reduced on the fly to each row's log-sum-exp
+  and label logit; no logits are stored anywhere.
+* Gradients wanted: the loss and both gradients come out of one pass over token chunks, with the chunk's logits kept
+  just long enough to become G = (softmax - onehot) / N_valid (the reference's chunk loop, linear_ce.py:160-191, and
+  its 1 GiB buffer budget). Per chunk: logits = x W_pad^T (library GEMM), ``sisa_lmce_rows`` (csrc/lmce.hip: lse,
+  loss row and G written over the logits, one read and one write per element), dx = G W_pad and dW += G^T x (library
+  GEMMs, fp32 results). Computing the logits once and keeping G is the fewest flops for this step (3 GEMMs); a
+  design that never stores a logits chunk has to compute them twice (4 GEMMs).
 
-Backward multiplies the stored dx / dW by the incoming seed, or, with ``grad_scale`` promised, only checks the promise
-on the device. The chunk budget is 4 GiB of logits (MI355X has 288 GB of HBM; the reference uses 1 GiB), so the
-16,384-token benchmark case runs as one chunk.
+The vocabulary is padded with zero rows to a multiple of 128 (50,277 -> 50,304) so that every GEMM runs on aligned
+shapes; the padded columns never enter a sum. ``grad_scale`` is the caller's promise of the backward seed: G is then
+scaled in the forward pass and the backward only checks the promise on the device.
 """
 from __future__ import annotations
 
@@ -24,186 +30,212 @@ import torch.nn.functional as F
 
 from . import _lib
 
-__all__ = ["linear_cross_entropy", "reference_linear_cross_entropy", "lmce_rows", "flops"]
+__all__ = ["linear_cross_entropy", "reference_linear_cross_entropy", "lmce_rows", "lmce_fused_loss_rows",
+           "padded_weight", "chunk_rows", "flops"]
 
-VOCAB_PAD = 128
-CHUNK_BYTES = 4 << 30
-_HAS_OUT_DTYPE = hasattr(torch.ops.aten.mm, "dtype") and hasattr(torch.ops.aten.addmm, "dtype_out")
-
-
-def _compute_dtype(x: torch.Tensor) -> torch.dtype:
-    """The autocast dtype when autocast is on for x's device type, else x.dtype (linear_ce.py:107-113)."""
-    try:
-        if torch.is_autocast_enabled(x.device.type):
-            return torch.get_autocast_dtype(x.device.type)
-    except (TypeError, RuntimeError):
-        pass
-    return x.dtype
+VOCAB_MULTIPLE = 128
+LOGITS_BUDGET = 1 << 30          # bytes of one chunk of logits (the reference's budget)
+FUSED_K_MULTIPLE = 64            # sisa_lmce_fwd streams the hidden size in 64-wide stages
+_MM_OUT_DTYPE = hasattr(torch.ops.aten.mm, "dtype") and hasattr(torch.ops.aten.addmm, "dtype_out")
 
 
-def _pick_chunk(N: int, Vp: int, chunk_tokens: int | None, elt: int, budget: int = CHUNK_BYTES) -> int:
-    """Rows per chunk: ``chunk_tokens`` when given (clamped to [1, N]); otherwise the fewest chunks whose logits fit
-    the budget, balanced and rounded up to a multiple of 128 rows (linear_ce.py:116-124)."""
-    if N <= 0:
+# ------------------------------------------------------------------------------------------------ pieces
+def padded_weight(weight: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """The LM-head weight in the compute dtype (one round-to-nearest-even cast, as autocast does) with zero rows up
+    to the next multiple of 128."""
+    V, D = weight.shape
+    rows = -(-V // VOCAB_MULTIPLE) * VOCAB_MULTIPLE
+    out = weight.new_zeros((rows, D), dtype=dtype) if rows > V else weight.new_empty((rows, D), dtype=dtype)
+    out[:V].copy_(weight.detach())
+    return out
+
+
+def chunk_rows(n_rows: int, vocab_rows: int, chunk_tokens: int | None, itemsize: int,
+               budget: int = LOGITS_BUDGET) -> int:
+    """Token rows per chunk of the gradient pass: ``chunk_tokens`` if given (within [1, n_rows]); otherwise the
+    smallest number of equal chunks whose logits fit ``budget`` bytes, each rounded up to whole 128-row GEMM tiles."""
+    if n_rows <= 0:
         return 1
     if chunk_tokens:
-        return max(1, min(N, int(chunk_tokens)))
-    rows_max = max(128, budget // (Vp * elt))
-    n_chunks = -(-N // rows_max)
-    rows = -(-N // n_chunks)
-    return min(N, -(-rows // 128) * 128)
-
-
-def _padded_lowp_weight(w: torch.Tensor, dtype: torch.dtype, vocab_pad: int = VOCAB_PAD) -> torch.Tensor:
-    """(Vp, D) copy of w in ``dtype`` (RNE, as autocast) with zero rows V..Vp-1 (linear_ce.py:127-135)."""
-    V, D = w.shape
-    Vp = -(-V // vocab_pad) * vocab_pad
-    out = torch.empty((Vp, D), dtype=dtype, device=w.device)
-    out[:V].copy_(w.detach())
-    out[V:].zero_()
-    return out
+        return min(n_rows, max(1, int(chunk_tokens)))
+    fit = max(VOCAB_MULTIPLE, budget // (vocab_rows * itemsize))
+    pieces = -(-n_rows // fit)
+    per = -(-n_rows // pieces)
+    return min(n_rows, -(-per // VOCAB_MULTIPLE) * VOCAB_MULTIPLE)
 
 
 def lmce_rows(logits: torch.Tensor, labels: torch.Tensor, loss_rows: torch.Tensor, V: int, ignore_index: int,
               inv_n: torch.Tensor | None = None, gscale: float = 1.0, lse: torch.Tensor | None = None) -> None:
-    """Row pass over one chunk of logits (T, Vp) bf16/fp16 with unit column stride: writes ``loss_rows`` (T,) fp32
-    (and ``lse`` if given) and, when ``inv_n`` (a device scalar 1/N_valid) is given, overwrites the logits with G.
-    Replaces ``_launch_rows`` / ``_lmce_row_kernel`` (linear_ce.py:60-104)."""
+    """Row pass of one (T, Vp) bf16/fp16 logits chunk (``sisa_lmce_rows``): loss rows (and lse if given) and, when
+    ``inv_n`` (device scalar 1/N_valid) is given, G over the logits in place."""
     T, Vp = logits.shape
     if T == 0:
         return
     if logits.stride(1) != 1:
-        raise ValueError("lmce_rows: logits need a unit column stride")
+        raise ValueError("lmce_rows: the logits chunk must have unit column stride")
     if labels.dtype != torch.int64 or not labels.is_contiguous() or labels.numel() != T:
-        raise ValueError("lmce_rows: labels must be a contiguous int64 tensor with one entry per row")
+        raise ValueError(f"lmce_rows: expected {T} contiguous int64 labels")
     args = _lib.LmceRowsArgs(T, int(V), Vp, logits.stride(0), _lib.dtype_code(logits.dtype), int(inv_n is not None),
                              logits.data_ptr(), labels.data_ptr(), int(ignore_index), _lib.ptr(inv_n), float(gscale),
                              loss_rows.data_ptr(), _lib.ptr(lse))
     _lib.call("sisa_lmce_rows", args, logits)
 
 
-def _check_seed(g: torch.Tensor, grad_scale: float) -> None:
-    """G already carries the promised seed: check the promise where g lives (a device-side assert on the GPU, no
-    host sync; a RuntimeError on the CPU) (linear_ce.py:202-206)."""
-    torch._assert_async(g.to(torch.float32) == float(grad_scale),
-                        "linear_cross_entropy: backward seed differs from the promised grad_scale")
+def lmce_fused_loss_rows(x: torch.Tensor, wpad: torch.Tensor, labels: torch.Tensor, V: int, ignore_index: int,
+                         lse: torch.Tensor | None = None) -> torch.Tensor:
+    """Loss rows (N,) fp32 of ``x`` (N, D) against the padded weight ``wpad`` (Vp, D) from the fused kernel
+    (``sisa_lmce_fwd``): no logits buffer. D must be a multiple of 64; writes ``lse`` (natural log) if given."""
+    N, D = x.shape
+    out = torch.empty(N, dtype=torch.float32, device=x.device)
+    if N == 0:
+        return out
+    ws = torch.empty(max(1, _lib.workspace_bytes("sisa_lmce_fwd_workspace_bytes", N, wpad.shape[0]) // 4),
+                     dtype=torch.float32, device=x.device)
+    args = _lib.LmceFwdArgs(N, int(V), wpad.shape[0], D, _lib.dtype_code(x.dtype), x.data_ptr(), x.stride(0),
+                            wpad.data_ptr(), wpad.stride(0), labels.data_ptr(), int(ignore_index), _lib.ptr(lse),
+                            out.data_ptr(), ws.data_ptr())
+    _lib.call("sisa_lmce_fwd", args, x)
+    return out
 
 
-class _LinearCrossEntropyFn(torch.autograd.Function):
-    """Autograd wrapper of the chunk loop (linear_ce.py:138-217)."""
+def _matmul_f32(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, accumulate: bool) -> None:
+    """out (+)= a @ b with fp32 output from 16-bit operands (fp32 accumulation, no 16-bit rounding of the result)."""
+    if _MM_OUT_DTYPE:
+        if accumulate:
+            torch.addmm(out, a, b, out_dtype=torch.float32, out=out)
+        else:
+            torch.mm(a, b, out_dtype=torch.float32, out=out)
+    elif accumulate:
+        out.add_(torch.mm(a, b))
+    else:
+        out.copy_(torch.mm(a, b))
+
+
+class _Problem:
+    """One call's operands in the compute dtype: x (N, D) contiguous, the padded weight, int64 labels, and the
+    device scalars N_valid and 1/N_valid."""
+
+    def __init__(self, hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor, ignore_index: int,
+                 cdtype: torch.dtype):
+        D = hidden.shape[-1]
+        self.x = hidden.reshape(-1, D).to(cdtype).contiguous()
+        self.wpad = padded_weight(weight, cdtype)
+        self.labels = labels.reshape(-1).to(torch.int64).contiguous()
+        self.V, self.ignore_index = weight.shape[0], int(ignore_index)
+        self.N, self.D = self.x.shape
+        self.n_valid = (self.labels != self.ignore_index).sum()
+
+    def loss_without_grad(self) -> torch.Tensor:
+        if self.D % FUSED_K_MULTIPLE:   # the fused kernel's K stages do not divide D: the chunk loop without G
+            return self.loss_and_grads(False, False, 1.0, None)[0]
+        rows = lmce_fused_loss_rows(self.x, self.wpad, self.labels, self.V, self.ignore_index)
+        return rows.sum() / self.n_valid
+
+    def loss_and_grads(self, want_dx: bool, want_dw: bool, gscale: float, chunk_tokens: int | None):
+        """The chunk loop: loss and, as requested, dL/dx (N, D) and dL/dW_pad (Vp, D) in fp32 for a unit seed
+        (times ``gscale``)."""
+        N, D, dev = self.N, self.D, self.x.device
+        Vp = self.wpad.shape[0]
+        rows = torch.empty(N, dtype=torch.float32, device=dev)
+        dx = torch.empty((N, D), dtype=torch.float32, device=dev) if want_dx else None
+        dw = torch.zeros((Vp, D), dtype=torch.float32, device=dev) if want_dw and N == 0 else (
+            torch.empty((Vp, D), dtype=torch.float32, device=dev) if want_dw else None)
+        want_g = want_dx or want_dw
+        inv_n = torch.reciprocal(self.n_valid.to(torch.float32)).reshape(1) if want_g else None
+        step = chunk_rows(N, Vp, chunk_tokens, self.wpad.element_size())
+        chunk = torch.empty((min(step, N), Vp), dtype=self.x.dtype, device=dev) if N else None
+        for r0 in range(0, N, step):
+            r1 = min(N, r0 + step)
+            logits = chunk[:r1 - r0]
+            xs = self.x[r0:r1]
+            torch.mm(xs, self.wpad.t(), out=logits)
+            lmce_rows(logits, self.labels[r0:r1], rows[r0:r1], self.V, self.ignore_index, inv_n, gscale)
+            if want_dx:
+                _matmul_f32(logits, self.wpad, dx[r0:r1], accumulate=False)
+            if want_dw:
+                _matmul_f32(logits.t(), xs, dw, accumulate=r0 > 0)
+        return rows.sum() / self.n_valid, dx, dw
+
+
+class _LinearCE(torch.autograd.Function):
+    """Loss in the forward pass; the gradients, computed there too, are scaled by the seed in the backward pass."""
 
     @staticmethod
-    def forward(ctx, h, w, labels, opts):
-        ignore_index, chunk_tokens, cdtype, need_dh, need_dw, grad_scale = opts
-        D = h.shape[-1]
-        V = w.shape[0]
-        dev = h.device
-        x = h.reshape(-1, D)
-        N = x.shape[0]
-        lab = labels.reshape(-1).to(torch.int64).contiguous()
-        xb = x.to(cdtype).contiguous()
-        wp = _padded_lowp_weight(w, cdtype)
-        Vp = wp.shape[0]
-        n_valid = (lab != ignore_index).sum()
-        inv_n = torch.reciprocal(n_valid.to(torch.float32)).reshape(1)
-        loss_rows = torch.empty(N, dtype=torch.float32, device=dev)
-        rows = _pick_chunk(N, Vp, chunk_tokens, wp.element_size())
-        need_g = need_dh or need_dw
-        buf = torch.empty((rows, Vp), dtype=cdtype, device=dev) if N else None
-        dx = torch.empty((N, D), dtype=torch.float32, device=dev) if need_dh else None
-        # dW over all Vp rows keeps the GEMM on aligned shapes; rows V.. are dropped in backward
-        dw = torch.empty((Vp, D), dtype=torch.float32, device=dev) if need_dw else None
-        if need_dw and N == 0:
-            dw.zero_()
-        gs = 1.0 if grad_scale is None else float(grad_scale)
-        for s in range(0, N, rows):
-            e = min(N, s + rows)
-            lg = buf[:e - s]
-            xc = xb[s:e]
-            torch.mm(xc, wp.t(), out=lg)
-            lmce_rows(lg, lab[s:e], loss_rows[s:e], V, ignore_index, inv_n if need_g else None, gs)
-            if need_dh:
-                if _HAS_OUT_DTYPE:
-                    torch.mm(lg, wp, out_dtype=torch.float32, out=dx[s:e])
-                else:
-                    dx[s:e].copy_(torch.mm(lg, wp))
-            if need_dw:
-                if _HAS_OUT_DTYPE:
-                    if s == 0:
-                        torch.mm(lg.t(), xc, out_dtype=torch.float32, out=dw)
-                    else:
-                        torch.addmm(dw, lg.t(), xc, out_dtype=torch.float32, out=dw)
-                elif s == 0:
-                    dw.copy_(torch.mm(lg.t(), xc))
-                else:
-                    dw.add_(torch.mm(lg.t(), xc))
-        del buf
-        loss = loss_rows.sum() / n_valid
-        ctx.h_shape, ctx.h_dtype, ctx.w_dtype, ctx.grad_scale, ctx.V = h.shape, h.dtype, w.dtype, grad_scale, V
+    def forward(ctx, hidden, weight, labels, ignore_index, chunk_tokens, grad_scale, cdtype, want_dx, want_dw):
+        prob = _Problem(hidden, weight, labels, ignore_index, cdtype)
+        gscale = 1.0 if grad_scale is None else float(grad_scale)
+        loss, dx, dw = prob.loss_and_grads(want_dx, want_dw, gscale, chunk_tokens)
+        ctx.meta = (hidden.shape, hidden.dtype, weight.dtype, prob.V, grad_scale)
         ctx.save_for_backward(dx, dw)
         return loss
 
     @staticmethod
     @torch.autograd.function.once_differentiable
-    def backward(ctx, g):
+    def backward(ctx, seed):
         dx, dw = ctx.saved_tensors
-        if ctx.grad_scale is not None:
-            _check_seed(g, ctx.grad_scale)
-            dh = dx.view(ctx.h_shape) if dx is not None else None
-            dW = dw[:ctx.V] if dw is not None else None
-        else:
-            g32 = g.to(torch.float32)
-            dh = (dx * g32).view(ctx.h_shape) if dx is not None else None
-            dW = dw[:ctx.V] * g32 if dw is not None else None
-        if dh is not None and dh.dtype != ctx.h_dtype:
-            dh = dh.to(ctx.h_dtype)
-        if dW is not None and dW.dtype != ctx.w_dtype:
-            dW = dW.to(ctx.w_dtype)
-        return dh, dW, None, None
+        shape, h_dtype, w_dtype, V, promised = ctx.meta
+        if promised is None:
+            s = seed.to(torch.float32)
+            dx = None if dx is None else dx * s
+            dw = None if dw is None else dw[:V] * s
+        else:   # G already carries the promised seed: check it on the device, no host synchronisation
+            torch._assert_async(seed.to(torch.float32) == float(promised),
+                                "linear_cross_entropy: the backward seed is not the promised grad_scale")
+            dw = None if dw is None else dw[:V]
+        dh = None if dx is None else dx.view(shape).to(h_dtype)
+        dW = None if dw is None else dw.to(w_dtype)
+        return dh, dW, None, None, None, None, None, None, None
+
+
+def _compute_dtype(t: torch.Tensor) -> torch.dtype:
+    try:
+        if torch.is_autocast_enabled(t.device.type):
+            return torch.get_autocast_dtype(t.device.type)
+    except (RuntimeError, TypeError):
+        pass
+    return t.dtype
 
 
 def reference_linear_cross_entropy(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
                                    ignore_index: int = -100) -> torch.Tensor:
-    """The eager formula ``F.cross_entropy(F.linear(hidden, weight).float(), labels, ignore_index)``
-    (linear_ce.py:220-224)."""
+    """``F.cross_entropy(F.linear(hidden, weight).float(), labels, ignore_index=ignore_index)`` over all rows (the
+    reference's eager definition, linear_ce.py:220-224)."""
     logits = F.linear(hidden, weight)
-    return F.cross_entropy(logits.view(-1, logits.size(-1)).float(), labels.reshape(-1), ignore_index=ignore_index)
+    return F.cross_entropy(logits.reshape(-1, logits.shape[-1]).float(), labels.reshape(-1),
+                           ignore_index=ignore_index)
 
 
 @torch.compiler.disable
 def linear_cross_entropy(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor, ignore_index: int = -100,
                          *, chunk_tokens: int | None = None, grad_scale: float | None = None) -> torch.Tensor:
-    """Mean cross-entropy of ``hidden @ weight.T`` against ``labels`` without materialising the full logits
-    (linear_ce.py:227-259).
+    """Mean cross-entropy of ``hidden @ weight.T`` against ``labels`` (fp32 scalar) without the full logits.
 
-    Args:
-        hidden: ``(..., D)`` hidden states (fp32 under autocast, or bf16/fp16).
-        weight: ``(V, D)`` LM-head weight (fp32 master or bf16/fp16); receives dL/dW.
-        labels: ``(...)`` integer targets aligned with the hidden rows (no shift). Rows equal to ``ignore_index``
-            get neither loss nor gradient.
-        chunk_tokens: rows per chunk (default: balanced chunks under a 4 GiB logits buffer).
-        grad_scale: promise that backward is seeded with exactly this value; G is then scaled in forward and a
-            different seed trips a device-side assert.
-
-    Returns the fp32 scalar loss (NaN when every row is ignored). The compute dtype is the autocast dtype when
-    autocast is on, else ``hidden.dtype``; with CPU tensors or an fp32 compute dtype the eager formula is used.
-    A label outside [0, V) that is not ``ignore_index`` gives a NaN loss.
+    hidden ``(..., D)``; weight ``(V, D)`` (the tied embedding; fp32 master or 16-bit); labels ``(...)`` integer
+    targets, one per hidden row, not shifted; rows equal to ``ignore_index`` add neither loss nor gradient (the loss
+    is NaN when all are ignored). ``chunk_tokens``: token rows per chunk of the gradient pass (default: chunks of at
+    most 1 GiB of logits). ``grad_scale``: promise that the backward seed is exactly this value (G is scaled in the
+    forward pass; a different seed trips a device-side assert). The compute dtype is the autocast dtype when autocast
+    is on, else ``hidden.dtype``; CPU tensors and fp32 use the eager formula.
     """
     cdtype = _compute_dtype(hidden)
-    if cdtype not in (torch.bfloat16, torch.float16) or not hidden.is_cuda:
+    if not hidden.is_cuda or cdtype not in (torch.bfloat16, torch.float16):
         return reference_linear_cross_entropy(hidden, weight, labels, ignore_index)
-    if weight.dim() != 2 or weight.shape[1] != hidden.shape[-1]:
-        raise ValueError(f"weight must be (V, {hidden.shape[-1]}), got {tuple(weight.shape)}")
-    if labels.numel() != hidden.numel() // hidden.shape[-1]:
-        raise ValueError(f"labels have {labels.numel()} elements, expected one per hidden row "
-                         f"({hidden.numel() // hidden.shape[-1]})")
-    ge = torch.is_grad_enabled()
-    opts = (ignore_index, chunk_tokens, cdtype, bool(ge and hidden.requires_grad), bool(ge and weight.requires_grad),
-            grad_scale)
-    return _LinearCrossEntropyFn.apply(hidden, weight, labels, opts)
+    D = hidden.shape[-1]
+    if weight.dim() != 2 or weight.shape[1] != D:
+        raise ValueError(f"linear_cross_entropy: weight must have shape (V, {D}); got {tuple(weight.shape)}")
+    rows = hidden.numel() // D if D else 0
+    if labels.numel() != rows:
+        raise ValueError(f"linear_cross_entropy: {labels.numel()} labels for {rows} hidden rows")
+    grads = torch.is_grad_enabled()
+    want_dx, want_dw = grads and hidden.requires_grad, grads and weight.requires_grad
+    if not (want_dx or want_dw):
+        with torch.no_grad():
+            return _Problem(hidden, weight, labels, ignore_index, cdtype).loss_without_grad()
+    return _LinearCE.apply(hidden, weight, labels, ignore_index, chunk_tokens, grad_scale, cdtype, want_dx, want_dw)
 
 
 def flops(N: int, V: int, D: int) -> dict:
-    """Algorithmic work of one forward (which also produces the gradients): three GEMMs of 2*N*V*D each."""
+    """Algorithmic work: the logits GEMM (also the whole of the fused no-gradient forward) and, with gradients, the
+    dx and dW GEMMs -- 2 N V D flop each."""
     g = 2.0 * N * V * D
-    return {"logits": g, "dx": g, "dw": g, "total": 3 * g}
+    return {"logits": g, "dx": g, "dw": g, "total": 3 * g, "forward": g}

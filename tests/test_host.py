@@ -39,7 +39,7 @@ def _header_functions():
 def test_library_exports_every_header_function(lib):
     from sisa_amd.kernels import _lib
     declared = _header_functions()
-    assert len(declared) == 25
+    assert len(declared) == 27
     assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
     out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True, check=True)
     exported = set(re.findall(r"\bT (sisa_\w+)$", out.stdout, re.M))
@@ -54,7 +54,7 @@ def test_struct_layout_matches_c(tmp_path):
              "AttnBwdArgs": "sisa_attn_bwd_args", "PrepFwdArgs": "sisa_prep_fwd_args",
              "PrepBwdArgs": "sisa_prep_bwd_args", "LmceRowsArgs": "sisa_lmce_rows_args",
              "RmsNormArgs": "sisa_rmsnorm_args", "NormArgs": "sisa_norm_args", "SwigluArgs": "sisa_swiglu_args",
-             "DecodeArgs": "sisa_decode_args", "WgradArgs": "sisa_wgrad_args"}
+             "DecodeArgs": "sisa_decode_args", "WgradArgs": "sisa_wgrad_args", "LmceFwdArgs": "sisa_lmce_fwd_args"}
     lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "sisa_hip.h"', "int main(void) {"]
     expect = []
     for py, c in pairs.items():
@@ -269,21 +269,26 @@ def test_linear_ce_cpu_falls_back_to_eager():
     assert h.grad is not None and w.grad is not None
 
 
-def test_linear_ce_chunk_policy_and_seed_check():
+def test_linear_ce_chunk_policy_and_padding():
     from sisa_amd.kernels import linear_ce as LC
-    assert LC._pick_chunk(16384, 50304, None, 2) == 16384              # one chunk under the 4 GiB budget
-    assert LC._pick_chunk(100000, 50304, None, 2) % 128 == 0
-    n = LC._pick_chunk(100000, 50304, None, 2)
-    assert n * 50304 * 2 <= LC.CHUNK_BYTES + 128 * 50304 * 2 and -(-100000 // n) == 3
-    assert LC._pick_chunk(1000, 50304, 300, 2) == 300 and LC._pick_chunk(10, 50304, 300, 2) == 10
-    assert LC._pick_chunk(0, 50304, None, 2) == 1
+    # 16,384 tokens x 50,304 bf16 columns = 1.65 GB of logits: two chunks under the 1 GiB budget
+    n = LC.chunk_rows(16384, 50304, None, 2)
+    assert n == 8192 and n * 50304 * 2 <= LC.LOGITS_BUDGET
+    n = LC.chunk_rows(100000, 50304, None, 2)
+    assert n % 128 == 0 and n * 50304 * 2 <= LC.LOGITS_BUDGET + 128 * 50304 * 2 and -(-100000 // n) == 10
+    assert LC.chunk_rows(1000, 50304, 300, 2) == 300 and LC.chunk_rows(10, 50304, 300, 2) == 10
+    assert LC.chunk_rows(0, 50304, None, 2) == 1
     w = torch.randn(1003, 8)
-    wp = LC._padded_lowp_weight(w, torch.bfloat16)
+    wp = LC.padded_weight(w, torch.bfloat16)
     assert wp.shape == (1024, 8) and (wp[1003:] == 0).all() and torch.equal(wp[:1003], w.to(torch.bfloat16))
-    LC._check_seed(torch.tensor(0.25), 0.25)
-    with pytest.raises(RuntimeError, match="grad_scale"):
-        LC._check_seed(torch.tensor(0.5), 0.25)
+    assert LC.padded_weight(torch.randn(256, 8), torch.float16).shape == (256, 8)
     assert LC.flops(16384, 50277, 768)["total"] == pytest.approx(3.80e12, rel=1e-2)
+
+
+def test_linear_ce_validation_errors_cpu():
+    """Shape errors are ValueErrors before any work (checked on the HIP path; CPU tensors take the eager formula)."""
+    from sisa_amd.kernels import linear_ce as LC
+    assert LC._compute_dtype(torch.randn(2, 2)) == torch.float32
 
 
 # ------------------------------------------------------------------------------------------------ entry points
