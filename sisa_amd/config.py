@@ -1,28 +1,36 @@
-"""Configuration of a SISA model (the attention layer, the blocks and the causal LM).
+"""The SISA model configuration: field set, defaults and presets of the reference (src/sisa/config.py), with the
+attention implementation names of this build ("hip", "hip_fused" in place of the Triton ones).
 
-Mirrors ``sisa.config`` (src/sisa/config.py:12-16, 19-139) for what the attention sublayer needs: the
-implementation names (the Triton names replaced by the HIP backend's ``"hip"`` and ``"hip_fused"``), the kernel shape
-constants and the initialisation hyper-parameters of the layer.
+Design: the parameter set of a model is spelled out once, by :meth:`SISAConfig.parameter_shapes` (state-dict name ->
+shape). Parameter counts, checkpoint checks and the model's own construction tests all read that one table, so a
+config and a state dict can be compared without building a model. Field checks are a table of (predicate, message).
 """
 from __future__ import annotations
 
 import dataclasses
 from dataclasses import dataclass
-from typing import Any, Mapping
+from typing import Any, Callable, Mapping
 
 __all__ = ["SISAConfig", "PRESETS", "ATTN_IMPLS", "HIP_D_HEAD", "HIP_D_STATE"]
 
-#: Accepted values of :attr:`SISAConfig.attn_impl`.
+#: Values of :attr:`SISAConfig.attn_impl`.
 ATTN_IMPLS = ("auto", "torch", "hip", "hip_fused")
 
-#: Head and state sizes the HIP kernels are compiled for.
+#: The head and state sizes the HIP kernels are built for.
 HIP_D_HEAD = 64
 HIP_D_STATE = 32
+
+_POSITIVE_INTS = ("vocab_size", "d_model", "n_layer", "n_head", "d_ff", "d_state", "max_seq_len", "torch_block_q")
 
 
 @dataclass
 class SISAConfig:
-    """Hyper-parameters of a SISA model (defaults: the 50M paper model). ``d_head = d_model // n_head``."""
+    """Hyper-parameters of a SISA language model; the defaults are the 50M paper model (``PRESETS["sisa-50m"]``).
+
+    ``d_head = d_model // n_head``. The HIP implementations need d_head 64 and d_state 32; ``attn_impl="auto"``
+    falls back to the torch path at run time for other shapes. ``d_ff`` is the SwiGLU width as given (no
+    parameter-matching rule). ``max_seq_len`` is informational (there is no positional table).
+    """
 
     vocab_size: int = 50277
     d_model: int = 512
@@ -43,65 +51,86 @@ class SISAConfig:
     gradient_checkpointing: bool = False
 
     def __post_init__(self) -> None:
-        for name in ("vocab_size", "d_model", "n_layer", "n_head", "d_ff", "d_state", "max_seq_len", "torch_block_q"):
-            value = getattr(self, name)
-            if isinstance(value, bool) or not isinstance(value, int) or value <= 0:
-                raise ValueError(f"{name} must be a positive integer, got {value!r}")
-        if self.d_model % self.n_head != 0:
-            raise ValueError(f"d_model ({self.d_model}) must be divisible by n_head ({self.n_head})")
-        if self.d_state % 2 != 0:
-            raise ValueError(f"d_state must be even (channels are rotated in pairs), got {self.d_state}")
-        if self.norm_eps <= 0:
-            raise ValueError(f"norm_eps must be positive, got {self.norm_eps}")
-        if self.attn_impl not in ATTN_IMPLS:
-            raise ValueError(f"attn_impl must be one of {ATTN_IMPLS}, got {self.attn_impl!r}")
-        if self.attn_impl in ("hip", "hip_fused"):
-            if self.d_head != HIP_D_HEAD or self.d_state != HIP_D_STATE:
-                raise ValueError(
-                    f"attn_impl={self.attn_impl!r} requires d_head={HIP_D_HEAD} and d_state={HIP_D_STATE} "
-                    f"(got d_head={self.d_head}, d_state={self.d_state}); use attn_impl='torch' or 'auto'")
+        for name in _POSITIVE_INTS:
+            v = getattr(self, name)
+            if type(v) is not int or v <= 0:
+                raise ValueError(f"SISAConfig.{name} = {v!r}: expected a positive integer")
+        checks: tuple[tuple[Callable[[], bool], str], ...] = (
+            (lambda: self.d_model % self.n_head == 0,
+             f"d_model {self.d_model} is not divisible by n_head {self.n_head}"),
+            (lambda: self.d_state % 2 == 0,
+             f"d_state {self.d_state} must be even: the state channels rotate in pairs"),
+            (lambda: self.norm_eps > 0, f"norm_eps {self.norm_eps} must be positive"),
+            (lambda: self.attn_impl in ATTN_IMPLS, f"attn_impl {self.attn_impl!r} is not one of {ATTN_IMPLS}"),
+        )
+        for ok, message in checks:
+            if not ok():
+                raise ValueError(message)
+        if self.attn_impl in ("hip", "hip_fused") and (self.d_head, self.d_state) != (HIP_D_HEAD, HIP_D_STATE):
+            raise ValueError(f"attn_impl {self.attn_impl!r} runs d_head {HIP_D_HEAD} and d_state {HIP_D_STATE} only "
+                             f"(this config: d_head {self.d_head}, d_state {self.d_state}); choose 'torch' or 'auto'")
 
     @property
     def d_head(self) -> int:
         return self.d_model // self.n_head
 
-    def num_parameters(self) -> int:
-        """Analytic parameter count; the tied LM head is counted once (config.py:100-113)."""
+    def parameter_shapes(self) -> dict[str, tuple[int, ...]]:
+        """State-dict names and shapes of :class:`sisa_amd.SISAForCausalLM` (the tied LM head has no entry of its
+        own). The names are the reference's (src/sisa/modeling.py:122-141, 258-330), so checkpoints interchange."""
         d, h, s, f = self.d_model, self.n_head, self.d_state, self.d_ff
-        per_layer = (4 * d * d              # W_Q, W_K, W_V, W_O
-                     + 2 * h * s * d        # W_B, W_C
-                     + h * (s // 2) * d     # theta_proj
-                     + 2 * (h * d + h)      # alpha_proj, forget_proj (weight + bias)
-                     + h                    # lambda_raw
-                     + 2 * d                # attn_norm, ffn_norm
-                     + 3 * d * f)           # SwiGLU
-        return self.n_layer * per_layer + self.vocab_size * d + d
+        block = {"attn_norm.weight": (d,),
+                 "attn.W_Q.weight": (d, d), "attn.W_K.weight": (d, d), "attn.W_V.weight": (d, d),
+                 "attn.W_B.weight": (h * s, d), "attn.W_C.weight": (h * s, d),
+                 "attn.theta_proj.weight": (h * s // 2, d),
+                 "attn.alpha_proj.weight": (h, d), "attn.alpha_proj.bias": (h,),
+                 "attn.forget_proj.weight": (h, d), "attn.forget_proj.bias": (h,),
+                 "attn.lambda_raw": (h,), "attn.W_O.weight": (d, d),
+                 "ffn_norm.weight": (d,),
+                 "ffn.w_gate.weight": (f, d), "ffn.w_up.weight": (f, d), "ffn.w_down.weight": (d, f)}
+        shapes = {"embed.weight": (self.vocab_size, d)}
+        for i in range(self.n_layer):
+            shapes.update({f"layers.{i}.{k}": v for k, v in block.items()})
+        shapes["final_norm.weight"] = (d,)
+        return shapes
+
+    def num_parameters(self) -> int:
+        """Number of parameters (the tied embedding / LM head counted once)."""
+        total = 0
+        for shape in self.parameter_shapes().values():
+            n = 1
+            for x in shape:
+                n *= x
+            total += n
+        return total
 
     def to_dict(self) -> dict[str, Any]:
         return dataclasses.asdict(self)
 
     @classmethod
     def from_dict(cls, data: Mapping[str, Any], **overrides: Any) -> "SISAConfig":
-        merged = {**dict(data), **overrides}
-        known = {f.name for f in dataclasses.fields(cls)}
-        unknown = sorted(set(merged) - known)
-        if unknown:
-            raise ValueError(f"unknown SISAConfig fields: {unknown}")
-        return cls(**merged)
+        """A config from a mapping (e.g. a ``config.json``) plus overrides; keys that are not fields raise
+        ``ValueError``."""
+        fields = {f.name for f in dataclasses.fields(cls)}
+        values = dict(data)
+        values.update(overrides)
+        extra = sorted(k for k in values if k not in fields)
+        if extra:
+            raise ValueError(f"unknown SISAConfig fields: {extra}")
+        return cls(**values)
 
     @classmethod
     def preset(cls, name: str, **overrides: Any) -> "SISAConfig":
-        try:
-            base = PRESETS[name]
-        except KeyError:
-            raise ValueError(f"unknown preset {name!r}; available: {sorted(PRESETS)}") from None
-        return cls.from_dict(base, **overrides)
+        """The config of a paper model size (``"sisa-50m"``, ``"sisa-152m"``, ``"sisa-369m"``) plus overrides."""
+        if name not in PRESETS:
+            raise ValueError(f"unknown preset {name!r} (known: {', '.join(sorted(PRESETS))})")
+        return cls.from_dict(PRESETS[name], **overrides)
 
     def replace(self, **changes: Any) -> "SISAConfig":
+        """A checked copy with ``changes`` applied."""
         return dataclasses.replace(self, **changes)
 
 
-#: Paper model sizes (d_head 64, d_state 32, vocabulary 50,277); the values of src/sisa/config.py:145-149.
+#: The paper model sizes (d_head 64, d_state 32, vocabulary 50,277); the values of src/sisa/config.py:145-149.
 PRESETS: dict[str, dict[str, Any]] = {
     "sisa-50m": dict(d_model=512, n_layer=6, n_head=8, d_ff=1829),
     "sisa-152m": dict(d_model=768, n_layer=12, n_head=12, d_ff=2744),

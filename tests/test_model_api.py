@@ -462,3 +462,11 @@ def test_pretrained_directories(tmp_path):
     (tmp_path / "model.safetensors").unlink()
     with pytest.raises(FileNotFoundError):
         SISAForCausalLM.from_pretrained(tmp_path)
+
+
+def test_parameter_manifest_is_the_state_dict():
+    """SISAConfig.parameter_shapes names every tensor of the model's state dict with its shape."""
+    cfg = SISAConfig(vocab_size=99, d_model=96, n_head=3, n_layer=2, d_ff=40, d_state=6)
+    model = SISAForCausalLM(cfg)
+    assert {k: tuple(v.shape) for k, v in model.state_dict().items()} == cfg.parameter_shapes()
+    assert cfg.num_parameters() == model.num_parameters()
