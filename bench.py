@@ -161,11 +161,11 @@ def prep_kernel_rates(proj, z, H: int) -> dict:
     dev = proj.device
     lib = _lib.load()
     st = _lib.stream_of(proj)
-    pf = FP._launch_prep_forward(proj, z, H)
+    pf = FP.prep_forward(proj, z, H)
     fa = _lib.PrepFwdArgs(B, L, H, _lib.dtype_code(proj.dtype), proj.data_ptr(), proj.stride(0), proj.stride(1),
-                          _lib.ptr(z), z.stride(0), z.stride(1), pf["CR"].data_ptr(), pf["BR"].data_ptr(),
-                          pf["G"].data_ptr(), _lib.ptr(pf["F"]), pf["ROWF"].data_ptr(), pf["COLF"].data_ptr(),
-                          pf["TOT"].data_ptr())
+                          _lib.ptr(z), z.stride(0), z.stride(1), pf.cr.data_ptr(), pf.br.data_ptr(),
+                          pf.g.data_ptr(), _lib.ptr(pf.f), pf.rowf.data_ptr(), pf.colf.data_ptr(),
+                          pf.totals.data_ptr())
     gen = torch.Generator().manual_seed(9)
     dg, dF = (torch.randn(B, H, L, generator=gen).to(dev) for _ in range(2))
     DCR, DBR = (torch.randn(B, L, H, 32, generator=gen).to(dev) for _ in range(2))
@@ -173,7 +173,7 @@ def prep_kernel_rates(proj, z, H: int) -> dict:
     DZ = torch.empty(B, L, H, device=dev)
     ws = torch.empty((_lib.workspace_bytes("sisa_prep_bwd_workspace_bytes", B, L, H),), device=dev, dtype=torch.uint8)
     ba = _lib.PrepBwdArgs(B, L, H, _lib.dtype_code(proj.dtype), proj.data_ptr(), proj.stride(0), proj.stride(1),
-                          _lib.ptr(z), z.stride(0), z.stride(1), pf["TOT"].data_ptr(), dg.data_ptr(), dF.data_ptr(),
+                          _lib.ptr(z), z.stride(0), z.stride(1), pf.totals.data_ptr(), dg.data_ptr(), dF.data_ptr(),
                           DCR.data_ptr(), DBR.data_ptr(), DP.data_ptr(), DP.stride(0), DP.stride(1), DZ.data_ptr(),
                           DZ.stride(0), DZ.stride(1), ws.data_ptr())
 
@@ -609,25 +609,24 @@ def main():
         e = [ev() for _ in range(5)] if record else None
         if record:
             e[0].record()
-        pf = FP._launch_prep_forward(proj, z, H)
+        pf = FP.prep_forward(proj, z, H)
         if record:
             e[1].record()
         q, k, v = col(proj, "Q"), col(proj, "K"), col(proj, "V")
-        c, b = pf["CR"].transpose(1, 2), pf["BR"].transpose(1, 2)
-        o, lse, _, _, _, o32 = A.attn_forward(q, k, v, c, b, pf["G"], lam, pf["F"], factors=(pf["ROWF"], pf["COLF"]),
-                                              want32=True)
+        c, b = pf.state_views()
+        o, lse, _, _, o32 = A.attn_forward(q, k, v, c, b, pf.g, lam, pf.f, factors=(pf.rowf, pf.colf), want32=True)
         if record:
             e[2].record()
         DP = torch.empty_like(proj)
         DCR = torch.empty((B, L, H, S), device=dev, dtype=torch.float32)
         DBR = torch.empty_like(DCR)
         do = dy.reshape(B, L, H, D).transpose(1, 2)
-        _, _, _, _, _, dg, dlam, dF = A.attn_backward(q, k, v, c, b, pf["G"], pf["F"], pf["ROWF"], pf["COLF"], lam, o,
+        _, _, _, _, _, dg, dlam, dF = A.attn_backward(q, k, v, c, b, pf.g, pf.f, pf.rowf, pf.colf, lam, o,
                                                       lse, do, True, dq=col(DP, "Q"), dk=col(DP, "K"), dv=col(DP, "V"),
                                                       dc=DCR.transpose(1, 2), db=DBR.transpose(1, 2), o32=o32)
         if record:
             e[3].record()
-        FP._launch_prep_backward(proj, z, pf["TOT"], dg, dF, DCR, DBR, DP, H)
+        FP.prep_backward(proj, z, pf.totals, dg, dF, DCR, DBR, DP, H)
         if record:
             e[4].record()
             for i, k_ in enumerate(marks):

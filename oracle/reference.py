@@ -102,6 +102,19 @@ def dense_attention(q, k, v, c, b, g, lam, Fg=None):
     return torch.matmul(torch.softmax(s, -1), v)
 
 
+def decode_rows(q, k, v, c, b, g_k, lam, f_k, q_start):
+    """o of the M query rows at positions q_start .. q_start+M-1 (q, c: (B, H, M, .)) over the cached keys 0 .. N-1
+    (k, v, b, g_k, f_k), N = q_start + M: the decode step of src/sisa/modeling.py:224-238. The rows are placed into
+    zero tensors of length N and scored with :func:`scores` (their g and F values are the cache's last M)."""
+    N, M = k.shape[2], q.shape[2]
+    assert q_start + M == N, (q_start, M, N)
+    qf = q.new_zeros(*q.shape[:2], N, q.shape[-1])
+    cf = c.new_zeros(*c.shape[:2], N, c.shape[-1])
+    qf[:, :, q_start:], cf[:, :, q_start:] = q, c
+    s, _, _, _ = scores(qf, k, cf, b, g_k, f_k, lam, q_start, N)
+    return torch.matmul(torch.softmax(s, -1), v)
+
+
 IN_NAMES = ["q", "k", "v", "c", "b", "g", "lam", "F"]
 GRAD_NAMES = ["dq", "dk", "dv", "dc", "db", "dg", "dlam", "dF"]
 

@@ -1,257 +1,240 @@
-"""Backend selection, device checks, launch configuration and the runtime check mode.
+"""Which SISA attention implementation runs, and how the HIP paths check their inputs.
 
-SISA attention has three implementations of the same function:
+Implementations of one function (the reference's ``attn_impl`` values, src/sisa/backends.py:47, with its Triton
+backends replaced by this build's HIP library):
 
-* ``"torch"``: the exact blocked reference in plain PyTorch (:func:`sisa_amd.functional.sisa_attention_torch`).
-  Works on any device and dtype.
-* ``"hip"``: torch glue (projections, cumulative sums, rotation) plus the gfx950 HIP attention kernels
-  (:func:`sisa_amd.kernels.attention.sisa_attention_hip`).
-* ``"hip_fused"``: one projection GEMM, then the HIP preparation kernels plus the HIP attention kernels
-  (:func:`sisa_amd.kernels.fused_prep.sisa_fused`).
+* ``"torch"``: the exact blocked PyTorch path (:func:`sisa_amd.functional.sisa_attention_torch`), any device/dtype.
+* ``"hip"``: projections etc. in torch, attention on the gfx950 kernels (:mod:`sisa_amd.kernels.attention`).
+* ``"hip_fused"``: one projection GEMM, the HIP preparation kernels and the HIP attention kernels
+  (:mod:`sisa_amd.kernels.fused_prep`).
 
-``"auto"`` picks ``hip_fused`` when eligible, else ``hip``, else ``torch``. Forcing a HIP implementation on an input
-it cannot handle raises ``ValueError``; nothing ever falls back silently. This mirrors the reference's
-``sisa.backends`` (src/sisa/backends.py:1-20, 47, 284-336) with the Triton backends replaced by the HIP library.
-
-HIP requirements: a ROCm build of PyTorch, an AMD Instinct MI355X-class GPU (gfx950; the kernels use
-``v_mfma_f32_16x16x32_{bf16,f16}`` and ``v_cvt_pk_bf16_f32``), the in-tree library ``libsisa_hip.so``,
-``d_head == 64`` and ``d_state == 32``. The fused path additionally needs a bf16/fp16 compute dtype.
+Selection is a table lookup: every HIP implementation has a list of requirements (a GPU that loads the library, the
+kernels' head/state sizes, a compute dtype from its set), and :func:`select_impl` collects the unmet ones. A forced
+implementation with an unmet requirement raises ``ValueError`` naming all of them; ``"auto"`` takes the first HIP
+implementation in preference order with none unmet, and otherwise the torch path, warning once per device and
+reason when that happens on a GPU. Nothing falls back silently.
 """
 from __future__ import annotations
 
 import threading
 import warnings
+from functools import lru_cache
 from typing import TYPE_CHECKING, Union
 
 import torch
+
+from .config import HIP_D_HEAD, HIP_D_STATE
 
 if TYPE_CHECKING:  # pragma: no cover
     from .config import SISAConfig
 
 DeviceLike = Union[torch.device, str, int]
 
-__all__ = [
-    "IMPLS",
-    "hip_status",
-    "fused_eligible",
-    "set_check_mode",
-    "get_check_mode",
-    "describe",
-    "select_impl",
-    "device_info",
-    "attention_config",
-]
+__all__ = ["IMPLS", "CHECK_MODES", "hip_status", "fused_eligible", "set_check_mode", "get_check_mode", "describe",
+           "select_impl", "device_info", "attention_config", "compute_dtype", "warn_fallback",
+           "reset_fallback_warnings"]
 
 IMPLS = ("auto", "torch", "hip", "hip_fused")
-SUPPORTED_ARCHS = ("gfx950",)
+#: gfx targets the library is compiled for.
+HIP_ARCHS = ("gfx950",)
+#: Compute dtypes each HIP implementation takes, in the order "auto" tries the implementations.
+_HIP_DTYPES: dict[str, tuple[torch.dtype, ...]] = {
+    "hip_fused": (torch.bfloat16, torch.float16),
+    "hip": (torch.bfloat16, torch.float16, torch.float32),
+}
 
-# Launch configuration of the attention kernels (fixed, no autotuning): the forward runs 128 queries per workgroup of
-# 8 waves (16 query rows per wave), the backward kernels 64 queries (dq) or keys (dk/dv/db) per workgroup of 4 waves;
-# 64-position tiles staged in LDS; decay factors over 64-row blocks (T).
-_ATTN_CFG_ALL = dict(T=64, tile=64, rows_per_wave=16, fwd_rows_per_wg=128, fwd_waves=8, bwd_rows_per_wg=64,
-                     bwd_waves=4)
-
-_CHECK_MODES = ("async", "sync", "off")
-_STATE = {"check": "async"}
-_LOCK = threading.Lock()
-_DEVICE_INFO: dict[int, dict] = {}
-_HIP_STATUS: dict[int, tuple[bool, str]] = {}
-_WARNED: set = set()
+#: Check modes of the HIP paths and what each one does.
+CHECK_MODES: dict[str, str] = {
+    "async": "device-side asserts (torch._assert_async), no host synchronisation; a failed check poisons the HIP "
+             "context and the next GPU call raises",
+    "sync": "one host synchronisation per call; a failed check raises at once (ValueError for a decay g that "
+            "increases, FloatingPointError for a non-finite score input of the fused layer)",
+    "off": "no checks (for timing)",
+}
+_mode = ["async"]
 
 
-# ---------------------------------------------------------------------------------------------------- check mode
+# ------------------------------------------------------------------------------------------------------ check mode
 def set_check_mode(mode: str) -> None:
-    """Set how the HIP paths check their inputs at run time.
+    """Choose how the HIP paths validate inputs: one of :data:`CHECK_MODES` (default ``"async"``).
 
-    ``"async"`` (default): device-side asserts (``torch._assert_async``), no host synchronisation; a failed check
-    stops the device context. ``"sync"``: the check synchronises once per call and raises a Python exception right
-    away (``ValueError`` for a non-monotone decay ``g``, ``FloatingPointError`` for non-finite values in the fused
-    layer). ``"off"``: no checks (benchmarks only). Semantics of the reference (src/sisa/backends.py:75-89).
+    What is checked: the unfused attention's ``g`` does not increase along the sequence (the fused layer builds it
+    monotone), and the fused layer's score inputs (q, k, c, b, lambda, g, F) are finite. Same modes and meanings as
+    the reference (src/sisa/backends.py:75-89).
     """
-    if mode not in _CHECK_MODES:
-        raise ValueError(f"check mode must be one of {_CHECK_MODES}, got {mode!r}")
-    _STATE["check"] = mode
+    if mode not in CHECK_MODES:
+        raise ValueError(f"unknown check mode {mode!r}; choose one of: {', '.join(CHECK_MODES)}")
+    _mode[0] = mode
 
 
 def get_check_mode() -> str:
-    """The current check mode (``"async"``, ``"sync"`` or ``"off"``)."""
-    return _STATE["check"]
+    """The check mode in force (a key of :data:`CHECK_MODES`)."""
+    return _mode[0]
 
 
-# ---------------------------------------------------------------------------------------------------- device facts
-def _cuda_index(device: DeviceLike | None = None) -> int:
+# ------------------------------------------------------------------------------------------------------ device facts
+def _device_index(device: DeviceLike | None) -> int:
     if device is None:
         return torch.cuda.current_device()
     dev = torch.device(device)
     if dev.type != "cuda":
-        raise ValueError(f"not a HIP/CUDA device: {dev}")
-    return dev.index if dev.index is not None else torch.cuda.current_device()
+        raise ValueError(f"{dev} is not a GPU device")
+    return torch.cuda.current_device() if dev.index is None else dev.index
+
+
+@lru_cache(maxsize=None)
+def _properties(index: int) -> tuple:
+    p = torch.cuda.get_device_properties(index)
+    arch = (getattr(p, "gcnArchName", "") or "").split(":")[0]
+    return (("index", index), ("name", p.name), ("arch", arch), ("cu_count", int(p.multi_processor_count)),
+            ("lds_per_block", int(getattr(p, "shared_memory_per_block", 0) or 0)),
+            ("total_memory", int(p.total_memory)))
 
 
 def device_info(device: DeviceLike | None = None) -> dict:
-    """Facts about a GPU that the launch configuration depends on (cached per device)."""
-    idx = _cuda_index(device)
-    info = _DEVICE_INFO.get(idx)
-    if info is not None:
-        return dict(info)
-    p = torch.cuda.get_device_properties(idx)
-    arch = str(getattr(p, "gcnArchName", "") or "")
-    info = dict(
-        index=idx,
-        name=p.name,
-        arch=arch.split(":")[0],
-        cu_count=int(p.multi_processor_count),
-        lds_per_block=int(getattr(p, "shared_memory_per_block", 0) or 0),
-        total_memory=int(p.total_memory),
-    )
-    _DEVICE_INFO[idx] = info
-    return dict(info)
+    """Name, gfx architecture, CU count, LDS per workgroup and memory of a GPU (default: the current one)."""
+    return dict(_properties(_device_index(device)))
 
 
 def attention_config(device: DeviceLike | None, dtype: torch.dtype) -> dict:
-    """Launch configuration of the attention kernels (identical for every dtype; fp32 uses fp32 MFMA)."""
-    if dtype not in (torch.bfloat16, torch.float16, torch.float32):
-        raise ValueError(f"unsupported attention dtype {dtype}")
-    cfg = dict(_ATTN_CFG_ALL)
-    cfg["mfma"] = "v_mfma_f32_16x16x4_f32" if dtype == torch.float32 else "v_mfma_f32_16x16x32_" + (
-        "bf16" if dtype == torch.bfloat16 else "f16")
-    return cfg
+    """The attention kernels' fixed launch geometry (no autotuning) and the MFMA instruction used for ``dtype``.
+
+    Forward: 8 waves x 16 query rows = 128 queries per workgroup; backward: 4 waves x 16 rows = one 64-row decay
+    block of queries (dq) or keys (dk, dv, db) per workgroup; the other operand streams through LDS in 64-position
+    tiles; decay factors are anchored per 64-row block (``T``). The geometry does not depend on the device.
+    """
+    mfma = {torch.bfloat16: "v_mfma_f32_16x16x32_bf16", torch.float16: "v_mfma_f32_16x16x32_f16",
+            torch.float32: "v_mfma_f32_16x16x4_f32"}.get(dtype)
+    if mfma is None:
+        raise ValueError(f"the attention kernels take bf16, fp16 or fp32 inputs, not {dtype}")
+    return dict(T=64, tile=64, rows_per_wave=16, fwd_waves=8, fwd_rows_per_wg=128, bwd_waves=4,
+                bwd_rows_per_wg=64, mfma=mfma)
 
 
-# ---------------------------------------------------------------------------------------------------- eligibility
+# ------------------------------------------------------------------------------------------------------ requirements
 def hip_status(device: DeviceLike | None = None) -> tuple[bool, str]:
-    """Whether the HIP kernels can run on ``device`` (default: the current GPU), with the reason.
+    """``(True, summary)`` if the HIP library runs on ``device`` (default: the current GPU), else ``(False, why)``.
 
-    Returns ``(True, summary)`` or ``(False, why_not)``; cached per device. The counterpart of the reference's
-    ``triton_status`` (src/sisa/backends.py:205-250).
+    The counterpart of the reference's ``triton_status`` (src/sisa/backends.py:205-250): ROCm PyTorch, a visible
+    gfx950 GPU, and ``libsisa_hip.so`` loading with the ABI version this package expects. Cached per device.
     """
     if not getattr(torch.version, "hip", None):
-        return False, "PyTorch is not a ROCm build"
+        return False, "this PyTorch is not a ROCm build"
     if not torch.cuda.is_available():
-        return False, "no HIP device is available"
+        return False, "PyTorch sees no GPU"
     if device is not None and torch.device(device).type != "cuda":
-        return False, f"device {torch.device(device)} is not a GPU device"
-    idx = _cuda_index(device)
-    hit = _HIP_STATUS.get(idx)
-    if hit is not None:
-        return hit
-    with _LOCK:
-        hit = _HIP_STATUS.get(idx)
-        if hit is not None:
-            return hit
-        res = _hip_status_uncached(idx)
-        _HIP_STATUS[idx] = res
-        return res
+        return False, f"{torch.device(device)} is not a GPU device"
+    return _status_of(_device_index(device))
 
 
-def _hip_status_uncached(idx: int) -> tuple[bool, str]:
-    info = device_info(idx)
-    if info["arch"] not in SUPPORTED_ARCHS:
-        return False, f"{info['name']}: architecture {info['arch'] or '?'} is not gfx950"
-    try:
-        from .kernels import _lib
-        _lib.load()
-    except Exception as e:  # noqa: BLE001 - report any load failure as the reason
-        return False, f"loading libsisa_hip.so failed: {type(e).__name__}: {e}"
-    return True, f"HIP kernels on {info['name']} ({info['arch']}, {info['cu_count']} CUs)"
+_status_lock = threading.Lock()
 
 
-def _compute_dtype(x: torch.Tensor) -> torch.dtype:
-    dt = x.device.type
-    try:
-        if torch.is_autocast_enabled(dt):
-            return torch.get_autocast_dtype(dt)
-    except (TypeError, RuntimeError):  # device types without autocast support
-        pass
+@lru_cache(maxsize=None)
+def _status_of(index: int) -> tuple[bool, str]:
+    with _status_lock:      # one library load at a time
+        info = device_info(index)
+        if info["arch"] not in HIP_ARCHS:
+            return False, f"{info['name']} is {info['arch'] or 'an unknown architecture'}; the library is built " \
+                          f"for {', '.join(HIP_ARCHS)}"
+        try:
+            from .kernels import _lib
+            _lib.load()
+        except Exception as e:  # noqa: BLE001 - any load failure is the answer
+            return False, f"libsisa_hip.so does not load ({type(e).__name__}: {e})"
+        return True, f"{info['name']}: {info['arch']}, {info['cu_count']} CUs, libsisa_hip.so loaded"
+
+
+def compute_dtype(x: torch.Tensor) -> torch.dtype:
+    """The dtype a layer's matrix products see for input ``x``: autocast's dtype when autocast is on for ``x``'s
+    device type, else ``x.dtype``."""
+    kind = x.device.type
+    if kind in ("cuda", "cpu") and torch.is_autocast_enabled(kind):
+        return torch.get_autocast_dtype(kind)
     return x.dtype
 
 
+def _unmet(impl: str, x: torch.Tensor, cfg: SISAConfig | None) -> list[str]:
+    """The requirements of HIP implementation ``impl`` that layer input ``x`` and config ``cfg`` do not meet."""
+    if not isinstance(x, torch.Tensor):
+        return [f"the layer input is a {type(x).__name__}, not a tensor"]
+    unmet = []
+    if x.device.type != "cuda":
+        unmet.append(f"the input is on the {x.device.type}, not a GPU")
+    else:
+        ok, why = hip_status(x.device)
+        if not ok:
+            unmet.append(why)
+    if cfg is not None:
+        d_head = cfg.d_model // cfg.n_head
+        if (d_head, cfg.d_state) != (HIP_D_HEAD, HIP_D_STATE):
+            unmet.append(f"the kernels are built for d_head {HIP_D_HEAD} and d_state {HIP_D_STATE}, this model has "
+                         f"{d_head} and {cfg.d_state}")
+    dt = compute_dtype(x)
+    if dt not in _HIP_DTYPES[impl]:
+        names = "/".join(str(d).replace("torch.", "") for d in _HIP_DTYPES[impl])
+        hint = " (run under autocast or with low-precision parameters)" if impl == "hip_fused" else ""
+        unmet.append(f"{impl} computes in {names}, the compute dtype here is {dt}{hint}")
+    return unmet
+
+
 def fused_eligible(x: torch.Tensor) -> bool:
-    """Whether the fused HIP layer path can run for layer input ``x`` (shape checks are done by select_impl)."""
-    if not isinstance(x, torch.Tensor) or x.device.type != "cuda":
-        return False
-    if _compute_dtype(x) not in (torch.bfloat16, torch.float16):
-        return False
-    return hip_status(x.device)[0]
+    """Whether ``hip_fused`` can run for layer input ``x`` as far as device and dtype go (the head/state sizes are
+    :func:`select_impl`'s part)."""
+    return not _unmet("hip_fused", x, None)
 
 
-def _shape_problem(cfg) -> str | None:
-    if cfg is None:
-        return None
-    d_model, n_head = int(cfg.d_model), int(cfg.n_head)
-    d_head = getattr(cfg, "d_head", None)
-    d_head = int(d_head) if d_head is not None else d_model // n_head
-    d_state = int(cfg.d_state)
-    if d_head != 64 or d_state != 32:
-        return f"the HIP kernels need d_head == 64 and d_state == 32 (got d_head={d_head}, d_state={d_state})"
-    return None
+_warned: set = set()
+
+
+def warn_fallback(device: torch.device, reason: str) -> None:
+    """Warn, once per (device, reason), that the torch attention path runs on a GPU in place of a HIP one."""
+    key = (str(device), reason)
+    if key not in _warned:
+        _warned.add(key)
+        warnings.warn(f"SISA: the torch attention implementation runs on {device}: {reason}", stacklevel=3)
+
+
+def reset_fallback_warnings() -> None:
+    """Forget which fallback warnings were given (tests use this to see them again)."""
+    _warned.clear()
 
 
 def select_impl(requested: str, x: torch.Tensor, cfg: SISAConfig | None) -> str:
-    """Resolve ``requested`` (one of ``IMPLS``) to the implementation used for layer input ``x``.
+    """The implementation that runs for ``requested`` (one of :data:`IMPLS`) on layer input ``x``.
 
-    ``"auto"`` returns ``"hip_fused"`` if eligible, else ``"hip"``, else ``"torch"`` (with a one-time warning on a
-    GPU). A forced HIP implementation on an ineligible input raises ``ValueError`` with the reason.
+    ``cfg`` supplies ``d_model``, ``n_head`` and ``d_state`` (``None`` skips the size requirement). ``"torch"`` is
+    returned as is; a forced HIP implementation is returned if every requirement holds and raises ``ValueError``
+    listing the unmet ones otherwise; ``"auto"`` takes ``hip_fused``, then ``hip``, then ``torch``.
     """
     if requested not in IMPLS:
-        raise ValueError(f"attn_impl must be one of {IMPLS}, got {requested!r}")
+        raise ValueError(f"unknown attn_impl {requested!r}; expected one of {IMPLS}")
     if requested == "torch":
         return "torch"
-    on_gpu = isinstance(x, torch.Tensor) and x.device.type == "cuda"
-    if on_gpu:
-        ok, why = hip_status(x.device)
-    else:
-        ok, why = False, f"input is on {x.device.type if isinstance(x, torch.Tensor) else type(x).__name__}, not a GPU"
-    shape = _shape_problem(cfg)
-    cdt = _compute_dtype(x) if isinstance(x, torch.Tensor) else None
-    hip_dtype_ok = cdt in (torch.bfloat16, torch.float16, torch.float32)
-    fused_dtype_ok = cdt in (torch.bfloat16, torch.float16)
-
-    if requested == "hip_fused":
-        if not ok:
-            raise ValueError(f"attn_impl='hip_fused' is not available: {why}")
-        if shape:
-            raise ValueError(f"attn_impl='hip_fused' is not available: {shape}")
-        if not fused_dtype_ok:
-            raise ValueError(f"attn_impl='hip_fused' needs a bf16/fp16 compute dtype (enable autocast or use "
-                             f"low-precision parameters); got {cdt}")
-        return "hip_fused"
-    if requested == "hip":
-        if not ok:
-            raise ValueError(f"attn_impl='hip' is not available: {why}")
-        if shape:
-            raise ValueError(f"attn_impl='hip' is not available: {shape}")
-        if not hip_dtype_ok:
-            raise ValueError(f"attn_impl='hip' supports bf16, fp16 and fp32 compute dtypes; got {cdt}")
-        return "hip"
-    # auto
-    if ok and not shape:
-        if fused_dtype_ok:
-            return "hip_fused"
-        if hip_dtype_ok:
-            return "hip"
-    if on_gpu:
-        reason = why if not ok else (shape or f"compute dtype {cdt}")
-        key = (x.device.index, reason)
-        if key not in _WARNED:
-            _WARNED.add(key)
-            warnings.warn(f"SISA: using the torch attention implementation on the GPU because {reason}", stacklevel=2)
+    if requested != "auto":
+        unmet = _unmet(requested, x, cfg)
+        if unmet:
+            raise ValueError(f"attn_impl={requested!r} is not available: {'; '.join(unmet)}")
+        return requested
+    unmet = {}
+    for impl in _HIP_DTYPES:
+        unmet[impl] = _unmet(impl, x, cfg)
+        if not unmet[impl]:
+            return impl
+    if isinstance(x, torch.Tensor) and x.device.type == "cuda":
+        warn_fallback(x.device, "; ".join(unmet["hip"]))
     return "torch"
 
 
 def describe() -> str:
-    """Human-readable summary of the environment, the HIP status and the default backend choice."""
-    lines = [f"torch {torch.__version__} (HIP {getattr(torch.version, 'hip', None)})", f"check mode: {get_check_mode()}"]
-    if not torch.cuda.is_available():
-        lines.append("GPU: not available -> attn_impl='auto' uses 'torch'")
-        return "\n".join(lines)
-    for idx in range(torch.cuda.device_count()):
-        info = device_info(idx)
-        ok, why = hip_status(idx)
-        lines.append(f"cuda:{idx} {info['name']} ({info['arch']}, {info['cu_count']} CUs)")
-        lines.append(f"  hip kernels: {'available' if ok else 'unavailable'} - {why}")
-        if ok:
-            lines.append("  attn_impl='auto': 'hip_fused' under bf16/fp16 autocast, 'hip' for fp32 inputs")
-        else:
-            lines.append("  attn_impl='auto': 'torch'")
-    return "\n".join(lines)
+    """A report of PyTorch, the check mode, and per GPU the HIP status and what ``attn_impl="auto"`` picks."""
+    out = [f"torch {torch.__version__}, HIP {getattr(torch.version, 'hip', None)}",
+           f"check mode: {get_check_mode()} ({CHECK_MODES[get_check_mode()]})"]
+    gpus = torch.cuda.device_count() if torch.cuda.is_available() else 0
+    if not gpus:
+        out.append("no GPU: attn_impl='auto' runs 'torch'")
+    for i in range(gpus):
+        ok, why = hip_status(i)
+        out.append(f"cuda:{i}: {why}")
+        out.append("  auto: 'hip_fused' for bf16/fp16 compute, 'hip' for fp32" if ok else "  auto: 'torch'")
+    return "\n".join(out)

@@ -1,238 +1,238 @@
-"""Exact SISA attention on gfx950 HIP kernels: host cores, autograd wrapper and the public entry point.
+"""Exact SISA attention on the gfx950 kernels of ``libsisa_hip.so``: the launch cores, the autograd function and the
+public entry point.
 
-    s_ij = q_i.k_j / sqrt(D) + lam_h * exp(g_i - g_j) * (c_i.b_j) + (F_i - F_j)        (j <= i)
-    o_i  = sum_j softmax_j(s_ij) v_j
+    s_ij = q_i.k_j / 8 + lam_h exp(g_i - g_j) (c_i.b_j) + (F_i - F_j)        (j <= i),    o_i = sum_j softmax_j(s_ij) v_j
 
-Mirrors the host side of the reference's ``sisa.kernels.attention`` (src/sisa/kernels/attention.py:666-877): the
-same core functions (``attn_forward``, ``attn_backward``), the same autograd contract (``_SISAAttentionFn``), the
-same validation (``_prepare_inputs``) and the public ``sisa_attention_hip`` (the counterpart of
-``sisa_attention_triton``). The arithmetic runs in ``libsisa_hip.so`` (sisa_amd/csrc/attention.hip).
+Public names and contracts are those of the reference's ``sisa.kernels.attention`` host half
+(src/sisa/kernels/attention.py:686-877): ``attn_forward`` / ``attn_backward`` (no autograd; the fused layer calls them
+with its own factor tables and gradient buffers) and ``sisa_attention_hip`` in place of ``sisa_attention_triton``.
 
-Numerics (as the reference's notes (A)-(E), attention.py:9-78): the decay is applied in fp32 after the c.b product,
-chunk-factored over 64-row blocks; differences are taken before log2(e); the backward uses the exact delta with the
-self-normalised fp32 o'' stored by the forward pass and the delta-free diagonal dS_tt. Deterministic (no atomics).
+The work per call is one C call each way. Forward: ``sisa_factors`` (per-64-row-block decay anchors rowf/colf and the
+largest rise of ``g`` in each block) unless the caller brings factors, then ``sisa_attn_fwd``, which writes ``o`` in
+(B, L, H, D) memory order, the row log-sum-exp (log2 units) and, for the exact backward, the self-normalised fp32
+output o''. Backward: ``sisa_attn_bwd`` (dq, then dk/dv/db with the per-block dlambda sums, then the dlambda total in
+fp64; deterministic). All numerics live in csrc/attention.hip and csrc/attention_bwd.hip.
 """
 from __future__ import annotations
 
 import math
+from typing import NamedTuple
 
 import torch
 
 from .. import backends
+from ..config import HIP_D_HEAD, HIP_D_STATE
 from . import _lib
 
-__all__ = ["sisa_attention_hip", "attn_forward", "attn_backward"]
+__all__ = ["sisa_attention_hip", "attn_forward", "attn_backward", "kernel_operands", "Forward", "Grads"]
 
-# Maximum allowed increase of g between neighbouring positions (fp32 cumulative sums of non-positive increments can
-# rise by a few ulps). Reference: attention.py:125.
+#: Largest rise of ``g`` between neighbours that still counts as non-increasing: fp32 cumulative sums of non-positive
+#: steps can go up by a few ulps (the reference allows 1e-3, src/sisa/kernels/attention.py:125).
 MONOTONE_TOL = 1e-3
+#: Decay-factor block of the kernels (rows per rowf/colf anchor).
 BLOCK = 64
+_INPUT_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 
 
-def _aligned(x: torch.Tensor) -> bool:
-    """Rows readable with 16-byte vector loads: contiguous last axis, 16-byte aligned base and row strides."""
-    es = x.element_size()
+class Forward(NamedTuple):
+    """Result of :func:`attn_forward`: ``o`` (B, H, L, D) in (B, L, H, D) memory order, ``lse`` (B, H, L) fp32 in log2
+    units, the decay factors ``rowf``/``colf`` (B, H, L) fp32, and ``o32`` -- the fp32 self-normalised output for the
+    exact backward (``o`` itself for fp32 inputs) or ``None`` when not asked for."""
+    o: torch.Tensor
+    lse: torch.Tensor
+    rowf: torch.Tensor
+    colf: torch.Tensor
+    o32: torch.Tensor | None
+
+
+class Grads(NamedTuple):
+    """Result of :func:`attn_backward`; ``dlam`` is (H,) and ``dF`` is ``None`` without a forget gate."""
+    dq: torch.Tensor
+    dk: torch.Tensor
+    dv: torch.Tensor
+    dc: torch.Tensor
+    db: torch.Tensor
+    dg: torch.Tensor
+    dlam: torch.Tensor
+    dF: torch.Tensor | None
+
+
+def _vector_rows(x: torch.Tensor) -> bool:
+    """Rows of ``x`` can be read with 16-byte loads: unit last stride, 16-byte aligned base and outer strides."""
     if x.stride(-1) != 1 or x.data_ptr() % 16:
         return False
-    return all((s * es) % 16 == 0 for s in x.stride()[:-1])
+    return all(s * x.element_size() % 16 == 0 for s in x.stride()[:-1])
 
 
-def _ready(x: torch.Tensor) -> torch.Tensor:
-    return x if _aligned(x) else x.contiguous()
+def _readable(x: torch.Tensor) -> torch.Tensor:
+    return x if _vector_rows(x) else x.contiguous()
 
 
-def _like(x: torch.Tensor) -> torch.Tensor:
-    return torch.empty_like(x) if _aligned(x) else torch.empty(x.shape, device=x.device, dtype=x.dtype)
+def _output_like(x: torch.Tensor) -> torch.Tensor:
+    """A gradient buffer for ``x``: its strides when those are vector-readable, else contiguous."""
+    return torch.empty_like(x) if _vector_rows(x) else torch.empty(x.shape, device=x.device, dtype=x.dtype)
 
 
-def _check_monotone(mono: torch.Tensor, mode: str) -> None:
-    if mode == "off":
-        return
+def _enforce_monotone(rise: torch.Tensor, mode: str) -> None:
+    """Check the per-block maxima of ``g[t+1] - g[t]`` written by the factor kernel against MONOTONE_TOL."""
     if mode == "sync":
-        mx = float(mono.max())
-        if not mx <= MONOTONE_TOL:
-            raise ValueError(f"g must be non-increasing along the sequence (max increase {mx:.3e} > {MONOTONE_TOL})")
-    else:
-        torch._assert_async(mono.max() <= MONOTONE_TOL, "SISA attention: g must be non-increasing along the sequence")
+        worst = rise.max().item()
+        if not worst <= MONOTONE_TOL:     # also catches NaN
+            raise ValueError(f"sisa_attention_hip: g rises by {worst:.3e} between neighbouring positions (more than "
+                             f"{MONOTONE_TOL}); the cumulative log-decay must not increase along the sequence")
+    elif mode == "async":
+        torch._assert_async(rise.max() <= MONOTONE_TOL,
+                            "sisa_attention_hip: the cumulative log-decay g increases along the sequence")
 
 
 def compute_factors(g: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """rowf, colf ((B,H,L) fp32 contiguous) and the per-64-block maximum increase of g."""
+    """``rowf``, ``colf`` ((B, H, L) fp32) and the largest rise of ``g`` in each 64-row block (B*H*ceil(L/64))."""
     B, H, L = g.shape
-    nt = -(-L // BLOCK)
     rowf = torch.empty((B, H, L), device=g.device, dtype=torch.float32)
     colf = torch.empty_like(rowf)
-    mono = torch.empty((B * H * nt,), device=g.device, dtype=torch.float32)
+    rise = torch.empty((B * H * -(-L // BLOCK),), device=g.device, dtype=torch.float32)
     _lib.call("sisa_factors", _lib.FactorsArgs(B, H, L, _lib.view(g), rowf.data_ptr(), colf.data_ptr(),
-                                                mono.data_ptr()), g)
-    return rowf, colf, mono
+                                                rise.data_ptr()), g)
+    return rowf, colf, rise
 
 
-def attn_forward(q, k, v, c, b, g, lam, fgate, factors=None, check=None, want32=False):
-    """Forward core (no autograd).
+def attn_forward(q, k, v, c, b, g, lam, fgate, factors=None, check=None, want32=False) -> Forward:
+    """Forward launch on kernel-ready operands (see :func:`kernel_operands`); no autograd.
 
-    ``factors=(rowf, colf)`` (built by the fused preparation, 64-row blocks) skips the factor kernel and the
-    monotonicity check. ``check`` overrides the global check mode. ``want32=True`` also returns the self-normalised
-    fp32 o'' = sum DT(pe)v / sum DT(pe) as a contiguous (B,H,L,D) tensor (fp32 inputs: o itself).
-
-    Returns ``(o, lse, rowf, colf, cfg, o32 or None)``; o is a (B,H,L,D) tensor in (B,L,H,D) memory layout and lse
-    is in log2 units. Reference: attention.py:686-727.
+    ``factors=(rowf, colf)``: anchors the caller already has (the fused layer builds them in its preparation pass);
+    then neither the factor kernel nor the monotonicity check runs. ``check``: a check mode for this call in place of
+    :func:`sisa_amd.backends.get_check_mode`. ``want32``: also produce the fp32 self-normalised output o''.
     """
     B, H, L, D = q.shape
-    dev = q.device
-    cfg = backends.attention_config(dev, q.dtype)
-    has_f = fgate is not None
+    backends.attention_config(q.device, q.dtype)          # rejects dtypes the kernels do not take
     if factors is None:
-        rowf, colf, mono = compute_factors(g)
+        rowf, colf, rise = compute_factors(g)
         if L > 1:
-            _check_monotone(mono, backends.get_check_mode() if check is None else check)
+            _enforce_monotone(rise, backends.get_check_mode() if check is None else check)
     else:
         rowf, colf = factors
-        assert rowf.is_contiguous() and colf.is_contiguous()
-    # o in (B,L,H,D) memory layout, so the layer's transpose(1,2).reshape is a view
-    o = torch.empty_strided((B, H, L, D), (L * H * D, D, H * D, 1), device=dev, dtype=q.dtype)
-    lse = torch.empty((B, H, L), device=dev, dtype=torch.float32)
-    store32 = bool(want32) and q.dtype != torch.float32
-    o32 = torch.empty((B, H, L, D), device=dev, dtype=torch.float32) if store32 else None
-    args = _lib.AttnFwdArgs(B, H, L, _lib.dtype_code(q.dtype), _lib.view(q), _lib.view(k), _lib.view(v),
-                            _lib.view(c), _lib.view(b), _lib.view(g), _lib.view(fgate if has_f else None),
-                            lam.data_ptr(), lam.stride(0), rowf.data_ptr(), colf.data_ptr(), _lib.view(o),
-                            lse.data_ptr(), _lib.ptr(o32))
-    _lib.call("sisa_attn_fwd", args, q)
-    if want32 and not store32:
-        o32 = o
-    return o, lse, rowf, colf, cfg, o32
+        if not (rowf.is_contiguous() and colf.is_contiguous()):
+            raise ValueError("attn_forward: factor tables must be contiguous (B, H, L) fp32")
+    # (B, L, H, D) memory order: the layer's transpose(1, 2).reshape(B, L, H*D) is then a view
+    o = torch.empty_strided((B, H, L, D), (L * H * D, D, H * D, 1), device=q.device, dtype=q.dtype)
+    lse = torch.empty((B, H, L), device=q.device, dtype=torch.float32)
+    separate32 = want32 and q.dtype != torch.float32
+    o32 = torch.empty((B, H, L, D), device=q.device, dtype=torch.float32) if separate32 else None
+    _lib.call("sisa_attn_fwd", _lib.AttnFwdArgs(
+        B, H, L, _lib.dtype_code(q.dtype), _lib.view(q), _lib.view(k), _lib.view(v), _lib.view(c), _lib.view(b),
+        _lib.view(g), _lib.view(fgate), lam.data_ptr(), lam.stride(0), rowf.data_ptr(), colf.data_ptr(),
+        _lib.view(o), lse.data_ptr(), _lib.ptr(o32)), q)
+    return Forward(o, lse, rowf, colf, o if want32 and not separate32 else o32)
 
 
 def attn_backward(q, k, v, c, b, g, fgate, rowf, colf, lam, o, lse, do, exact=True,
-                  dq=None, dk=None, dv=None, dc=None, db=None, o32=None):
-    """Backward core (no autograd); the exact-delta scheme.
+                  dq=None, dk=None, dv=None, dc=None, db=None, o32=None) -> Grads:
+    """Backward launch; no autograd.
 
-    dq .. db may be caller buffers of any 16-byte-aligned strides (e.g. views of the fused layer's d proj, fp32
-    dc/db). ``o32`` is the self-normalised fp32 o'' of ``attn_forward(want32=True)`` (None: delta = o.do).
-    Returns ``(dq, dk, dv, dc, db, dg, dlam (H,), dF or None)``. Reference: attention.py:730-784.
+    ``dq`` .. ``db``: optional caller buffers with vector-readable rows (the fused layer passes views of its
+    projection gradient, and fp32 ``dc``/``db``). ``exact=True`` is the exact-delta backward, using ``o32`` (the o''
+    of ``attn_forward(want32=True)``) when given; ``exact=False`` is the FlashAttention-standard backward
+    (delta = o.do, no diagonal correction), kept for comparisons.
     """
     B, H, L, D = q.shape
-    dev = q.device
-    has_f = fgate is not None
-    do = _ready(do)
-    dq = _like(q) if dq is None else dq
-    dk = _like(k) if dk is None else dk
-    dv = _like(v) if dv is None else dv
-    dc = _like(c) if dc is None else dc
-    db = _like(b) if db is None else db
+    do = _readable(do)
+    dq, dk, dv, dc, db = (_output_like(ref) if buf is None else buf
+                          for ref, buf in ((q, dq), (k, dk), (v, dv), (c, dc), (b, db)))
+    if not (dq.dtype == dk.dtype == dv.dtype == q.dtype):
+        raise TypeError(f"attn_backward: dq/dk/dv buffers must be {q.dtype}")
     if dc.dtype != db.dtype or dc.dtype not in (q.dtype, torch.float32):
-        raise TypeError(f"dc/db must share dtype {q.dtype} or float32, got {dc.dtype}/{db.dtype}")
-    for name, t in (("dq", dq), ("dk", dk), ("dv", dv), ("dc", dc), ("db", db)):
-        if not _aligned(t):
-            raise ValueError(f"{name} buffer rows must be 16-byte aligned with a contiguous last axis")
-    if dq.dtype != q.dtype or dk.dtype != q.dtype or dv.dtype != q.dtype:
-        raise TypeError("dq/dk/dv buffers must have the dtype of q")
-    f32 = dict(device=dev, dtype=torch.float32)
-    dg = torch.empty((B, H, L), **f32)
-    dF = torch.empty((B, H, L), **f32) if has_f else None
-    dlam = torch.empty((H,), **f32)
-    ws = torch.empty((_lib.workspace_bytes("sisa_attn_bwd_workspace_bytes", B, H, L) // 4,), **f32)
-    has32 = bool(exact) and o32 is not None and o32 is not o
-    if has32:
-        assert o32.shape == (B, H, L, D) and o32.is_contiguous() and o32.dtype == torch.float32
-    args = _lib.AttnBwdArgs(B, H, L, _lib.dtype_code(q.dtype), _lib.dtype_code(dc.dtype),
-                            _lib.view(q), _lib.view(k), _lib.view(v), _lib.view(c), _lib.view(b), _lib.view(g),
-                            _lib.view(fgate if has_f else None), lam.data_ptr(), lam.stride(0),
-                            rowf.data_ptr(), colf.data_ptr(), _lib.view(o), o32.data_ptr() if has32 else None,
-                            lse.data_ptr(), _lib.view(do), _lib.view(dq), _lib.view(dk), _lib.view(dv),
-                            _lib.view(dc), _lib.view(db), dg.data_ptr(), _lib.ptr(dF), dlam.data_ptr(),
-                            ws.data_ptr(), 1 if exact else 0)
-    _lib.call("sisa_attn_bwd", args, q)
-    return dq, dk, dv, dc, db, dg, dlam, dF
+        raise TypeError(f"attn_backward: dc/db buffers must both be {q.dtype} or both float32, got {dc.dtype}/"
+                        f"{db.dtype}")
+    unreadable = [n for n, t in zip(("dq", "dk", "dv", "dc", "db"), (dq, dk, dv, dc, db)) if not _vector_rows(t)]
+    if unreadable:
+        raise ValueError(f"attn_backward: buffers {unreadable} need a unit last stride and 16-byte aligned rows")
+    use32 = bool(exact) and o32 is not None and o32 is not o
+    if use32 and not (o32.shape == (B, H, L, D) and o32.is_contiguous() and o32.dtype == torch.float32):
+        raise ValueError("attn_backward: o32 must be a contiguous (B, H, L, D) float32 tensor")
+    rows = dict(device=q.device, dtype=torch.float32)
+    dg = torch.empty((B, H, L), **rows)
+    dF = None if fgate is None else torch.empty((B, H, L), **rows)
+    dlam = torch.empty((H,), **rows)
+    workspace = torch.empty((_lib.workspace_bytes("sisa_attn_bwd_workspace_bytes", B, H, L) // 4,), **rows)
+    _lib.call("sisa_attn_bwd", _lib.AttnBwdArgs(
+        B, H, L, _lib.dtype_code(q.dtype), _lib.dtype_code(dc.dtype), _lib.view(q), _lib.view(k), _lib.view(v),
+        _lib.view(c), _lib.view(b), _lib.view(g), _lib.view(fgate), lam.data_ptr(), lam.stride(0), rowf.data_ptr(),
+        colf.data_ptr(), _lib.view(o), o32.data_ptr() if use32 else None, lse.data_ptr(), _lib.view(do),
+        _lib.view(dq), _lib.view(dk), _lib.view(dv), _lib.view(dc), _lib.view(db), dg.data_ptr(), _lib.ptr(dF),
+        dlam.data_ptr(), workspace.data_ptr(), int(bool(exact))), q)
+    return Grads(dq, dk, dv, dc, db, dg, dlam, dF)
 
 
 class _SISAAttentionFn(torch.autograd.Function):
-    """Autograd wrapper of the HIP cores (exact-delta backward). Reference: attention.py:788-809."""
+    """Autograd over the two launches. Arguments are kernel-ready operands plus ``exact`` (the public entry passes
+    True; False selects the FlashAttention-standard backward for comparisons)."""
 
     @staticmethod
     def forward(ctx, q, k, v, c, b, g, lam, fgate, exact):
-        need = bool(exact) and any(ctx.needs_input_grad)
-        o, lse, rowf, colf, _, o32 = attn_forward(q, k, v, c, b, g, lam, fgate, want32=need)
-        has_f = fgate is not None
-        ctx.save_for_backward(q, k, v, c, b, g, fgate if has_f else g, rowf, colf, lam, o, lse,
-                              o32 if (need and o32 is not o) else None)
-        ctx.meta = (has_f, bool(exact))
-        return o
+        keep32 = bool(exact) and any(ctx.needs_input_grad)
+        fw = attn_forward(q, k, v, c, b, g, lam, fgate, want32=keep32)
+        extra32 = fw.o32 if keep32 and fw.o32 is not fw.o else None
+        ctx.save_for_backward(q, k, v, c, b, g, fgate, fw.rowf, fw.colf, lam, fw.o, fw.lse, extra32)
+        ctx.exact = bool(exact)
+        return fw.o
 
     @staticmethod
     def backward(ctx, do):
-        q, k, v, c, b, g, Fp, rowf, colf, lam, o, lse, o32 = ctx.saved_tensors
-        has_f, exact = ctx.meta
-        dq, dk, dv, dc, db, dg, dlam, dF = attn_backward(q, k, v, c, b, g, Fp if has_f else None, rowf, colf, lam,
-                                                         o, lse, do, exact, o32=o32)
-        return dq, dk, dv, dc, db, dg, dlam, dF, None
+        q, k, v, c, b, g, fgate, rowf, colf, lam, o, lse, o32 = ctx.saved_tensors
+        gr = attn_backward(q, k, v, c, b, g, fgate, rowf, colf, lam, o, lse, do, ctx.exact, o32=o32)
+        return gr.dq, gr.dk, gr.dv, gr.dc, gr.db, gr.dg, gr.dlam, gr.dF, None
 
 
-def _prepare_inputs(q, k, v, c, b, g, lam, fgate):
-    """Validation and dtype/stride normalisation (reference: attention.py:812-850)."""
-    if q.dim() != 4 or q.shape[-1] != 64 or c.dim() != 4 or c.shape[-1] != 32:
-        raise ValueError(f"the HIP kernels support d_head=64 and d_state=32 only; got q {tuple(q.shape)}, "
-                         f"c {tuple(c.shape)}")
-    if q.dtype not in (torch.bfloat16, torch.float16, torch.float32):
-        raise TypeError(f"q must be bf16, fp16 or fp32, got {q.dtype}")
-    if k.dtype != q.dtype or v.dtype != q.dtype:
-        raise TypeError(f"q/k/v dtypes differ: {q.dtype}, {k.dtype}, {v.dtype}")
-    if not (q.is_cuda and k.device == q.device and v.device == q.device and c.device == q.device
-            and b.device == q.device and g.device == q.device and lam.device == q.device):
-        raise ValueError("all inputs must be on the same GPU device")
+def kernel_operands(q, k, v, c, b, g, lam, fgate):
+    """Check prepared attention inputs against what the kernels take and return them kernel-ready.
+
+    Shapes: q, k, v (B, H, L, 64); c, b (B, H, L, 32); g and fgate (B, H, L); lam (H,); L >= 1 (``ValueError``
+    otherwise). Dtypes: q, k, v one of bf16/fp16/fp32, g and fgate fp32 (``TypeError`` otherwise). Everything on one
+    GPU. c and b are cast to q's dtype and lam to fp32; tensors whose rows are not vector-readable are copied.
+    Same contract as the reference's ``_prepare_inputs`` (src/sisa/kernels/attention.py:812-850).
+    """
+    if q.dim() != 4:
+        raise ValueError(f"sisa_attention_hip: q must be (B, H, L, {HIP_D_HEAD}), got {tuple(q.shape)}")
     B, H, L, _ = q.shape
-    if L < 1:
-        raise ValueError("sequence length must be >= 1")
-    if k.shape != q.shape or v.shape != q.shape:
-        raise ValueError(f"k/v shapes {tuple(k.shape)}/{tuple(v.shape)} != q shape {tuple(q.shape)}")
-    if c.shape != (B, H, L, 32) or b.shape != (B, H, L, 32):
-        raise ValueError(f"c/b must have shape {(B, H, L, 32)}, got {tuple(c.shape)}/{tuple(b.shape)}")
-    if g.dtype != torch.float32:
-        raise TypeError(f"g must be fp32, got {g.dtype}")
-    if g.shape != (B, H, L):
-        raise ValueError(f"g must have shape {(B, H, L)}, got {tuple(g.shape)}")
+    want = {"q": (q, (B, H, L, HIP_D_HEAD)), "k": (k, (B, H, L, HIP_D_HEAD)), "v": (v, (B, H, L, HIP_D_HEAD)),
+            "c": (c, (B, H, L, HIP_D_STATE)), "b": (b, (B, H, L, HIP_D_STATE)), "g": (g, (B, H, L)),
+            "lam": (lam, (H,))}
     if fgate is not None:
-        if fgate.dtype != torch.float32:
-            raise TypeError(f"fgate must be fp32, got {fgate.dtype}")
-        if fgate.shape != g.shape:
-            raise ValueError(f"fgate shape {tuple(fgate.shape)} != g shape {tuple(g.shape)}")
-        if fgate.device != q.device:
-            raise ValueError("all inputs must be on the same GPU device")
-    if lam.shape != (H,):
-        raise ValueError(f"lam must have shape {(H,)}, got {tuple(lam.shape)}")
-    if lam.dtype != torch.float32:
-        lam = lam.float()
-    if c.dtype != q.dtype:
-        c = c.to(q.dtype)
-    if b.dtype != q.dtype:
-        b = b.to(q.dtype)
-    q, k, v, c, b = [_ready(x) for x in (q, k, v, c, b)]
-    return q, k, v, c, b, g, lam, fgate
+        want["fgate"] = (fgate, (B, H, L))
+    misfits = [f"{n} {tuple(t.shape)} (expected {shape})" for n, (t, shape) in want.items() if tuple(t.shape) != shape]
+    if misfits:
+        raise ValueError(f"sisa_attention_hip: the kernels take d_head {HIP_D_HEAD} and d_state {HIP_D_STATE}; "
+                         f"wrong shapes: {', '.join(misfits)}")
+    if L < 1:
+        raise ValueError("sisa_attention_hip: the sequence is empty")
+    if q.dtype not in _INPUT_DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError(f"sisa_attention_hip: q, k, v must share one of bf16/fp16/fp32, got {q.dtype}, {k.dtype}, "
+                        f"{v.dtype}")
+    wide = {n: t.dtype for n, t in (("g", g), ("fgate", fgate)) if t is not None and t.dtype != torch.float32}
+    if wide:
+        raise TypeError(f"sisa_attention_hip: g and fgate must be float32, got {wide}")
+    places = {t.device for t, _ in want.values()}
+    if len(places) != 1 or not q.is_cuda:
+        raise ValueError(f"sisa_attention_hip: all inputs must be on one GPU, got {sorted(map(str, places))}")
+    q, k, v = (_readable(t) for t in (q, k, v))
+    c, b = (_readable(t.to(q.dtype)) for t in (c, b))
+    return q, k, v, c, b, g, lam.to(torch.float32), fgate
 
 
 def sisa_attention_hip(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, c: torch.Tensor, b: torch.Tensor,
                        g: torch.Tensor, lam: torch.Tensor, fgate: torch.Tensor | None = None) -> torch.Tensor:
-    """Exact SISA attention (HIP, gfx950), differentiable with respect to every tensor argument.
+    """Exact SISA attention on the HIP kernels, differentiable in every tensor argument.
 
-    Computes ``o = softmax(s) v`` with, for ``j <= i``,
-    ``s_ij = q_i.k_j / 8 + lam_h * exp(g_i - g_j) * (c_i.b_j) + (fgate_i - fgate_j)``.
+    ``q, k, v``: (B, H, L, 64) bf16/fp16/fp32, any strides with a unit last one; ``c, b``: (B, H, L, 32) rotated
+    state vectors (cast to q's dtype; their gradients return in their own dtype); ``g``: (B, H, L) fp32 cumulative
+    log-decay, non-increasing (checked per :func:`sisa_amd.backends.set_check_mode`); ``lam``: (H,) state-term
+    weights; ``fgate``: (B, H, L) fp32 cumulative log-sigmoid forget gate or ``None``.
 
-    Args:
-        q, k, v: ``(B, H, L, 64)`` bf16, fp16 or fp32. Any strides with a contiguous last dimension.
-        c, b: ``(B, H, L, 32)`` rotated SSM read/write vectors (cast to ``q.dtype`` if they differ).
-        g: ``(B, H, L)`` fp32 cumulative log-decay, non-increasing along L (checked per the check mode).
-        lam: ``(H,)`` fp32 side-term weights ``softplus(lambda_raw)``.
-        fgate: ``(B, H, L)`` fp32 cumulative log-sigmoid forget gate, or ``None``.
-
-    Returns:
-        ``(B, H, L, 64)`` in ``q.dtype``, stored in ``(B, L, H, 64)`` memory layout.
-
-    Deterministic: two calls with the same inputs give bit-identical outputs and gradients.
-    Reference counterpart: ``sisa_attention_triton`` (attention.py:853-877).
+    Returns (B, H, L, 64) in q's dtype, laid out as (B, L, H, 64). Bitwise deterministic, gradients included; the
+    backward is the exact-delta one. Counterpart of the reference's ``sisa_attention_triton``
+    (src/sisa/kernels/attention.py:853-877).
     """
-    q, k, v, c, b, g, lam, fgate = _prepare_inputs(q, k, v, c, b, g, lam, fgate)
-    return _SISAAttentionFn.apply(q, k, v, c, b, g, lam, fgate, True)
+    return _SISAAttentionFn.apply(*kernel_operands(q, k, v, c, b, g, lam, fgate), True)
 
 
 def flops(B: int, H: int, L: int, d_head: int = 64, d_state: int = 32) -> dict:

@@ -70,7 +70,7 @@ def run(ins: dict, exact: bool) -> dict:
     if exact:
         o = A.sisa_attention_hip(*args)
     else:
-        o = A._SISAAttentionFn.apply(*A._prepare_inputs(*args), False)
+        o = A._SISAAttentionFn.apply(*A.kernel_operands(*args), False)
     o.backward(ins["do"])
     torch.cuda.synchronize()
     d = {"o": o.detach(), "dlam": leaves["lam"].grad, "dF": None if Fx is None else Fx.grad}

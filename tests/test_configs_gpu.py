@@ -29,7 +29,7 @@ DEV = "cuda"
 
 # ------------------------------------------------------------------------------------------------ config 1
 def test_config1_fused_layer():
-    from sisa_amd.kernels.fused_prep import _launch_prep_forward, sisa_fused
+    from sisa_amd.kernels.fused_prep import prep_forward, sisa_fused
     from sisa_amd.workloads import config_inputs
 
     inp = config_inputs(1, device=DEV)
@@ -51,13 +51,13 @@ def test_config1_fused_layer():
     y, dP, dl, dz = first
     assert all(bool(torch.isfinite(t).all()) for t in first)
     assert bool((dP[..., off["NTOT"]:] == 0).all()), "pad columns of d proj must be zero"
-    pf = _launch_prep_forward(proj, z, H)
+    pf = prep_forward(proj, z, H)
     glue = R.glue(proj, z, H, dtype=torch.float32)
     dl64 = torch.zeros(H, dtype=torch.float64, device=DEV)
     errs: dict[str, float] = {}
     for r in range(B):
-        vals = dict(q=glue["q"][r:r + 1], k=glue["k"][r:r + 1], c=pf["CR"][r:r + 1].transpose(1, 2),
-                    b=pf["BR"][r:r + 1].transpose(1, 2), g=pf["G"][r:r + 1], F=pf["F"][r:r + 1])
+        vals = dict(q=glue["q"][r:r + 1], k=glue["k"][r:r + 1], c=pf.cr[r:r + 1].transpose(1, 2),
+                    b=pf.br[r:r + 1].transpose(1, 2), g=pf.g[r:r + 1], F=pf.f[r:r + 1])
         y64, dP64, dlr, dz64 = R.fused64(proj[r:r + 1], z[r:r + 1], lam, H, vals, dy[r:r + 1])
         dl64 += dlr.double()
         row = dict(y=R.rel(y[r:r + 1], y64), dz=R.rel(dz[r:r + 1], dz64))

@@ -22,19 +22,18 @@ def _step(proj, z, lam, dy, H):
     def col(t, name, w=64):
         return t[..., off[name]:off[name] + H * w].view(B, L, H, w).transpose(1, 2)
 
-    pf = FP._launch_prep_forward(proj, z, H)
+    pf = FP.prep_forward(proj, z, H)
     q, k, v = col(proj, "Q"), col(proj, "K"), col(proj, "V")
-    c, b = pf["CR"].transpose(1, 2), pf["BR"].transpose(1, 2)
-    o, lse, _, _, _, o32 = A.attn_forward(q, k, v, c, b, pf["G"], lam, pf["F"], factors=(pf["ROWF"], pf["COLF"]),
-                                          want32=True)
+    c, b = pf.state_views()
+    o, lse, _, _, o32 = A.attn_forward(q, k, v, c, b, pf.g, lam, pf.f, factors=(pf.rowf, pf.colf), want32=True)
     DP = torch.empty_like(proj)
     DCR = torch.empty((B, L, H, 32), device=proj.device, dtype=torch.float32)
     DBR = torch.empty_like(DCR)
     do = dy.reshape(B, L, H, 64).transpose(1, 2)
-    _, _, _, _, _, dg, dlam, dF = A.attn_backward(q, k, v, c, b, pf["G"], pf["F"], pf["ROWF"], pf["COLF"], lam, o,
+    _, _, _, _, _, dg, dlam, dF = A.attn_backward(q, k, v, c, b, pf.g, pf.f, pf.rowf, pf.colf, lam, o,
                                                   lse, do, True, dq=col(DP, "Q"), dk=col(DP, "K"), dv=col(DP, "V"),
                                                   dc=DCR.transpose(1, 2), db=DBR.transpose(1, 2), o32=o32)
-    DZ = FP._launch_prep_backward(proj, z, pf["TOT"], dg, dF, DCR, DBR, DP, H)
+    DZ = FP.prep_backward(proj, z, pf.totals, dg, dF, DCR, DBR, DP, H)
     return o, DP, dlam, DZ
 
 

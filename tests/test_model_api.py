@@ -18,7 +18,7 @@ from oracle import model64 as M64
 from model_utils import rel_err, tiny_config, tiny_model, token_ids
 from sisa_amd import PRESETS, SISAAttention, SISABlock, SISAConfig, SISAForCausalLM, sisa_attention
 from sisa_amd import checkpoint as CK
-from sisa_amd.functional import _attend_rows, rotate_pairs, sisa_attention_torch
+from sisa_amd.functional import attend_block, rotate_pairs, sisa_attention_torch
 from sisa_amd.generation import SISACache
 
 V = 257
@@ -150,7 +150,7 @@ def test_loss_and_logits_options():
     out = model(ids, labels=ids)
     assert out.logits.shape == (2, 33, V) and out.logits.dtype == torch.float32 and out.loss.dim() == 0
     assert torch.equal(out.loss, F.cross_entropy(out.logits[:, :-1].reshape(-1, V), ids[:, 1:].reshape(-1)))
-    with pytest.raises(ValueError, match="CUDA"):
+    with pytest.raises(ValueError, match="GPU"):
         model(ids, labels=ids, fused_ce=True)
     no_labels = model(ids, fused_ce=True)                           # fused_ce without labels: plain logits
     assert no_labels.loss is None and torch.equal(no_labels.logits, model(ids).logits)
@@ -297,10 +297,10 @@ def test_torch_attention_is_fp32_under_autocast(block_q):
 
 def test_decode_rows_are_fp32_under_autocast():
     q, k, v, c, b, g, lam, f = _inputs(4, L=40)
-    rows = (q[:, :, -3:], k, v, c[:, :, -3:], b, g[:, :, -3:], g, lam, f[:, :, -3:], f, 37)
-    plain = _attend_rows(*rows)
+    args = ((q[:, :, -3:], c[:, :, -3:], g[:, :, -3:], f[:, :, -3:]), (k, v, b, g, f), lam, 37)
+    plain = attend_block(*args)
     with torch.autocast("cpu", dtype=torch.bfloat16):
-        out = _attend_rows(*rows)
+        out = attend_block(*args)
     assert out.dtype == torch.float32
     torch.testing.assert_close(out, plain, rtol=1e-6, atol=1e-6)
     assert rel_err(out, _dense64(q, k, v, c, b, g, lam, f)[:, :, -3:]) < 1e-5

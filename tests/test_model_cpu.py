@@ -186,7 +186,7 @@ def test_paper_checkpoint_keys(tmp_path):
     bad = dict(sd)
     bad["layers.0.attn.W_Q.weight"] = torch.zeros(3, 3)
     with pytest.raises(ValueError, match="shape mismatch"):
-        CK._load_exact(CK._uninitialised_model(model.config), bad)
+        CK.model_from_state_dict(model.config, bad)
     with pytest.raises(ValueError, match="two checkpoint keys"):
         CK.convert_state_dict({"layers.0.W_Q.weight": sd["layers.0.attn.W_Q.weight"],
                                "layers.0.attn.W_Q.weight": sd["layers.0.attn.W_Q.weight"]})

@@ -15,6 +15,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle import model64 as M64
+from oracle import reference as R
 
 from model_utils import rel_err, tiny_model, token_ids
 
@@ -178,14 +179,13 @@ def _decode_inputs(B, H, M, N, dtype, seed, has_f=True):
                                                  (1, 16, 2, 16384, torch.bfloat16, True),
                                                  (8, 12, 1024, 2048, torch.bfloat16, True)])   # 2 launches
 def test_decode_kernel(B, H, M, N, dtype, has_f):
-    from sisa_amd.functional import _attend_rows
     from sisa_amd.kernels.decode import sisa_decode_hip
     d = _decode_inputs(B, H, M, N, dtype, seed=N + M, has_f=has_f)
     got = sisa_decode_hip(d["q"], d["k"], d["v"], d["c"], d["b"], d["g_q"], d["g_k"], d["lam"], d["f_q"], d["f_k"],
                           d["q_start"])
     f = lambda x: None if x is None else x.double()                      # noqa: E731
-    ref = _attend_rows(f(d["q"]), f(d["k"]), f(d["v"]), f(d["c"]), f(d["b"]), f(d["g_q"]), f(d["g_k"]), f(d["lam"]),
-                       f(d["f_q"]), f(d["f_k"]), d["q_start"])
+    ref = R.decode_rows(f(d["q"]), f(d["k"]), f(d["v"]), f(d["c"]), f(d["b"]), f(d["g_k"]), f(d["lam"]), f(d["f_k"]),
+                        d["q_start"])
     assert got.dtype == torch.float32 and got.shape == (B, H, M, 64)
     assert rel_err(got, ref) < 1e-5
     again = sisa_decode_hip(d["q"], d["k"], d["v"], d["c"], d["b"], d["g_q"], d["g_k"], d["lam"], d["f_q"], d["f_k"],
@@ -313,9 +313,9 @@ def test_auto_selection_and_fallbacks():
     g = torch.cumsum(-torch.rand(1, 2, 80, generator=gen), 2).to(DEV)
     f = torch.cumsum(F.logsigmoid(torch.randn(1, 2, 80, generator=gen)), 2).to(DEV)
     lam = torch.tensor([0.3, 1.0], device=DEV)
-    backends._WARNED.clear()
+    backends.reset_fallback_warnings()
     for g_in, f_in in ((g.bfloat16(), f), (g, f.bfloat16())):
-        with pytest.warns(UserWarning, match="torch attention implementation"):
+        with pytest.warns(UserWarning, match="torch attention implementation runs"):
             out = sisa_attention(q, k, v, c, b, g_in, lam, f_in, impl="auto")
         assert torch.equal(out, sisa_attention_torch(q, k, v, c, b, g_in, lam, f_in))
         with pytest.raises(ValueError, match="float32"):

@@ -209,6 +209,18 @@ def test_blocked_vs_dense(block_q):
     assert torch.allclose(ob, _dense(ins), atol=1e-12)
 
 
+@pytest.mark.parametrize("M", [1, 3, 70])
+def test_decode_rows_are_the_last_rows_of_dense(M):
+    """The decode-step oracle equals the last M rows of the full attention, and changes when a cached key does."""
+    ins = _rand_ins(H=2, L=70, D=16, S=8, seed=7)
+    q, k, v, c, b, g, lam, Fg = (ins[n] for n in ("q", "k", "v", "c", "b", "g", "lam", "F"))
+    rows = R.decode_rows(q[:, :, -M:], k, v, c[:, :, -M:], b, g, lam, Fg, 70 - M)
+    assert torch.allclose(rows, _dense(ins)[:, :, -M:], atol=1e-12)
+    k2 = k.clone()
+    k2[:, :, -2] += 1.0
+    assert not torch.allclose(R.decode_rows(q[:, :, -M:], k2, v, c[:, :, -M:], b, g, lam, Fg, 70 - M), rows)
+
+
 def test_fa_emulation_modes():
     ins = _rand_ins(H=2, L=20, D=64, S=32, seed=7)
     T = R.truth64(ins)

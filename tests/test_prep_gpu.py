@@ -40,28 +40,28 @@ def test_prep_accuracy(B, L, H, seed, hasf, kw):
     from sisa_amd.kernels import attention as A
     proj, z, off = R.make_proj(B, L, H, seed, device=DEV, **kw)
     z = z if hasf else None
-    P = FP()._launch_prep_forward(proj, z, H)
+    P = FP().prep_forward(proj, z, H)
     T = torch_glue(proj, z, H)
     X = R.glue(proj, z, H)
     bad = []
     if L > 1:
-        inc = float((P["G"][..., 1:] - P["G"][..., :-1]).max())
+        inc = float((P.g[..., 1:] - P.g[..., :-1]).max())
         if inc > 0:
             bad.append(f"g not monotone (+{inc:.3e})")
-    eg, egt = R.rel(P["G"], X["g"]), R.rel(T["g"], X["g"])
+    eg, egt = R.rel(P.g, X["g"]), R.rel(T["g"], X["g"])
     if eg > 2 * egt + 1e-7:
         bad.append(f"g error {eg:.2e} > 2x torch {egt:.2e}")
     if hasf:
-        ef, eft = R.rel(P["F"], X["F"]), R.rel(T["F"], X["F"])
+        ef, eft = R.rel(P.f, X["F"]), R.rel(T["F"], X["F"])
         if ef > 2 * eft + 1e-7:
             bad.append(f"F error {ef:.2e} > 2x torch {eft:.2e}")
-    for n, key in (("c", "CR"), ("b", "BR")):
-        e_k = R.rel(P[key].transpose(1, 2), X[n])
+    for n, key in (("c", "cr"), ("b", "br")):
+        e_k = R.rel(getattr(P, key).transpose(1, 2), X[n])
         e_t = R.rel(T[n].to(torch.bfloat16), X[n])
         if e_k > 1.02 * e_t + 1e-7:
             bad.append(f"{n} error {e_k:.2e} above the torch bf16 path {e_t:.2e}")
-    rowf, colf, _ = A.compute_factors(P["G"])
-    if not (torch.equal(rowf, P["ROWF"]) and torch.equal(colf, P["COLF"])):
+    rowf, colf, _ = A.compute_factors(P.g)
+    if not (torch.equal(rowf, P.rowf) and torch.equal(colf, P.colf)):
         bad.append("rowf/colf != factor kernel on the same g")
     assert not bad, "; ".join(bad)
 
@@ -101,10 +101,10 @@ def test_fused_gradients_vs_fp64(B, L, H, seed, hasf):
     z = z if hasf else None
     lam = torch.tensor([0.31, 3.0, 1e-7, 0.8, 0.31, 0.3, 0.29, 0.31][:H], device=DEV)
     dy = torch.randn(B, L, H * 64, generator=torch.Generator().manual_seed(seed + 100)).to(DEV).to(torch.bfloat16)
-    pf = FP()._launch_prep_forward(proj, z, H)
+    pf = FP().prep_forward(proj, z, H)
     glue32 = R.glue(proj, z, H, dtype=torch.float32)
-    vals = {"fused": dict(q=glue32["q"], k=glue32["k"], c=pf["CR"].transpose(1, 2), b=pf["BR"].transpose(1, 2),
-                          g=pf["G"], F=pf["F"]),
+    vals = {"fused": dict(q=glue32["q"], k=glue32["k"], c=pf.state_views()[0], b=pf.state_views()[1],
+                          g=pf.g, F=pf.f),
             "glue": dict(q=glue32["q"], k=glue32["k"], c=glue32["c"].to(torch.bfloat16),
                          b=glue32["b"].to(torch.bfloat16), g=glue32["g"], F=glue32["F"])}
     res = {}

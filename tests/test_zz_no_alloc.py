@@ -23,8 +23,8 @@ def _backward(entry: str, ins: dict, exact: bool = True) -> list[torch.Tensor]:
     from sisa_amd.kernels import _lib
     from sisa_amd.kernels import attention as A
 
-    q, k, v, c, b, g, lam, Fg = A._prepare_inputs(*[ins[n] for n in R.IN_NAMES])
-    o, lse, rowf, colf, _, o32 = A.attn_forward(q, k, v, c, b, g, lam, Fg, want32=exact)
+    q, k, v, c, b, g, lam, Fg = A.kernel_operands(*[ins[n] for n in R.IN_NAMES])
+    o, lse, rowf, colf, o32 = A.attn_forward(q, k, v, c, b, g, lam, Fg, want32=exact)
     B, H, L, _ = q.shape
     do = ins["do"]
     dq, dk, dv, dc, db = (torch.full_like(x, float("nan")) for x in (q, k, v, c, b))
