@@ -28,6 +28,7 @@ from __future__ import annotations
 import torch
 import torch.nn.functional as F
 
+from .. import backends
 from . import _lib
 
 __all__ = ["linear_cross_entropy", "reference_linear_cross_entropy", "lmce_rows", "lmce_fused_loss_rows",
@@ -187,15 +188,6 @@ class _LinearCE(torch.autograd.Function):
         return dh, dW, None, None, None, None, None, None, None
 
 
-def _compute_dtype(t: torch.Tensor) -> torch.dtype:
-    try:
-        if torch.is_autocast_enabled(t.device.type):
-            return torch.get_autocast_dtype(t.device.type)
-    except (RuntimeError, TypeError):
-        pass
-    return t.dtype
-
-
 def reference_linear_cross_entropy(hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor,
                                    ignore_index: int = -100) -> torch.Tensor:
     """``F.cross_entropy(F.linear(hidden, weight).float(), labels, ignore_index=ignore_index)`` over all rows (the
@@ -217,7 +209,7 @@ def linear_cross_entropy(hidden: torch.Tensor, weight: torch.Tensor, labels: tor
     forward pass; a different seed trips a device-side assert). The compute dtype is the autocast dtype when autocast
     is on, else ``hidden.dtype``; CPU tensors and fp32 use the eager formula.
     """
-    cdtype = _compute_dtype(hidden)
+    cdtype = backends.compute_dtype(hidden)
     if not hidden.is_cuda or cdtype not in (torch.bfloat16, torch.float16):
         return reference_linear_cross_entropy(hidden, weight, labels, ignore_index)
     D = hidden.shape[-1]

@@ -285,10 +285,12 @@ def test_linear_ce_chunk_policy_and_padding():
     assert LC.flops(16384, 50277, 768)["total"] == pytest.approx(3.80e12, rel=1e-2)
 
 
-def test_linear_ce_validation_errors_cpu():
-    """Shape errors are ValueErrors before any work (checked on the HIP path; CPU tensors take the eager formula)."""
-    from sisa_amd.kernels import linear_ce as LC
-    assert LC._compute_dtype(torch.randn(2, 2)) == torch.float32
+def test_compute_dtype_follows_autocast():
+    """The compute dtype every HIP path keys on: the input's dtype, or autocast's when autocast is on."""
+    from sisa_amd import backends
+    assert backends.compute_dtype(torch.randn(2, 2)) == torch.float32
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        assert backends.compute_dtype(torch.randn(2, 2)) == torch.bfloat16
 
 
 # ------------------------------------------------------------------------------------------------ entry points
