@@ -23,8 +23,10 @@ ARCH = "gfx950"
 HIPFLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", f"-I{os.path.join(ROOT, 'include')}",
             f"-I{CSRC}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 # Per-source additions: the backward attention kernels (dependency chains of MFMA, exponentials and fp32 row sums)
-# run faster under LLVM's max-ILP machine scheduler, the forward kernel under the default one (measured on MI355X).
-EXTRA_FLAGS = {"attention_bwd.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]}
+# and the fused CE forward (all operand fragments of a step read ahead of its MFMAs) run faster under LLVM's max-ILP
+# machine scheduler, the forward attention kernel under the default one (measured on MI355X).
+_MAX_ILP = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
+EXTRA_FLAGS = {"attention_bwd.hip": _MAX_ILP, "lmce_fwd.hip": _MAX_ILP}
 
 
 def _hipcc() -> str:

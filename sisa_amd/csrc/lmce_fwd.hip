@@ -125,33 +125,41 @@ __global__ __launch_bounds__(64 * NWC) void lmce_fwd_kernel(sisa_lmce_fwd_args a
     for (int g = 0; g < total; ++g) {
         const int buf = g & 1;
         if (g + 1 < total) issue(g + 1, buf ^ 1);
+        // all 12 operand fragments of a 32-deep step are read before its 32 MFMAs (two waves per SIMD leave room
+        // for them), so one LDS wait per step instead of one per 4 MFMAs
 #pragma unroll
         for (int step = 0; step < TK / 32; ++step) {
-            frag8<T> xf[JB];
+            frag8<T> xf[JB], wf[IB];
 #pragma unroll
             for (int j = 0; j < JB; ++j) xf[j] = frag_rows<T, TK>(sm.x[buf], wn + 16 * j, step, lane);
 #pragma unroll
-            for (int i = 0; i < IB; ++i) {
-                const frag8<T> wf = frag_rows<T, TK>(sm.w[buf], wv + 16 * i, step, lane);
+            for (int i = 0; i < IB; ++i) wf[i] = frag_rows<T, TK>(sm.w[buf], wv + 16 * i, step, lane);
 #pragma unroll
-                for (int j = 0; j < JB; ++j) acc[i][j] = mma(wf, xf[j], acc[i][j]);
-            }
+            for (int i = 0; i < IB; ++i)
+#pragma unroll
+                for (int j = 0; j < JB; ++j) acc[i][j] = mma(wf[i], xf[j], acc[i][j]);
         }
         if (g % nks == nks - 1) {
             // the tile is complete: lane holds logits of rows wn + 16 j + lc at columns v0 + wv + 16 i + 4 grp + r
             const int vt = t_begin + g / nks;
-            const int64_t vbase = (int64_t)vt * TV + wv + 4 * grp;
-#pragma unroll
-            for (int j = 0; j < JB; ++j) {
-                float mt = -__builtin_inff();
+            if ((int64_t)(vt + 1) * TV > V) {   // the last tile: padding columns do not enter the sums
+                const int lim = (int)(V - (int64_t)vt * TV) - wv - 4 * grp;
 #pragma unroll
                 for (int i = 0; i < IB; ++i)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const bool in = vbase + 16 * i + r < V;   // padding columns do not enter the sum
-                        acc[i][j][r] = in ? acc[i][j][r] * LOG2E : -__builtin_inff();
-                        mt = fmaxf(mt, acc[i][j][r]);
-                    }
+                    for (int r = 0; r < 4; ++r)
+#pragma unroll
+                        for (int j = 0; j < JB; ++j)
+                            acc[i][j][r] = 16 * i + r < lim ? acc[i][j][r] : -__builtin_inff();
+            }
+#pragma unroll
+            for (int j = 0; j < JB; ++j) {
+                float mt = -__builtin_inff();   // the tile's maximum logit of the row, then in log2 units
+#pragma unroll
+                for (int i = 0; i < IB; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) mt = fmaxf(mt, acc[i][j][r]);
+                mt *= LOG2E;
                 if (mt > m[j]) {
                     s[j] *= fast_exp2(m[j] - mt);
                     m[j] = mt;
@@ -160,9 +168,9 @@ __global__ __launch_bounds__(64 * NWC) void lmce_fwd_kernel(sisa_lmce_fwd_args a
 #pragma unroll
                 for (int i = 0; i < IB; ++i)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) ls += fast_exp2(acc[i][j][r] - m[j]);
+                    for (int r = 0; r < 4; ++r) ls += fast_exp2(fmaf(acc[i][j][r], LOG2E, -m[j]));
                 s[j] += ls;
-                if (lab_tile[j] == vt) {   // rare: pick the label's logit (log2 units)
+                if (lab_tile[j] == vt) {   // rare: pick the label's logit (natural units)
                     float z = 0.f;
 #pragma unroll
                     for (int i = 0; i < IB; ++i)
@@ -186,7 +194,7 @@ __global__ __launch_bounds__(64 * NWC) void lmce_fwd_kernel(sisa_lmce_fwd_args a
     for (int j = 0; j < JB; ++j) {
         rm[j] = group_max(m[j]);
         rsum[j] = group_sum(s[j] * fast_exp2(m[j] - rm[j]));
-        if (got[j]) a.workspace[2 * (int64_t)S * N + row0 + wn + 16 * j + lc] = zlab[j] * LN2;
+        if (got[j]) a.workspace[2 * (int64_t)S * N + row0 + wn + 16 * j + lc] = zlab[j];
     }
     if ((w & 1) && grp == 0) {
 #pragma unroll

@@ -151,7 +151,7 @@ def test_backend_selection_on_cpu():
     with pytest.raises(ValueError):
         backends.select_impl("triton", x, cfg)
     ok, why = backends.hip_status()
-    assert ok is False and why
+    assert why and (ok is False or torch.cuda.is_available())
     assert not backends.fused_eligible(x)
     assert "check mode" in backends.describe()
     assert backends.attention_config(None, torch.bfloat16)["mfma"].endswith("bf16")
