@@ -364,6 +364,58 @@ def test_greedy_generation_equals_the_uncached_argmax_loop():
         model.generate(prompt, 2, do_sample=True, top_k=0)
 
 
+def test_cache_slabs_grow_and_match_concatenation():
+    """SISACache appends in place into preallocated slabs (doubling without a capacity); the state it hands out is
+    the concatenation of everything appended, and earlier views keep their values after a regrowth."""
+    gen = torch.Generator().manual_seed(0)
+    parts = [dict(k=torch.randn(2, 3, n, 8, generator=gen), v=torch.randn(2, 3, n, 8, generator=gen),
+                  b=torch.randn(2, 3, n, 4, generator=gen), g=torch.randn(2, 3, n, generator=gen),
+                  fgate=torch.randn(2, 3, n, generator=gen), phi=torch.randn(2, 3, 2, generator=gen))
+             for n in (5, 1, 1, 7, 1)]
+    for capacity in (None, 64):
+        cache = SISACache(capacity)
+        first = None
+        for i, p in enumerate(parts):
+            st = cache.update(0, **p)
+            if i == 0:
+                first = st.k.clone(), st.k
+        for name in ("k", "v", "b", "g", "fgate"):
+            assert torch.equal(getattr(st, name), torch.cat([p[name] for p in parts], dim=2)), (capacity, name)
+        assert torch.equal(st.phi, parts[-1]["phi"]) and cache.seq_len == 15 and len(cache) == 1
+        assert torch.equal(first[1], first[0])             # the first state's view is unchanged
+        slab = cache._slabs[0]
+        assert slab.capacity == (64 if capacity else 20)   # 5 -> 10 (doubling) -> 20 on the 7-row append
+    with pytest.raises(ValueError):
+        SISACache(0)
+    with pytest.raises(ValueError):
+        SISACache().update(0, **dict(parts[0], g=torch.zeros(2, 3, 4)))
+
+
+def test_cache_keeps_autograd_history():
+    """Appends that carry autograd history are concatenated out of place, so gradients reach every appended part."""
+    a = torch.randn(1, 1, 3, 4, requires_grad=True)
+    b = torch.randn(1, 1, 2, 4, requires_grad=True)
+    z = dict(v=torch.zeros(1, 1, 3, 4), b=torch.zeros(1, 1, 3, 2), g=torch.zeros(1, 1, 3), fgate=torch.zeros(1, 1, 3),
+             phi=torch.zeros(1, 1, 1))
+    cache = SISACache()
+    cache.update(0, k=a, **z)
+    st = cache.update(0, k=b, **{n: t[:, :, :2] if n != "phi" else t for n, t in z.items()})
+    st.k.sum().backward()
+    assert torch.equal(a.grad, torch.ones_like(a)) and torch.equal(b.grad, torch.ones_like(b))
+
+
+def test_top_k_sampling_stays_among_the_k_largest():
+    from sisa_amd.generation import _pick
+    gen = torch.Generator().manual_seed(5)
+    logits = torch.randn(64, 100, generator=gen)
+    top3 = logits.topk(3, dim=-1).indices
+    for _ in range(5):
+        tok = _pick(logits, True, 0.7, 3, gen)
+        assert bool((tok[:, None] == top3).any(-1).all())
+    assert torch.equal(_pick(logits, False, 1.0, None, None), logits.argmax(-1))
+    assert torch.equal(_pick(logits, True, 1.0, 1, gen), logits.argmax(-1))
+
+
 def test_cpu_autocast_decoding_close_to_full_forward():
     model = tiny_model(seed=7)
     ids = token_ids(1, 30, seed=7)

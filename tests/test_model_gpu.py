@@ -258,6 +258,24 @@ def test_hip_determinism_and_fused_ce():
         assert rel_err(g1, g2) < 2e-2, grp
 
 
+def test_compile_common_logits_free_loss():
+    """After compile_common, the logits-free loss runs the chunked HIP linear CE: without gradients the fused forward
+    (no logits buffer), with gradients the chunk loop; both match the full-logits loss under bf16 autocast."""
+    model = tiny_model(seed=6, theta_scale=0.25, attn_impl="hip_fused").to(DEV)
+    ids = token_ids(2, 100, seed=6).to(DEV)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        ref = model(ids, labels=ids).loss.item()
+        assert model.compile_common() is model
+        out = model(ids, labels=ids, return_logits=False)
+    assert out.logits is None and abs(out.loss.item() - ref) < 1e-2
+    model.zero_grad(set_to_none=True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        loss = model(ids, labels=ids, return_logits=False).loss
+    loss.backward()
+    assert abs(loss.item() - ref) < 1e-2
+    assert all(p.grad is not None and bool(torch.isfinite(p.grad).all()) for p in model.parameters())
+
+
 def test_gpu_decoding_matches_full_forward():
     """Prefill + decode steps on the HIP paths (decode kernel) against the full forward, fp32 model."""
     model = tiny_model(seed=5, attn_impl="hip").to(DEV).eval()
