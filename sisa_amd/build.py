@@ -22,11 +22,12 @@ ARCH = "gfx950"
 # -packed-fp32-ops: hipcc never emits v_pk_{add,mul,fma}_f32 for this library.
 HIPFLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", f"-I{os.path.join(ROOT, 'include')}",
             f"-I{CSRC}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
-# Per-source additions: the backward attention kernels (dependency chains of MFMA, exponentials and fp32 row sums)
-# and the fused CE forward (all operand fragments of a step read ahead of its MFMAs) run faster under LLVM's max-ILP
-# machine scheduler, the forward attention kernel under the default one (measured on MI355X).
+# Per-source additions: the backward attention kernels (dependency chains of MFMA, exponentials and fp32 row sums),
+# the fused CE forward and the weight-gradient GEMM (all operand fragments of a step read ahead of its MFMAs) run
+# faster under LLVM's max-ILP machine scheduler, the forward attention kernel under the default one (measured on
+# MI355X).
 _MAX_ILP = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
-EXTRA_FLAGS = {"attention_bwd.hip": _MAX_ILP, "lmce_fwd.hip": _MAX_ILP}
+EXTRA_FLAGS = {"attention_bwd.hip": _MAX_ILP, "lmce_fwd.hip": _MAX_ILP, "wgrad.hip": _MAX_ILP}
 
 
 def _hipcc() -> str:
