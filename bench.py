@@ -70,7 +70,7 @@ PEAK_HBM_GBS = 8000.0
 # line quotes the committed measurements: HBM bytes per dispatch (FETCH_SIZE / WRITE_SIZE, each scaled by what the
 # counter reads for a plain 1 GiB copy) and the counter-measured MFMA busy fraction of the attention kernels.
 PROFILES = os.path.join(ROOT, "profiles")
-ATTN_KERNELS = ("attn_fwd_kernelIDF16b", "attn_bwd_dq_kernelIDF16b", "attn_bwd_dkv_kernelIDF16b", "dlam_kernel")
+ATTN_KERNELS = ("attn_fwd_kernelIDF16b", "attn_bwd_dq_kernelIDF16b", "attn_bwd_dkv_kernelIDF16b")
 PREP_FWD_KERNELS = ("prep_sums_kernelIDF16b", "prep_fwd_kernelIDF16b")
 
 
@@ -712,7 +712,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": profiled_traffic(ATTN_KERNELS) if cfg == "ns" else None,
-                     "kernel": "attention fwd + bwd launches (attn_fwd, attn_bwd_dq, attn_bwd_dkv, dlam)",
+                     "kernel": "attention fwd + bwd launches (attn_fwd, attn_bwd_dq, attn_bwd_dkv)",
                      "algorithmic": f"1152 flop per causal pair x {fl['pairs']:.4g} pairs per step"},
         "roofline_prep": {"bound": "hbm", "achieved": round(prep_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": round(prep_gbs / PEAK_HBM_GBS, 4),

@@ -77,7 +77,8 @@ typedef struct {
 /* Workspace (bytes) of sisa_attn_bwd: six (B,H,L) fp32 row buffers. */
 int64_t sisa_attn_bwd_workspace_bytes(int32_t B, int32_t H, int32_t L);
 
-/* Backward: dq, dk, dv, dc, db, dg, dF and dlambda, exact-delta scheme by default (`exact`).
+/* Backward: dq, dk, dv, dc, db, dg, dF and dlambda, exact-delta scheme by default (`exact`). Two launches; the
+ * first writes fp64 dlambda sums of 16-row groups, the second adds each head's groups in a fixed order.
  * Replaces `_bwd_dq` (src/sisa/kernels/attention.py:300-491), `_bwd_dkv` (attention.py:495-663), the fp64 dlambda
  * reduction (attention.py:781-783) and the host core `attn_backward` (attention.py:730-784). */
 typedef struct {
@@ -108,11 +109,11 @@ int sisa_factors(const sisa_factors_args* a, void* stream);
 int sisa_attn_fwd(const sisa_attn_fwd_args* a, void* stream);
 int sisa_attn_bwd(const sisa_attn_bwd_args* a, void* stream);
 
-/* Largest B*H*L that sisa_attn_bwd_noalloc takes: its scratch holds the backward workspace for it (32 MiB). */
+/* Largest B*H*L that sisa_attn_bwd_noalloc takes: its scratch holds the backward workspace for it (28 MiB). */
 #define SISA_NOALLOC_MAX_BHL (1 << 20)
 
-/* sisa_attn_bwd without a caller workspace and without any allocation: `workspace` must be NULL, and the six row
- * buffers live in the library's static device scratch (one 32 MiB copy per GPU, held until the process ends).
+/* sisa_attn_bwd without a caller workspace and without any allocation: `workspace` must be NULL, and the five row
+ * buffers live in the library's static device scratch (one 28 MiB copy per GPU, held until the process ends).
  * No counterpart in the reference: for callers that cannot allocate (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). Limits: B*H*L <= SISA_NOALLOC_MAX_BHL (else SISA_ERR_INVALID); the stream
  * must belong to the current device. All calls on one GPU share its scratch: calls that overlap on one GPU (on

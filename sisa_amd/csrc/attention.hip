@@ -1,5 +1,5 @@
-// SISA attention for gfx950: decay factors, forward, exact-delta backward (query-owned and key-owned kernels, in
-// attention_bwd.hip) and the deterministic fp64 dlambda reduction, with the C entry points.
+// SISA attention for gfx950: decay factors, forward and exact-delta backward (query-owned and key-owned kernels, in
+// attention_bwd.hip, which also hold the deterministic fp64 dlambda reduction), with the C entry points.
 //
 //   s_ij = q_i.k_j / 8 + lam * exp(g_i - g_j) * (c_i.b_j) + (F_i - F_j)        (j <= i)
 //   o_i  = sum_j softmax_j(s_ij) v_j
@@ -89,11 +89,13 @@ struct __attribute__((aligned(16))) FwdLds {
 
 
 // One 64-key tile for a wave's 16 queries. cx0/cx1: for off-block tiles the folded c~ operand (hi, lo; FoldC types)
-// or the plain c~ (fp16, cx1 unused); for the diagonal tile the plain c~ (cx1 unused).
+// or the plain c~ (fp16, cx1 unused); for the diagonal tile the plain c~ (cx1 unused). nkb (diagonal tile only,
+// wave-uniform): the 16-key blocks at or before the wave's last query; later blocks are masked for all 16 queries
+// and are skipped (zero weights).
 template <class T, bool DIAG>
 SISA_DEV void fwd_tile(const FwdLds<T>& sm, int qblk, int lane, int n0, int q0, int L, const frag8<T> (&qf)[2],
                        const frag8<T>& cx0, const frag8<T>& cx1, const frag8<T>& onesf, float fq, float rs, float gq,
-                       float lam, float& m, float& l, f32x4 (&acc)[5]) {
+                       float lam, float& m, float& l, f32x4 (&acc)[5], int nkb = 4) {
     constexpr bool ANCH = Anchor<T>::on && !DIAG;
     const int grp = lane >> 4, lc = lane & 15;
     const int qq = q0 + lc;
@@ -101,6 +103,7 @@ SISA_DEV void fwd_tile(const FwdLds<T>& sm, int qblk, int lane, int n0, int q0, 
     f32x4 sc[4], cb[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
+        if (DIAG && kb >= nkb) continue;
         const frag8<T> k0 = frag_rows<T, DH>(sm.ks, kb * 16, 0, lane);
         const frag8<T> k1 = frag_rows<T, DH>(sm.ks, kb * 16, 1, lane);
         const frag8<T> bf = frag_rows<T, DS>(sm.bs, kb * 16, 0, lane);
@@ -112,6 +115,7 @@ SISA_DEV void fwd_tile(const FwdLds<T>& sm, int qblk, int lane, int n0, int q0, 
     float mloc = -__builtin_inff();
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
+        if (DIAG && kb >= nkb) continue;
         const int j0 = kb * 16 + 4 * grp;
         if constexpr (!ANCH) {   // the reference's difference F_i - F_j per element
             const f32x4 fk = lds4f(&sm.fk[j0]);
@@ -162,20 +166,26 @@ SISA_DEV void fwd_tile(const FwdLds<T>& sm, int qblk, int lane, int n0, int q0, 
     float ls = 0.f;
     const float off = ANCH ? ft - m : -m;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < 4; ++kb) {
+        if (DIAG && kb >= nkb) {
+            sc[kb] = zero4();
+            continue;
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float pe = fast_exp2(fmaf(sc[kb][i], LOG2E, off));
             sc[kb][i] = pe;
             ls += pe;
         }
+    }
     l += ls;
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
+        if (DIAG && 2 * st >= nkb) break;
         const frag8<T> pf = pack8<T>(sc[2 * st], sc[2 * st + 1]);
 #pragma unroll
         for (int db = 0; db < 4; ++db) acc[db] = mma(frag_tr<T, DH>(sm.vs, db * 16, st, lane), pf, acc[db]);
-        acc[4] = mma(onesf, pf, acc[4]);   // row 0 of block 4: the sum of the rounded weights (o'' normaliser)
+        acc[4] = mma(onesf, pf, acc[4]);   // block 4: every row holds the sum of the rounded weights
     }
 }
 
@@ -233,7 +243,7 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
         const int qq = q0 + lc;
         return qq < L ? load8<T>(C + (int64_t)qq * scl + 8 * grp) : zero8<T>();
     };
-    const frag8<T> onesf = ones_row_frag<T>(lane);
+    const frag8<T> onesf = ones_frag<T>();
 
     float m = M_FLOOR, l = 0.f;
     f32x4 acc[5];
@@ -324,7 +334,8 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
     if (live) {
         const FwdLds<T>& sm = smb[nfull & (NBUF - 1)];
         if (qblk == 0)
-            fwd_tile<T, true>(sm, 0, lane, tile0, q0, L, qf, diag_c(), cx1, onesf, fq, rs, gq, lam, m, l, acc);
+            fwd_tile<T, true>(sm, 0, lane, tile0, q0, L, qf, diag_c(), cx1, onesf, fq, rs, gq, lam, m, l, acc,
+                              (w & 3) + 1);
         else
             fwd_tile<T, false>(sm, 1, lane, tile0, q0, L, qf, cx0, cx1, onesf, fq, rs, gq, lam, m, l, acc);
     }
@@ -333,13 +344,16 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
         advance(nfull + 1);
         if (live && qblk == 1) {
             const FwdLds<T>& sm = smb[(nfull + 1) & (NBUF - 1)];
-            fwd_tile<T, true>(sm, 1, lane, tile0 + 64, q0, L, qf, diag_c(), cx1, onesf, fq, rs, gq, lam, m, l, acc);
+            fwd_tile<T, true>(sm, 1, lane, tile0 + 64, q0, L, qf, diag_c(), cx1, onesf, fq, rs, gq, lam, m, l, acc,
+                              (w & 3) + 1);
         }
     }
     if (!live) return;
     T* O = (T*)a.o.ptr + (int64_t)b * a.o.sb + (int64_t)h * a.o.sh;
+    // o and lse are normalised by the fp32 sum of the weights (the backward recomputes weights that sum to 1 in fp32
+    // with this lse); o'' by the sum of the rounded weights, which every element of block 4 holds.
     const float lt = group_sum(l);
-    const float lbt = group_bcast0(acc[4][0], lane);   // row 0 of block 4: sum of the rounded weights
+    const float lbt = acc[4][0];
     const int qq = q0 + lc;
     if (qq >= L) return;
     const float ls = (lt == 0.f) ? 1.f : lt;
@@ -355,27 +369,6 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
     if (grp == 0) a.lse[(int64_t)bh * L + qq] = m + __builtin_amdgcn_logf(ls);
 }
 
-// dlambda_h = sum over (b, t) of the per-row parts, in fp64 with a fixed reduction order (attention.py:781-783): the
-// dkv kernel sums each 64-row block; this kernel sums the B * ceil(L/64) block sums of head h.
-__global__ __launch_bounds__(256) void dlam_kernel(const double* __restrict__ blk, float* __restrict__ dlam, int B,
-                                                   int H, int nkt) {
-    __shared__ double red[256];
-    const int h = blockIdx.x;
-    const int64_t n = (int64_t)B * nkt;
-    double s = 0.0;
-    for (int64_t t = threadIdx.x; t < n; t += 256) {
-        const int64_t bb = t / nkt, kt = t % nkt;
-        s += blk[(bb * H + h) * nkt + kt];
-    }
-    red[threadIdx.x] = s;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) dlam[h] = (float)red[0];
-}
-
 template <class T>
 int launch_fwd(const sisa_attn_fwd_args* a, hipStream_t st) {
     const dim3 grid((unsigned)(sisa::cdiv(a->L, 128) * a->B * a->H));
@@ -383,14 +376,6 @@ int launch_fwd(const sisa_attn_fwd_args* a, hipStream_t st) {
     return sisa::launch_status("sisa_attn_fwd");
 }
 
-template <class T>
-int launch_bwd(const sisa_attn_bwd_args* a, hipStream_t st) {
-    const int rc = sisa::detail::attn_bwd_dq_dkv(a, st);   // the dq and dkv kernels (attention_bwd.hip)
-    if (rc) return rc;
-    const int64_t BHL = (int64_t)a->B * a->H * a->L;
-    dlam_kernel<<<a->H, 256, 0, st>>>(ws_block_dlam(a->workspace, BHL), a->dlam, a->B, a->H, (a->L + 63) / 64);
-    return sisa::launch_status("sisa_attn_bwd (dlam)");
-}
 
 bool g_view_ok(const sisa_view& v) {
     return v.ptr != nullptr;
@@ -438,10 +423,10 @@ extern "C" int sisa_attn_fwd(const sisa_attn_fwd_args* a, void* stream) {
     }
 }
 
-// Six (B,H,L) fp32 row buffers, then (B*H, ceil(L/64)) fp64 block sums of dlambda (8-byte aligned).
+// Five (B,H,L) fp32 row buffers, then (B*H, ceil(L/16)) fp64 group sums of dlambda (8-byte aligned).
 static int64_t bwd_workspace_bytes(int64_t B, int64_t H, int64_t L) {
     const int64_t BHL = B * H * L;
-    return (WS_N * BHL + (BHL & 1)) * (int64_t)sizeof(float) + B * H * ((L + 63) / 64) * (int64_t)sizeof(double);
+    return (WS_N * BHL + (BHL & 1)) * (int64_t)sizeof(float) + B * H * ((L + 15) / 16) * (int64_t)sizeof(double);
 }
 
 extern "C" int64_t sisa_attn_bwd_workspace_bytes(int32_t B, int32_t H, int32_t L) {
@@ -475,13 +460,8 @@ static int check_bwd(const sisa_attn_bwd_args* a) {
     return SISA_OK;
 }
 
-static int launch_bwd_any(const sisa_attn_bwd_args* a, hipStream_t st) {
-    switch (a->dtype) {
-        case SISA_BF16: return launch_bwd<__bf16>(a, st);
-        case SISA_F16: return launch_bwd<_Float16>(a, st);
-        default: return launch_bwd<float>(a, st);
-    }
-}
+// the dq and dkv kernels (attention_bwd.hip); dlambda is summed inside them
+static int launch_bwd_any(const sisa_attn_bwd_args* a, hipStream_t st) { return sisa::detail::attn_bwd_dq_dkv(a, st); }
 
 extern "C" int sisa_attn_bwd(const sisa_attn_bwd_args* a, void* stream) {
     SISA_REQUIRE(a != nullptr, "sisa_attn_bwd: null args");
@@ -490,12 +470,12 @@ extern "C" int sisa_attn_bwd(const sisa_attn_bwd_args* a, void* stream) {
 }
 
 // ------------------------------------------------------------------------------------------------ no-alloc backward
-// The backward's workspace (six (B,H,L) fp32 row buffers and the fp64 dlambda block sums; for B*H*L <= 2^20 at most
-// 2^20 blocks) in a file-scope device array, for callers that cannot allocate. Every GPU the library runs on holds its
-// own copy (32 MiB) until the process ends. In host code `scratch` names a host-side
+// The backward's workspace (five (B,H,L) fp32 row buffers and the fp64 dlambda group sums, at most 2^20 of them for
+// B*H*L <= 2^20) in a file-scope device array, for callers that cannot allocate. Every GPU the library runs on holds its
+// own copy (28 MiB) until the process ends. In host code `scratch` names a host-side
 // stand-in, not device memory: its device address is looked up once per device (hipGetSymbolAddress, with that
 // device current) and only that address is ever handed to kernels.
-static __device__ __align__(256) float scratch[(WS_N + 2) * (int64_t)SISA_NOALLOC_MAX_BHL];   // 32 MiB
+static __device__ __align__(256) float scratch[(WS_N + 2) * (int64_t)SISA_NOALLOC_MAX_BHL];   // 28 MiB
 
 namespace {
 constexpr int MAX_DEVICES = 64;

@@ -28,10 +28,12 @@ struct RowSums {
 // key tile's last F (F_e - F_j enters the q.k MFMA as its accumulator input, (F_i - F_e) log2e - lse is one offset
 // per query and tile) and dP - Delta comes out of the dO.V MFMA (-Delta as its accumulator input). The dkv kernel
 // evaluates the same pairs with the same anchors and the same accumulator inputs.
+// nkb (own-block tile only, wave-uniform): the 16-key blocks at or before the wave's last query; later blocks are
+// masked for all 16 queries and are skipped.
 template <class T, bool DIAG>
 SISA_DEV void dq_tile(const DqLds<T>& sm, int lane, int n0, int q0, int L, const frag8<T> (&qf)[2],
                       const frag8<T>& cfr, const frag8<T> (&dof)[2], float fq, float rs, float gq, float lse,
-                      float dhat, float lam, bool exact, RowSums& R, f32x4 (&dqa)[4], f32x4 (&dca)[2]) {
+                      float dhat, float lam, bool exact, RowSums& R, f32x4 (&dqa)[4], f32x4 (&dca)[2], int nkb = 4) {
     constexpr bool F16 = Anchor<T>::on;
     constexpr bool ANCH = F16 && !DIAG;
     const int grp = lane >> 4, lc = lane & 15;
@@ -41,11 +43,16 @@ SISA_DEV void dq_tile(const DqLds<T>& sm, int lane, int n0, int q0, int L, const
     const f32x4 ndh = F16 ? f32x4{-dhat, -dhat, -dhat, -dhat} : zero4();
 #pragma unroll
     for (int st = 0; st < 2; ++st) {           // 32 keys (one K-step of the dq/dc products) at a time
+        if (DIAG && 2 * st >= nkb) break;
         f32x4 dsv[2], wv[2];                   // dq and dc operands of the two 16-key blocks (before rounding)
 #pragma unroll
         for (int hb = 0; hb < 2; ++hb) {       // one 16-key block at a time keeps the live set small
             __builtin_amdgcn_sched_barrier(0);
             const int kb = 2 * st + hb;
+            if (DIAG && kb >= nkb) {
+                dsv[hb] = wv[hb] = zero4();
+                continue;
+            }
             const int j0 = kb * 16 + 4 * grp;
             const f32x4 sc = mma(frag_rows<T, DH>(sm.ks, kb * 16, 1, lane), qf[1],
                                  mma(frag_rows<T, DH>(sm.ks, kb * 16, 0, lane), qf[0],
@@ -268,13 +275,12 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
         R.ya *= rowfq;
         dca[0] *= rs;
         dca[1] *= rs;
-        dq_tile<T, true>(sm, lane, tile0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, exact, R, dqa, dca);
+        dq_tile<T, true>(sm, lane, tile0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, exact, R, dqa, dca, w + 1);
     }
     if (!live) return;
     const float xat = group_sum(R.xa), yat = group_sum(R.ya), Wa = group_sum(R.wa), Za = group_sum(R.za);
     const float Ptt = group_sum(R.ptt), Dptt = group_sum(R.dptt), Xd = group_sum(R.xd);
     const int qq = q0 + lc;
-    if (qq >= L) return;
     // Self-normalised exact delta T^ = Delta + ddel and the delta-free diagonal (attention.py:453-463). ddel is kept
     // as its own quantity: forming T^ = Delta + ddel and taking T^ - Delta again would quantise ddel to the fp32 ulp
     // of Delta, an absolute error that dominates every dS of rows whose mass sits on one key. The
@@ -285,6 +291,15 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
     const float ddel = exact ? (Ptt * x0 + Wa) / ssum : 0.f;
     const float dstt = exact ? Ptt * (Za * x0 - Wa) / ssum : 0.f;
     const float dl_row = xat - ddel * yat;
+    const float rl = exact ? dl_row + dstt * Xd : dl_row + Xd;   // the row's dlambda part (FA: Xd = dS_tt cb_tt)
+    {
+        // the wave's 16 rows summed in fp64 in a fixed butterfly order (lanes of group 0; rows past L add zero)
+        double v = (grp == 0 && qq < L) ? (double)rl : 0.0;
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o);
+        if (lane == 0) ws_block_dlam(a.workspace, BHL)[(int64_t)bh * ((L + 15) / 16) + (q0 >> 4)] = v;
+    }
+    if (qq >= L) return;
     const float dsq = (float)cvt<T>(dstt);           // one DT rounding of the diagonal operands
     const float dsc = (float)cvt<T>(dstt * lam);
     const T* krow = K + (int64_t)qq * skl;
@@ -320,7 +335,6 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
         WS[WS_DDEL * BHL + o] = ddel;
         WS[WS_DSD * BHL + o] = dstt;
         WS[WS_RG * BHL + o] = lam * dl_row;
-        WS[WS_RL * BHL + o] = exact ? dl_row + dstt * Xd : dl_row + Xd;   // FA: Xd = dS_tt cb_tt
         WS[WS_RF * BHL + o] = Wa - Za * ddel;
     }
 }
@@ -342,24 +356,32 @@ struct __attribute__((aligned(16))) DkvLds {
 // kf holds k/8 (the same exact products as the dq kernel's q/8); for 16-bit inputs off-block tiles use the dq kernel's
 // anchor (nfe = F_e - F_j of the workgroup's key block as the q.k accumulator input, ftl per query) and -Delta as the
 // dO.V accumulator input, so both kernels evaluate every pair with the same operations.
+// q0b (own-block tile only, wave-uniform): the first 16-query block at or after the wave's first key; earlier blocks
+// are masked for all 16 keys and are skipped (16-bit types; the fp32 kernel, at its register limit, computes them).
 template <class T, bool PAIR>
 SISA_DEV void dkv_tile(const DkvLds<T>& sm, int lane, int m0, int k0, int L, const frag8<T> (&kf)[2],
                        const frag8<T> (&vf)[2], const frag8<T>& bfr, float fk, float nfe, float rk, float gk, float dsd,
                        float lam, bool exact, float& dgu, float& dfs, f32x4 (&dva)[4], f32x4 (&dka)[4],
-                       f32x4 (&dba)[2]) {
+                       f32x4 (&dba)[2], int q0b = 0) {
     constexpr bool F16 = Anchor<T>::on;
     constexpr bool ANCH = F16 && !PAIR;
+    constexpr bool SKIP = PAIR && sizeof(T) == 2;
     const int grp = lane >> 4, lc = lane & 15;
     const int kk = k0 + lc;
     const float* rqm = sm.rq;
     const f32x4 nfe4 = ANCH ? f32x4{nfe, nfe, nfe, nfe} : zero4();
 #pragma unroll
     for (int st = 0; st < 2; ++st) {           // 32 queries (one K-step of the dk/dv/db products) at a time
+        if (SKIP && 2 * st + 1 < q0b) continue;
         f32x4 pv[2], kv[2], bv[2];             // dv, dk and db operands of the two 16-query blocks (before rounding)
 #pragma unroll
         for (int hb = 0; hb < 2; ++hb) {       // one 16-query block at a time keeps the live set small
             __builtin_amdgcn_sched_barrier(0);
             const int qb = 2 * st + hb;
+            if (SKIP && qb < q0b) {
+                pv[hb] = kv[hb] = bv[hb] = zero4();
+                continue;
+            }
             const int i0 = qb * 16 + 4 * grp;
             const f32x4 sc = mma(frag_rows<T, DH>(sm.qs, qb * 16, 1, lane), kf[1],
                                  mma(frag_rows<T, DH>(sm.qs, qb * 16, 0, lane), kf[0], nfe4));
@@ -574,15 +596,21 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
         dba[0] *= rk;
         dba[1] *= rk;
         dkv_tile<T, true>(sm, lane, ktile0, k0, L, kf, vf, bfr, fk, nfe, rk, gk, dsd, lam, exact, dgu, dfs, dva, dka,
-                                 dba);
+                          dba, w);
     }
-    if (w == 0) {
-        // the block's 64 per-row dlambda parts (written by the dq kernel) summed in fp64 in a fixed butterfly order
-        const int r = ktile0 + lane;
-        double v = r < L ? (double)WS[WS_RL * BHL + (int64_t)bh * L + r] : 0.0;
+    if (w == 0 && b == 0 && ktile == 0) {
+        // dlambda_h: the B * ceil(L/16) group sums of head h (written by the dq kernel) added in a fixed order,
+        // lane-strided then a butterfly, by the workgroup of (batch 0, key block 0) (attention.py:781-783)
+        const int ng = (L + 15) / 16, n = a.B * ng;
+        const double* blk = ws_block_dlam(a.workspace, BHL);
+        double sum = 0.0;
+        for (int t = lane; t < n; t += 64) {
+            const int bb = t / ng, s = t - bb * ng;
+            sum += blk[((int64_t)bb * H + h) * ng + s];
+        }
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-        if (lane == 0) ws_block_dlam(a.workspace, BHL)[(int64_t)bh * ((L + 63) / 64) + ktile] = v;
+        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+        if (lane == 0) a.dlam[h] = (float)sum;
     }
     if (!live) return;
     const float Dgu = group_sum(dgu), Dfs = group_sum(dfs);

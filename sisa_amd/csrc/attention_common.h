@@ -68,8 +68,9 @@ template <class T> SISA_DEV void split_frag(const frag8<T>& f, float s, frag8<T>
 }
 
 // Row buffers handed from the dq kernel to the dkv kernel (workspace, each (B,H,L) fp32), followed by the fp64 sums
-// of the per-row dlambda parts over each 64-row block, (B*H, ceil(L/64)), written by the dkv kernel.
-enum { WS_DELTA = 0, WS_DDEL, WS_DSD, WS_RG, WS_RL, WS_RF, WS_N };
+// of the per-row dlambda parts over each 16-row group of queries, (B*H, ceil(L/16)), written by the dq kernel's waves
+// and added up per head by one dkv workgroup.
+enum { WS_DELTA = 0, WS_DDEL, WS_DSD, WS_RG, WS_RF, WS_N };
 __host__ __device__ inline double* ws_block_dlam(void* ws, int64_t BHL) {
     return reinterpret_cast<double*>(static_cast<float*>(ws) + WS_N * BHL + (BHL & 1));   // 8-byte aligned
 }

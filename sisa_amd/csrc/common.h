@@ -92,12 +92,6 @@ SISA_DEV float group_sum(float x) {
     r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
-// Value of lane (l % 16) (lane group 0) broadcast to the four lanes of its group.
-SISA_DEV float group_bcast0(float x, int lane) {
-    const unsigned u = __float_as_uint(x);
-    const unsigned v = (unsigned)__builtin_amdgcn_ds_bpermute((lane & 15) << 2, (int)u);
-    return __uint_as_float(v);
-}
 
 // 16-byte / 8-byte loads of 8 or 4 consecutive elements.
 template <class T> SISA_DEV frag8<T> load8(const T* p) { return *reinterpret_cast<const frag8<T>*>(p); }
@@ -261,13 +255,12 @@ SISA_DEV frag8<float> frag_tr<float, 32>(const float* X, int f0, int step, int l
     return r;
 }
 
-// The A fragment of a 16-row block whose row 0 is all ones and rows 1..15 are zero: MFMA with it sums the B
-// operand over K into row 0 of the output block.
+// The A fragment of a 16-row block of ones: MFMA with it sums the B operand over K into every row of the output
+// block, so each lane holds the column sums of its columns.
 template <class T>
-SISA_DEV frag8<T> ones_row_frag(int lane) {
+SISA_DEV frag8<T> ones_frag() {
     frag8<T> r;
-    const float v = (lane & 15) == 0 ? 1.f : 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] = (T)v;
+    for (int j = 0; j < 8; ++j) r[j] = (T)1.f;
     return r;
 }

@@ -124,7 +124,8 @@ def test_decoder_block_entry_points_reject_bad_arguments(lib):
 
 def test_workspace_sizes(lib):
     B, H, L = 2, 3, 1000
-    assert lib.sisa_attn_bwd_workspace_bytes(B, H, L) >= 6 * 4 * B * H * L
+    # five fp32 (B,H,L) row buffers and the fp64 dlambda sums of 16-row groups (B*H*L even: no alignment pad)
+    assert lib.sisa_attn_bwd_workspace_bytes(B, H, L) == 5 * 4 * B * H * L + 8 * B * H * -(-L // 16)
     assert lib.sisa_prep_bwd_workspace_bytes(B, L, H) > 0
     assert lib.sisa_rmsnorm_bwd_workspace_bytes(16384, 768) >= (16384 // 8 + 64) * 768 * 4
     assert lib.sisa_norm_bwd_workspace_bytes(16384, 768, 12) >= (16384 // 8 + 64 + 64 * 16) * 768 * 4
