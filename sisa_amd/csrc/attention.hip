@@ -13,10 +13,11 @@
 // Work decomposition (16 rows per wave: one column group of the 16x16 MFMA blocks; no atomics):
 //   forward: a workgroup of 8 waves owns 128 consecutive queries; key tiles of 64 positions are staged row-major in
 //     LDS while the next tile's global loads are in flight; at most 128 VGPRs, so 4 waves per SIMD.
-//   dq kernel: a workgroup of 4 waves owns one 64-query decay block; every key tile before the block is an
-//     off-block tile for all four waves and the block's own tile comes last, in its own code region.
+//   dq kernel: a workgroup of 8 waves owns 128 queries, two 64-query decay blocks; every key tile before them is an
+//     off-block tile for all waves, then block 0's own tile (off-block for block 1's waves) and block 1's; at most
+//     128 VGPRs (16-bit types), so 4 waves per SIMD.
 //   dkv kernel: a workgroup of 4 waves owns one 64-key block; query tiles are visited from the last one down to the
-//     block's own tile. Both backward kernels run 3 waves per SIMD.
+//     block's own tile; 3 waves per SIMD.
 //   Operands of the sequence-contracted products (P V, dS K, ...) are read from the row-major tiles with the gfx950
 //   LDS transpose read, so no transposed copy is ever stored.
 //   Ownership is exclusive: dq/dc by query blocks, dk/dv/db/dg/dF by key blocks.

@@ -14,7 +14,7 @@ struct __attribute__((aligned(16))) DqLds {
     T bs[64 * DS];               // B~ (scores; transposed reads for dc)
     float fk[64], gk[64];
     float nfe[64];               // F_e - F_j (F_e = F at the tile's last key; anchored off-block scores)
-    float cfm[64];               // colf * mid for the workgroup's query block
+    float cfm[2][64];            // colf * mid for the workgroup's two query blocks
 };
 
 // Per-query row sums of the dq kernel (diagonal excluded): xa = sum dS^ u, ya = sum P u, wa = D = sum dS^,
@@ -31,14 +31,14 @@ struct RowSums {
 // nkb (own-block tile only, wave-uniform): the 16-key blocks at or before the wave's last query; later blocks are
 // masked for all 16 queries and are skipped.
 template <class T, bool DIAG>
-SISA_DEV void dq_tile(const DqLds<T>& sm, int lane, int n0, int q0, int L, const frag8<T> (&qf)[2],
+SISA_DEV void dq_tile(const DqLds<T>& sm, int qblk, int lane, int n0, int q0, int L, const frag8<T> (&qf)[2],
                       const frag8<T>& cfr, const frag8<T> (&dof)[2], float fq, float rs, float gq, float lse,
                       float dhat, float lam, bool exact, RowSums& R, f32x4 (&dqa)[4], f32x4 (&dca)[2], int nkb = 4) {
     constexpr bool F16 = Anchor<T>::on;
     constexpr bool ANCH = F16 && !DIAG;
     const int grp = lane >> 4, lc = lane & 15;
     const int qq = q0 + lc;
-    const float* cfm = sm.cfm;
+    const float* cfm = sm.cfm[qblk];
     const float ftl = ANCH ? fmaf(fq - sm.fk[63], LOG2E, -lse) : -lse;
     const f32x4 ndh = F16 ? f32x4{-dhat, -dhat, -dhat, -dhat} : zero4();
 #pragma unroll
@@ -121,15 +121,16 @@ SISA_DEV void dq_tile(const DqLds<T>& sm, int lane, int n0, int q0, int L, const
 }
 
 template <class T>
-__global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void attn_bwd_dq_kernel(sisa_attn_bwd_args a) {
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 ? 4 : 2)))
+void attn_bwd_dq_kernel(sisa_attn_bwd_args a) {
     constexpr int NBUF = sizeof(T) == 2 ? 2 : 1;
     __shared__ DqLds<T> smb[NBUF];
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int NQT = (a.L + 63) / 64;
+    const int NQT = (a.L + 127) / 128;
     int bh, rank;
     xcd_map(blockIdx.x, NQT, a.B * a.H, bh, rank);
-    const int tile = NQT - 1 - rank;               // heavy (late) query blocks first
+    const int tile = NQT - 1 - rank;               // heavy (late) query tiles first
     const int H = a.H, L = a.L;
     const int b = bh / H, h = bh % H;
     const bool has_f = a.f.ptr != nullptr;
@@ -153,10 +154,13 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
     const int64_t BHL = (int64_t)a.B * H * L;
     float* WS = (float*)a.workspace;
 
-    const int tile0 = tile * 64;                   // the workgroup's 64-row decay block
+    const int tile0 = tile * 128;                  // the workgroup's two 64-row decay blocks
     const int q0 = tile0 + 16 * w;
+    const int qblk = w >> 2;                       // the wave's block
     const bool live = q0 < L;
-    const float ga = G[(int64_t)tile0 * sgl];      // anchor: g at the start of the block
+    const int ta0 = tile0 < L ? tile0 : L - 1, ta1 = tile0 + 64 < L ? tile0 + 64 : L - 1;
+    const float ga0 = G[(int64_t)ta0 * sgl];       // anchors: g at the start of each block
+    const float ga1 = G[(int64_t)ta1 * sgl];
 
     frag8<T> qf[2], cfr, dof[2];
     float fq, rowfq, rs, gq, lse, dhat;
@@ -206,14 +210,15 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
     // Key tiles straight into LDS (DMA buffer loads); 16-bit types double-buffer them (one barrier per tile), fp32
     // uses one buffer. The per-key scalars (F_j, g_j, colf_j, g at the tile's last key) are fetched into registers by
     // the first wave one tile ahead.
-    DmaStage<T, DH, NWB> dk, dv;
-    DmaStage<T, DS, NWB> dbt;
+    DmaStage<T, DH, NW> dk, dv;
+    DmaStage<T, DS, NW> dbt;
     const int64_t xk = ((int64_t)(L - 1) * skl + DH) * (int64_t)sizeof(T);   // view extents (bytes)
     const int64_t xv = ((int64_t)(L - 1) * svl + DH) * (int64_t)sizeof(T);
     const int64_t xb = ((int64_t)(L - 1) * sbl + DS) * (int64_t)sizeof(T);
     dk.init(skl, w, lane);
     dv.init(svl, w, lane);
     dbt.init(sbl, w, lane);
+    const int kend = (tile0 + 128 < L) ? tile0 + 128 : L;
     float pf_f = 0.f, pf_g = 0.f, pf_cf = 0.f, pf_ge = 0.f, pf_fe = 0.f;
     auto fetch_scalars = [&](int n0) {
         if (tid < 64) {
@@ -235,47 +240,70 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void 
             d.fk[tid] = pf_f;
             d.nfe[tid] = pf_fe - pf_f;
             d.gk[tid] = pf_g;
-            d.cfm[tid] = pf_cf * exp2_le0((ga - pf_ge) * LOG2E);
+            d.cfm[0][tid] = pf_cf * exp2_le0((ga0 - pf_ge) * LOG2E);
+            d.cfm[1][tid] = pf_cf * exp2_le0((ga1 - pf_ge) * LOG2E);
         }
     };
-    // tile t (keys 64 t ..) is in buffer t & (NBUF-1) after advance(t) (and, for two buffers, the barrier before it)
-    auto advance = [&](int t) {
+    // tile t (keys 64 t ..) is in buffer t & (NBUF-1) after advance_into(t, ...) (and, for two buffers, the barrier
+    // before it)
+    auto advance_into = [&](int t, DqLds<T>& nxt) {   // nxt: the buffer that is idle during tile t
         const int n0 = 64 * t;
         if (NBUF == 2) {
-            if (n0 + 64 <= tile0) {
-                issue_tile(smb[(t + 1) & (NBUF - 1)], n0 + 64);
-                if (n0 + 128 <= tile0) fetch_scalars(n0 + 128);
+            if (n0 + 64 < kend) {
+                issue_tile(nxt, n0 + 64);
+                if (n0 + 128 < kend) fetch_scalars(n0 + 128);
             }
         } else if (t > 0) {
             __syncthreads();
             issue_tile(smb[0], n0);
             __syncthreads();
-            if (n0 + 64 <= tile0) fetch_scalars(n0 + 64);
+            if (n0 + 64 < kend) fetch_scalars(n0 + 64);
         }
     };
     fetch_scalars(0);
     issue_tile(smb[0], 0);
-    if (64 <= tile0) fetch_scalars(64);
+    if (64 < kend) fetch_scalars(64);
     __syncthreads();
-    // key tiles before the block (all off-block), then the block's own tile
+    // key tiles before the workgroup's first block (off-block for every wave), then the blocks' own tiles
     const int nt = tile0 / 64;
-    for (int t = 0; t < nt; ++t) {
-        advance(t);
-        if (live) {
-            const DqLds<T>& sm = smb[t & (NBUF - 1)];
-            dq_tile<T, false>(sm, lane, 64 * t, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, exact, R, dqa, dca);
-        }
+    auto off_tile = [&](int t, const DqLds<T>& sm, DqLds<T>& nxt) {
+        advance_into(t, nxt);
+        if (live)
+            dq_tile<T, false>(sm, qblk, lane, 64 * t, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, exact, R, dqa,
+                              dca);
         if (NBUF == 2) __syncthreads();
+    };
+    if constexpr (NBUF == 2) {
+        // two tiles per iteration, so that each names its LDS buffers statically (no per-tile address arithmetic)
+        int t = 0;
+        for (; t + 2 <= nt; t += 2) {
+            off_tile(t, smb[0], smb[NBUF - 1]);
+            off_tile(t + 1, smb[NBUF - 1], smb[0]);
+        }
+        if (t < nt) off_tile(t, smb[0], smb[NBUF - 1]);
+    } else {
+        for (int t = 0; t < nt; ++t) off_tile(t, smb[0], smb[0]);
     }
-    advance(nt);
-    if (live) {
-        // the block's own tile: apply the off-block row factors once, in fp32, then the diagonal path
-        const DqLds<T>& sm = smb[nt & (NBUF - 1)];
+    // block 0's own tile (its waves' last tile; an off-block tile for block 1's waves), then block 1's own tile. The
+    // off-block row factors (lam * rowf for dc) are applied once, in fp32, before a wave's own tile.
+    auto own_tile = [&](const DqLds<T>& sm, int n0) {
         R.xa *= rowfq;
         R.ya *= rowfq;
         dca[0] *= rs;
         dca[1] *= rs;
-        dq_tile<T, true>(sm, lane, tile0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, exact, R, dqa, dca, w + 1);
+        dq_tile<T, true>(sm, qblk, lane, n0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, exact, R, dqa, dca,
+                         (w & 3) + 1);
+    };
+    advance_into(nt, smb[(nt + 1) & (NBUF - 1)]);
+    if (live) {
+        const DqLds<T>& sm = smb[nt & (NBUF - 1)];
+        if (qblk == 0) own_tile(sm, tile0);
+        else dq_tile<T, false>(sm, 1, lane, tile0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, exact, R, dqa, dca);
+    }
+    if (tile0 + 64 < kend) {
+        if (NBUF == 2) __syncthreads();
+        advance_into(nt + 1, smb[nt & (NBUF - 1)]);
+        if (live && qblk == 1) own_tile(smb[(nt + 1) & (NBUF - 1)], tile0 + 64);
     }
     if (!live) return;
     const float xat = group_sum(R.xa), yat = group_sum(R.ya), Wa = group_sum(R.wa), Za = group_sum(R.za);
@@ -649,11 +677,12 @@ namespace detail {
 
 template <class T>
 static int launch_dq_dkv(const sisa_attn_bwd_args* a, hipStream_t st) {
-    const dim3 grid((unsigned)(sisa::cdiv(a->L, 64) * a->B * a->H));
-    attn_bwd_dq_kernel<T><<<grid, NTHB, 0, st>>>(*a);
+    const dim3 qgrid((unsigned)(sisa::cdiv(a->L, 128) * a->B * a->H));
+    attn_bwd_dq_kernel<T><<<qgrid, NTH, 0, st>>>(*a);
     const int rc = sisa::launch_status("sisa_attn_bwd (dq)");
     if (rc) return rc;
-    attn_bwd_dkv_kernel<T><<<grid, NTHB, 0, st>>>(*a);
+    const dim3 kgrid((unsigned)(sisa::cdiv(a->L, 64) * a->B * a->H));
+    attn_bwd_dkv_kernel<T><<<kgrid, NTHB, 0, st>>>(*a);
     return sisa::launch_status("sisa_attn_bwd (dkv)");
 }
 

@@ -17,9 +17,9 @@ constexpr float M_FLOOR = -1e30f;     // forward: initial running maximum (finit
 // 64-position tiles of the other operand staged row-major in LDS.
 constexpr int NW = 8;
 constexpr int NTH = 64 * NW;
-// Backward kernels: 4 waves x 16 rows = one 64-row decay block per workgroup, so that every tile before the block is
-// an off-block tile for all waves and the block's own tile comes last (two code regions with small register sets;
-// three workgroups per CU).
+// dkv kernel: 4 waves x 16 rows = one 64-row decay block per workgroup, so that every tile before the block is an
+// off-block tile for all waves and the block's own tile comes last (two code regions with small register sets; three
+// workgroups per CU). The dq kernel uses the forward's 8-wave workgroups (two decay blocks).
 constexpr int NWB = 4;
 constexpr int NTHB = 64 * NWB;
 
