@@ -34,7 +34,10 @@ Reported (one JSON line on rank 0):
              the bf16 MFMA peak.
   cpu_baseline   the reference's pure-PyTorch path (oracle restatement of src/sisa/functional.py:106-155 plus the
              modeling.py glue) on the host cores, on a bounded sample of the same workload (one batch row, all 8
-             heads, T=4096, fp32 forward + backward).
+             heads, T=4096, fp32 forward + backward); config0: BASELINE.json config 0 itself (B=1, T=256, H=4, fp32
+             fwd+bwd) on the same cores.
+  config0_gpu  config 0 on the GPU through the product path (torch glue + the fp32 HIP attention kernels): a latency
+             figure beside cpu_baseline.config0.
 """
 from __future__ import annotations
 
@@ -568,7 +571,83 @@ def cpu_baseline(reps: int) -> dict:
     flop = 1152 * B * H * L * L / 2
     return {"value": round(flop / t / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"1 batch row (8 heads) of the T=4096 workload in fp32 (1/4 of one step), glue + attention "
-                      f"fwd+bwd, median of {reps} runs after 1 warm-up: {t * 1e3:.0f} ms = {B * L / t:.0f} tokens/s"}
+                      f"fwd+bwd, median of {reps} runs after 1 warm-up: {t * 1e3:.0f} ms = {B * L / t:.0f} tokens/s",
+            "config0": cpu_config0(reps)}
+
+
+def gpu_config0(reps: int = 20) -> dict:
+    """BASELINE.json config 0 (B=1, T=256, H=4, fp32, fwd+bwd with the glue) on the GPU through the product path:
+    the glue in torch (sisa_amd.functional.rotate_pairs, cumsums) and sisa_attention(impl="hip") in fp32. Median of
+    ``reps`` HIP-event timed steps; each step is a handful of small launches, so this is a latency figure."""
+    import torch
+    import torch.nn.functional as F
+
+    from sisa_amd.functional import rotate_pairs, sisa_attention
+    dev = torch.device("cuda:0")
+    B, H, L = 1, 4, 256
+    gen = torch.Generator().manual_seed(0)
+    leaves = dict(q=torch.randn(B, H, L, 64, generator=gen), k=torch.randn(B, H, L, 64, generator=gen),
+                  v=torch.randn(B, H, L, 64, generator=gen), b=torch.randn(B, H, L, 32, generator=gen),
+                  c=torch.randn(B, H, L, 32, generator=gen), theta=0.01 * torch.randn(B, L, H, 16, generator=gen),
+                  a=-5 + 0.5 * torch.randn(B, L, H, generator=gen), z=4 + 0.5 * torch.randn(B, L, H, generator=gen),
+                  lam_raw=torch.full((H,), -1.0))
+    leaves = {n: t.to(dev).requires_grad_(True) for n, t in leaves.items()}
+    dy = torch.randn(B, H, L, 64, generator=gen).to(dev)
+
+    def step():
+        phi = torch.cumsum(leaves["theta"], 1).transpose(1, 2)
+        g = torch.cumsum(-F.softplus(leaves["a"]), 1).transpose(1, 2).contiguous()
+        fg = torch.cumsum(F.logsigmoid(leaves["z"]), 1).transpose(1, 2).contiguous()
+        o = sisa_attention(leaves["q"], leaves["k"], leaves["v"], rotate_pairs(leaves["c"], phi),
+                           rotate_pairs(leaves["b"], phi), g, F.softplus(leaves["lam_raw"]), fg, impl="hip")
+        torch.autograd.grad(o, list(leaves.values()), dy)
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        step()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    t = statistics.median(times) * 1e-3
+    return {"ms": round(t * 1e3, 3), "tokens_per_s": round(B * L / t, 1),
+            "shape": "B=1, T=256, H=4, d_h=64, d_s=32, fp32, fwd+bwd (glue in torch, attention on the HIP kernels)"}
+
+
+def cpu_config0(reps: int) -> dict:
+    """BASELINE.json config 0 as the reference defines it, on the host cores: one SISA attention op fwd+bwd in fp32 at
+    B=1, T=256, H=4, d_h=64, d_s=32 (glue from theta, decay and forget logits included; upstream grad N(0,1)), with
+    the oracle's restatement of the reference's pure-PyTorch path."""
+    import torch
+
+    from oracle import reference as R
+    B, H, L = 1, 4, 256
+    gen = torch.Generator().manual_seed(0)
+    leaves = dict(q=torch.randn(B, H, L, 64, generator=gen), k=torch.randn(B, H, L, 64, generator=gen),
+                  v=torch.randn(B, H, L, 64, generator=gen), b=torch.randn(B, H, L, 32, generator=gen),
+                  c=torch.randn(B, H, L, 32, generator=gen), theta=0.01 * torch.randn(B, L, H, 16, generator=gen),
+                  a=-5 + 0.5 * torch.randn(B, L, H, generator=gen), z=4 + 0.5 * torch.randn(B, L, H, generator=gen),
+                  lam_raw=torch.full((H,), -1.0))
+    leaves = {n: t.requires_grad_(True) for n, t in leaves.items()}
+    dy = torch.randn(B, H, L, 64, generator=gen)
+
+    def step():
+        c, b, g, Fg, lam = R.unfused_glue(leaves)
+        o = R.attention_blocked(leaves["q"], leaves["k"], leaves["v"], c, b, g, lam, Fg, block_q=256)
+        torch.autograd.grad(o, list(leaves.values()), dy)
+    step()
+    times = []
+    for _ in range(max(reps, 5)):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"ms": round(t * 1e3, 3), "tokens_per_s": round(B * L / t, 1),
+            "tflops": round(1152 * B * H * L * L / 2 / t / 1e12, 6), "cores": torch.get_num_threads(),
+            "shape": "B=1, T=256, H=4, d_h=64, d_s=32, fp32, fwd+bwd (glue included)"}
 
 
 def main():
@@ -734,6 +813,7 @@ def main():
         backends.set_check_mode(default_mode)
         out["block_kernels"] = bench_block_kernels()
         out["projection_gemms"] = bench_projection_gemms()
+    out["config0_gpu"] = gpu_config0()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_reps)
     print(json.dumps(out), flush=True)
