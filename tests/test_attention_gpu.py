@@ -137,6 +137,10 @@ CASES += [
     _case("shift_g_minus5000_L1000", H=4, L=1000, seed=401, grid=True, shift_g=-5000.0,
           heads=[(0.31, "slow", "fox"), (3.0, "slow", "fox"), (R.TINY, "model", "none"), (0.0, "slow", "fox")]),
 ]
+# the reference's other shifts of g and F (tests/test_attention_kernel.py:501-538): a constant shift changes no score
+CASES += [_case(f"shift_{w}_minus{int(-d)}_L1000", H=4, L=1000, seed=402 + i, grid=True, **{f"shift_{w}": d},
+                heads=[(0.31, "slow", "fox"), (3.0, "slow", "fox"), (R.TINY, "model", "none"), (0.0, "slow", "fox")])
+          for i, (w, d) in enumerate([("F", -1000.0), ("F", -20000.0), ("g", -1000.0), ("g", -20000.0)])]
 
 
 @pytest.mark.parametrize("spec", CASES)
