@@ -113,6 +113,8 @@ def _case(name, **spec):
 
 SWEEP = [1, 2, 17, 63, 64, 65, 127, 128, 129, 200, 511, 1000, 2048]
 CASES = [_case(f"sweep_L{L}_H12", H=12, L=L, seed=L) for L in SWEEP]
+# the top of the reference's sweep, with fewer heads (the fp64 truth is dense in L)
+CASES += [_case("sweep_L4096_H4", H=4, L=4096, seed=4096), _case("sweep_L8192_H2", H=2, L=8192, seed=8192)]
 CASES += [
     _case("batch_B2_H12_L65", B=2, H=12, L=65, seed=11),
     _case("batch_B3_H2_L300", B=3, H=2, L=300, seed=13),
