@@ -203,6 +203,15 @@ def test_nan_guard_sync_mode():
         pn[0, 7, off["A"] + 2] = float("inf")
         with pytest.raises(FloatingPointError):
             FP().sisa_fused(pn, z, lam, H)
+        pt = proj.clone()                  # theta: the rotation angles of C and B
+        pt[0, 40, off["TH"] + 5] = float("-inf")
+        with pytest.raises(FloatingPointError):
+            FP().sisa_fused(pt, z, lam, H)
+        ln = lam.clone()
+        ln[1] = float("nan")
+        with pytest.raises(FloatingPointError):
+            FP().sisa_fused(proj, z, ln, H)
+        FP().sisa_fused(proj, z, lam, H)   # finite inputs pass the same check
     finally:
         backends.set_check_mode(old)
 
