@@ -11,8 +11,9 @@
 // structure (tiles, wave ownership, MFMA layouts, LDS staging) is this library's own.
 //
 // Work decomposition (16 rows per wave: one column group of the 16x16 MFMA blocks; no atomics):
-//   forward: a workgroup of 8 waves owns 128 consecutive queries; key tiles of 64 positions are staged row-major in
-//     LDS while the next tile's global loads are in flight; at most 128 VGPRs, so 4 waves per SIMD.
+//   forward: a workgroup of 8 waves owns 128 consecutive queries; key tiles of 64 positions, nearest first, are
+//     staged row-major in LDS while the next tile's global loads are in flight; at most 128 VGPRs, so 4 waves per
+//     SIMD.
 //   dq kernel: a workgroup of 8 waves owns 128 queries, two 64-query decay blocks; every key tile before them is an
 //     off-block tile for all waves, then block 0's own tile (off-block for block 1's waves) and block 1's; at most
 //     128 VGPRs (16-bit types), so 4 waves per SIMD.
@@ -289,65 +290,80 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
             d.cfm[1][tid] = pf_cf * exp2_le0((ga1 - pf_ge) * LOG2E);
         }
     };
-    // Advance to tile t (key offset 64 t): afterwards (and after the caller's barrier for two buffers) the tile is in
-    // LDS buffer t & (NBUF-1).
-    auto advance_into = [&](int t, FwdLds<T>& nxt) {   // nxt: the buffer that is idle during tile t
-        const int n0 = 64 * t;
+    // Key tiles are visited from the workgroup's last one down to key 0: the nearest keys, which usually hold a row's
+    // largest scores, come first, so that the running maximum is set early and the lazy rescale seldom fires again.
+    // Position k holds tile tlast - k, in LDS buffer k & (NBUF-1); advance_into(k, nxt) issues position k + 1 into
+    // nxt, the buffer idle during position k (two buffers), or loads position k (one buffer).
+    const int nfull = tile0 / 64;                  // tiles before the workgroup's first query block
+    const int tlast = (tile0 + 64 < kend) ? nfull + 1 : nfull;
+    auto advance_into = [&](int k, FwdLds<T>& nxt) {
+        const int t = tlast - k;
         if (NBUF == 2) {
-            if (n0 + 64 < kend) {
-                issue_tile(nxt, n0 + 64);
-                if (n0 + 128 < kend) fetch_scalars(n0 + 128);
+            if (t > 0) {
+                issue_tile(nxt, 64 * (t - 1));
+                if (t > 1) fetch_scalars(64 * (t - 2));
             }
-        } else if (t > 0) {
+        } else if (k > 0) {
             __syncthreads();
-            issue_tile(smb[0], n0);
+            issue_tile(smb[0], 64 * t);
             __syncthreads();
-            if (n0 + 64 < kend) fetch_scalars(n0 + 64);
+            if (t > 0) fetch_scalars(64 * (t - 1));
         }
     };
-    auto advance = [&](int t) { advance_into(t, smb[(t + 1) & (NBUF - 1)]); };
-    fetch_scalars(0);
-    issue_tile(smb[0], 0);
-    if (64 < kend) fetch_scalars(64);
+    fetch_scalars(64 * tlast);
+    issue_tile(smb[0], 64 * tlast);
+    if (tlast > 0) fetch_scalars(64 * (tlast - 1));
     __syncthreads();
-    // tiles before the workgroup's first query block: off-block for every wave (one code path in the loop)
-    const int nfull = tile0 / 64;
-    auto off_tile = [&](int t, const FwdLds<T>& sm, FwdLds<T>& nxt) {
-        advance_into(t, nxt);
+    // the workgroup's own tiles first: block 1's (its waves' diagonal), then block 0's (diagonal for block 0's waves,
+    // off-block for block 1's)
+    int k = 0;
+    if (tlast == nfull + 1) {
+        advance_into(0, smb[NBUF - 1]);
+        if (live && qblk == 1)
+            fwd_tile<T, true>(smb[0], 1, lane, tile0 + 64, q0, L, qf, diag_c(), cx1, onesf, fq, rs, gq, lam, m, l, acc,
+                              (w & 3) + 1);
+        if (NBUF == 2) __syncthreads();
+        k = 1;
+    }
+    {
+        const FwdLds<T>& sm = smb[k & (NBUF - 1)];
+        advance_into(k, smb[(k + 1) & (NBUF - 1)]);
         if (live) {
-            fwd_tile<T, false>(sm, qblk, lane, 64 * t, q0, L, qf, cx0, cx1, onesf, fq, rs, gq, lam, m, l, acc);
+            if (qblk == 0)
+                fwd_tile<T, true>(sm, 0, lane, tile0, q0, L, qf, diag_c(), cx1, onesf, fq, rs, gq, lam, m, l, acc,
+                                  (w & 3) + 1);
+            else
+                fwd_tile<T, false>(sm, 1, lane, tile0, q0, L, qf, cx0, cx1, onesf, fq, rs, gq, lam, m, l, acc);
         }
+        if (NBUF == 2) __syncthreads();
+        ++k;
+    }
+    // then the tiles before the workgroup's first block, nearest first: off-block for every wave
+    auto off_tile = [&](int kk, const FwdLds<T>& sm, FwdLds<T>& nxt) {
+        advance_into(kk, nxt);
+        if (live)
+            fwd_tile<T, false>(sm, qblk, lane, 64 * (tlast - kk), q0, L, qf, cx0, cx1, onesf, fq, rs, gq, lam, m, l,
+                               acc);
         if (NBUF == 2) __syncthreads();
     };
     if constexpr (NBUF == 2) {
-        // two tiles per iteration, so that each names its LDS buffers statically (no per-tile address arithmetic)
-        int t = 0;
-        for (; t + 2 <= nfull; t += 2) {
-            off_tile(t, smb[0], smb[NBUF - 1]);
-            off_tile(t + 1, smb[NBUF - 1], smb[0]);
+        // two tiles per iteration, so that each names its LDS buffers statically (no per-tile address arithmetic);
+        // the first off-block position is even or odd depending on whether block 1 had a tile
+        if (k & 1) {
+            for (; k + 2 <= tlast + 1; k += 2) {
+                off_tile(k, smb[1], smb[0]);
+                off_tile(k + 1, smb[0], smb[1]);
+            }
+            if (k <= tlast) off_tile(k, smb[1], smb[0]);
+        } else {
+            for (; k + 2 <= tlast + 1; k += 2) {
+                off_tile(k, smb[0], smb[1]);
+                off_tile(k + 1, smb[1], smb[0]);
+            }
+            if (k <= tlast) off_tile(k, smb[0], smb[1]);
         }
-        if (t < nfull) off_tile(t, smb[0], smb[NBUF - 1]);
     } else {
-        for (int t = 0; t < nfull; ++t) off_tile(t, smb[0], smb[0]);
-    }
-    // the workgroup's own tiles: block 0's (off-block for block 1's waves), then block 1's
-    advance(nfull);
-    if (live) {
-        const FwdLds<T>& sm = smb[nfull & (NBUF - 1)];
-        if (qblk == 0)
-            fwd_tile<T, true>(sm, 0, lane, tile0, q0, L, qf, diag_c(), cx1, onesf, fq, rs, gq, lam, m, l, acc,
-                              (w & 3) + 1);
-        else
-            fwd_tile<T, false>(sm, 1, lane, tile0, q0, L, qf, cx0, cx1, onesf, fq, rs, gq, lam, m, l, acc);
-    }
-    if (tile0 + 64 < kend) {
-        if (NBUF == 2) __syncthreads();
-        advance(nfull + 1);
-        if (live && qblk == 1) {
-            const FwdLds<T>& sm = smb[(nfull + 1) & (NBUF - 1)];
-            fwd_tile<T, true>(sm, 1, lane, tile0 + 64, q0, L, qf, diag_c(), cx1, onesf, fq, rs, gq, lam, m, l, acc,
-                              (w & 3) + 1);
-        }
+        for (; k <= tlast; ++k) off_tile(k, smb[0], smb[0]);
     }
     if (!live) return;
     T* O = (T*)a.o.ptr + (int64_t)b * a.o.sb + (int64_t)h * a.o.sh;
