@@ -482,8 +482,10 @@ SISA_DEV void dkv_tile(const DkvLds<T>& sm, int lane, int m0, int k0, int L, con
     }
 }
 
+// Occupancy hint 2: the max-ILP schedule then takes 165 VGPRs for 16-bit types (still 3 waves per SIMD; the hint 3
+// held it to 158 with a slower schedule, about 20 us more per backward at the north-star shape); fp32 takes 189 (2).
 template <class T>
-__global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(3))) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a) {
+__global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(2))) void attn_bwd_dkv_kernel(sisa_attn_bwd_args a) {
     constexpr int NBUF = sizeof(T) == 2 ? 2 : 1;
     __shared__ DkvLds<T> smb[NBUF];
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
