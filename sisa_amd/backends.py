@@ -99,16 +99,17 @@ def device_info(device: DeviceLike | None = None) -> dict:
 def attention_config(device: DeviceLike | None, dtype: torch.dtype) -> dict:
     """The attention kernels' fixed launch geometry (no autotuning) and the MFMA instruction used for ``dtype``.
 
-    Forward: 8 waves x 16 query rows = 128 queries per workgroup; backward: 4 waves x 16 rows = one 64-row decay
-    block of queries (dq) or keys (dk, dv, db) per workgroup; the other operand streams through LDS in 64-position
-    tiles; decay factors are anchored per 64-row block (``T``). The geometry does not depend on the device.
+    Forward and dq kernel: 8 waves x 16 query rows = 128 queries (two 64-row decay blocks) per workgroup; dkv
+    kernel: 4 waves x 16 rows = one 64-row decay block of keys (dk, dv, db) per workgroup; the other operand streams
+    through LDS in 64-position tiles; decay factors are anchored per 64-row block (``T``). The geometry does not
+    depend on the device.
     """
     mfma = {torch.bfloat16: "v_mfma_f32_16x16x32_bf16", torch.float16: "v_mfma_f32_16x16x32_f16",
             torch.float32: "v_mfma_f32_16x16x4_f32"}.get(dtype)
     if mfma is None:
         raise ValueError(f"the attention kernels take bf16, fp16 or fp32 inputs, not {dtype}")
-    return dict(T=64, tile=64, rows_per_wave=16, fwd_waves=8, fwd_rows_per_wg=128, bwd_waves=4,
-                bwd_rows_per_wg=64, mfma=mfma)
+    return dict(T=64, tile=64, rows_per_wave=16, fwd_waves=8, fwd_rows_per_wg=128, dq_waves=8, dq_rows_per_wg=128,
+                dkv_waves=4, dkv_rows_per_wg=64, mfma=mfma)
 
 
 # ------------------------------------------------------------------------------------------------------ requirements

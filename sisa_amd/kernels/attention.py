@@ -10,8 +10,9 @@ with its own factor tables and gradient buffers) and ``sisa_attention_hip`` in p
 The work per call is one C call each way. Forward: ``sisa_factors`` (per-64-row-block decay anchors rowf/colf and the
 largest rise of ``g`` in each block) unless the caller brings factors, then ``sisa_attn_fwd``, which writes ``o`` in
 (B, L, H, D) memory order, the row log-sum-exp (log2 units) and, for the exact backward, the self-normalised fp32
-output o''. Backward: ``sisa_attn_bwd`` (dq, then dk/dv/db with the per-block dlambda sums, then the dlambda total in
-fp64; deterministic). All numerics live in csrc/attention.hip and csrc/attention_bwd.hip.
+output o''. Backward: ``sisa_attn_bwd`` (two launches: dq with the fp64 dlambda sums of 16-row groups, then
+dk/dv/db, in which one workgroup adds each head's group sums in a fixed order; deterministic). All numerics live in
+csrc/attention.hip and csrc/attention_bwd.hip.
 """
 from __future__ import annotations
 
