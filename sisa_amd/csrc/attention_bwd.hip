@@ -165,40 +165,56 @@ void attn_bwd_dq_kernel(sisa_attn_bwd_args a) {
     frag8<T> qf[2], cfr, dof[2];
     float fq, rowfq, rs, gq, lse, dhat;
     {
+        // every load from a row in range (rows past L read row L - 1 and are masked), all in flight together
         const int qq = q0 + lc;
         const bool ok = qq < L;
+        const int64_t qc = ok ? qq : L - 1;
+        frag8<T> qr[2], dr[2];
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            qr[st] = load8<T>(Q + qc * a.q.sl + 32 * st + 8 * grp);
+            dr[st] = load8<T>(DO + qc * a.dout.sl + 32 * st + 8 * grp);
+        }
+        const frag8<T> cr = load8<T>(C + qc * a.c.sl + 8 * grp);
+        const float fr = has_f ? FF[qc * sfl] : 0.f;
+        const float rr = ROWF[qc];
+        gq = G[qc * sgl];
+        const float lr = LSE[qc];
+        // exact mode: Delta'' = o''.do with the fp32 o'' as stored (no snapping to the DT o: a snapped element
+        // carries up to the snap threshold of error, not proportional to the non-dominant mass of the row)
+        f32x4 oa[2], ob[2];
+        if (O32) {
+            const float* p32 = O32 + ((int64_t)bh * L + qc) * DH + 8 * grp;
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                oa[st] = *reinterpret_cast<const f32x4*>(p32 + 32 * st);
+                ob[st] = *reinterpret_cast<const f32x4*>(p32 + 32 * st + 4);
+            }
+        } else {
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                const frag8<T> ov = load8<T>(O + qc * a.o.sl + 32 * st + 8 * grp);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    oa[st][j] = (float)ov[j];
+                    ob[st][j] = (float)ov[j + 4];
+                }
+            }
+        }
         float part = 0.f;
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
-            qf[st] = ok ? scale_frag<T>(load8<T>(Q + (int64_t)qq * a.q.sl + 32 * st + 8 * grp), QSCALE) : zero8<T>();
-            dof[st] = ok ? load8<T>(DO + (int64_t)qq * a.dout.sl + 32 * st + 8 * grp) : zero8<T>();
-            if (ok) {
-                // exact mode: Delta'' = o''.do with the fp32 o'' as stored (no snapping to the DT o: a snapped element
-                // carries up to the snap threshold of error, not proportional to the non-dominant mass of the row)
-                f32x4 oa, ob;
-                if (O32) {
-                    const float* p32 = O32 + ((int64_t)bh * L + qq) * DH + 32 * st + 8 * grp;
-                    oa = *reinterpret_cast<const f32x4*>(p32);
-                    ob = *reinterpret_cast<const f32x4*>(p32 + 4);
-                } else {
-                    const frag8<T> ov = load8<T>(O + (int64_t)qq * a.o.sl + 32 * st + 8 * grp);
+            qf[st] = ok ? scale_frag<T>(qr[st], QSCALE) : zero8<T>();
+            dof[st] = ok ? dr[st] : zero8<T>();
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        oa[j] = (float)ov[j];
-                        ob[j] = (float)ov[j + 4];
-                    }
-                }
-#pragma unroll
-                for (int j = 0; j < 4; ++j) part += oa[j] * (float)dof[st][j] + ob[j] * (float)dof[st][j + 4];
-            }
+            for (int j = 0; j < 4; ++j) part += oa[st][j] * (float)dof[st][j] + ob[st][j] * (float)dof[st][j + 4];
         }
         dhat = group_sum(part);
-        cfr = ok ? load8<T>(C + (int64_t)qq * a.c.sl + 8 * grp) : zero8<T>();
-        fq = (has_f && ok) ? FF[(int64_t)qq * sfl] : 0.f;
-        rowfq = ok ? ROWF[qq] : 0.f;
+        cfr = ok ? cr : zero8<T>();
+        fq = ok ? fr : 0.f;
+        rowfq = ok ? rr : 0.f;
         rs = lam * rowfq;
-        gq = G[(int64_t)(ok ? qq : L - 1) * sgl];
-        lse = ok ? LSE[qq] : __builtin_inff();
+        lse = ok ? lr : __builtin_inff();
     }
 
     f32x4 dqa[4], dca[2];
