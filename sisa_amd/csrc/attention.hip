@@ -313,30 +313,56 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(4))) void a
     fetch_scalars(64 * tlast);
     issue_tile(smb[0], 64 * tlast);
     if (tlast > 0) fetch_scalars(64 * (tlast - 1));
-    __syncthreads();
-    // the workgroup's own tiles first: block 1's (its waves' diagonal), then block 0's (diagonal for block 0's waves,
-    // off-block for block 1's)
-    int k = 0;
-    if (tlast == nfull + 1) {
-        advance_into(0, smb[NBUF - 1]);
-        if (live && qblk == 1)
-            fwd_tile<T, true>(smb[0], 1, lane, tile0 + 64, q0, L, qf, diag_c(), cx1, onesf, fq, rs, gq, lam, m, l, acc,
-                              (w & 3) + 1);
-        if (NBUF == 2) __syncthreads();
-        k = 1;
+    // 16-bit types with both query blocks in range: block 0's tile goes into the second buffer in the prologue too, so
+    // that the two blocks' diagonal tiles run in the same position (each wave group still sees its tiles in the same
+    // order: block 1's waves T1, T0, T-1, ...; block 0's waves T0, T-1, ...)
+    const bool both = NBUF == 2 && tlast == nfull + 1;
+    if (both) {
+        issue_tile(smb[NBUF - 1], 64 * (tlast - 1));
+        if (tlast > 1) fetch_scalars(64 * (tlast - 2));
     }
-    {
-        const FwdLds<T>& sm = smb[k & (NBUF - 1)];
-        advance_into(k, smb[(k + 1) & (NBUF - 1)]);
+    __syncthreads();
+    int k = 0;
+    if (both) {
         if (live) {
-            if (qblk == 0)
-                fwd_tile<T, true>(sm, 0, lane, tile0, q0, L, qf, diag_c(), cx1, onesf, fq, rs, gq, lam, m, l, acc,
-                                  (w & 3) + 1);
+            if (qblk == 1)
+                fwd_tile<T, true>(smb[0], 1, lane, tile0 + 64, q0, L, qf, diag_c(), cx1, onesf, fq, rs, gq, lam, m, l,
+                                  acc, (w & 3) + 1);
             else
-                fwd_tile<T, false>(sm, 1, lane, tile0, q0, L, qf, cx0, cx1, onesf, fq, rs, gq, lam, m, l, acc);
+                fwd_tile<T, true>(smb[NBUF - 1], 0, lane, tile0, q0, L, qf, diag_c(), cx1, onesf, fq, rs, gq, lam, m, l,
+                                  acc, (w & 3) + 1);
         }
-        if (NBUF == 2) __syncthreads();
-        ++k;
+        __syncthreads();
+        // block 1's waves take block 0's tile (off-block for them) while the next tile's DMA fills the first buffer
+        advance_into(1, smb[0]);
+        if (live && qblk == 1)
+            fwd_tile<T, false>(smb[NBUF - 1], 1, lane, tile0, q0, L, qf, cx0, cx1, onesf, fq, rs, gq, lam, m, l, acc);
+        __syncthreads();
+        k = 2;
+    } else {
+        // the workgroup's own tiles first: block 1's (its waves' diagonal), then block 0's (diagonal for block 0's
+        // waves, off-block for block 1's)
+        if (tlast == nfull + 1) {
+            advance_into(0, smb[NBUF - 1]);
+            if (live && qblk == 1)
+                fwd_tile<T, true>(smb[0], 1, lane, tile0 + 64, q0, L, qf, diag_c(), cx1, onesf, fq, rs, gq, lam, m, l,
+                                  acc, (w & 3) + 1);
+            if (NBUF == 2) __syncthreads();
+            k = 1;
+        }
+        {
+            const FwdLds<T>& sm = smb[k & (NBUF - 1)];
+            advance_into(k, smb[(k + 1) & (NBUF - 1)]);
+            if (live) {
+                if (qblk == 0)
+                    fwd_tile<T, true>(sm, 0, lane, tile0, q0, L, qf, diag_c(), cx1, onesf, fq, rs, gq, lam, m, l,
+                                      acc, (w & 3) + 1);
+                else
+                    fwd_tile<T, false>(sm, 1, lane, tile0, q0, L, qf, cx0, cx1, onesf, fq, rs, gq, lam, m, l, acc);
+            }
+            if (NBUF == 2) __syncthreads();
+            ++k;
+        }
     }
     // then the tiles before the workgroup's first block, nearest first: off-block for every wave
     auto off_tile = [&](int kk, const FwdLds<T>& sm, FwdLds<T>& nxt) {
@@ -491,8 +517,8 @@ extern "C" int sisa_attn_bwd(const sisa_attn_bwd_args* a, void* stream) {
 
 // ------------------------------------------------------------------------------------------------ no-alloc backward
 // The backward's workspace (five (B,H,L) fp32 row buffers and the fp64 dlambda group sums, at most 2^20 of them for
-// B*H*L <= 2^20) in a file-scope device array, for callers that cannot allocate. Every GPU the library runs on holds its
-// own copy (28 MiB) until the process ends. In host code `scratch` names a host-side
+// B*H*L <= 2^20) in a file-scope device array, for callers that cannot allocate. Every GPU the library runs on holds
+// its own copy (28 MiB) until the process ends. In host code `scratch` names a host-side
 // stand-in, not device memory: its device address is looked up once per device (hipGetSymbolAddress, with that
 // device current) and only that address is ever handed to kernels.
 static __device__ __align__(256) float scratch[(WS_N + 2) * (int64_t)SISA_NOALLOC_MAX_BHL];   // 28 MiB
