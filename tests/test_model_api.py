@@ -509,7 +509,7 @@ def test_pretrained_directories(tmp_path):
     assert loaded.config == src.config and not loaded.training and torch.equal(loaded(ids).logits, src(ids).logits)
     other = SISAForCausalLM.from_pretrained(tmp_path, attn_impl="auto", dtype=torch.bfloat16)
     assert other.config.attn_impl == "auto" and other.embed.weight.dtype == torch.bfloat16
-    with pytest.raises(ValueError, match="not a directory"):
+    with pytest.raises(ValueError, match="expects the directory save_pretrained writes"):
         SISAForCausalLM.from_pretrained(tmp_path / "missing")
     (tmp_path / "model.safetensors").unlink()
     with pytest.raises(FileNotFoundError):
