@@ -230,7 +230,7 @@ def select_impl(requested: str, x: torch.Tensor, cfg: SISAConfig | None) -> str:
 def describe() -> str:
     """A report of PyTorch, the check mode, and per GPU the HIP status and what ``attn_impl="auto"`` picks."""
     out = [f"torch {torch.__version__}, HIP {getattr(torch.version, 'hip', None)}",
-           f"check mode: {get_check_mode()} ({CHECK_MODES[get_check_mode()]})"]
+           f"check mode {get_check_mode()!r}: {CHECK_MODES[get_check_mode()]}"]
     gpus = torch.cuda.device_count() if torch.cuda.is_available() else 0
     if not gpus:
         out.append("no GPU: attn_impl='auto' runs 'torch'")

@@ -106,7 +106,7 @@ class SISACache:
 
     @property
     def seq_len(self) -> int:
-        """Number of cached positions (0 when empty)."""
+        """How many positions the cache holds (0 before the prefill)."""
         slab = self._slabs.get(0)
         return 0 if slab is None else slab.filled
 
@@ -122,8 +122,8 @@ def _eos_ids(eos_token_id: int | Iterable[int] | Tensor | None) -> list[int]:
     an iterable of integers. Booleans, strings, floats and arrays of more than one dimension raise ``TypeError``."""
     if eos_token_id is None:
         return []
-    err = TypeError(f"eos_token_id must be an integer or an iterable of integers, got {eos_token_id!r} "
-                    f"({type(eos_token_id).__name__})")
+    err = TypeError(f"eos_token_id takes one token id or a flat collection of ids; {eos_token_id!r} "
+                    f"({type(eos_token_id).__name__}) is neither")
     if isinstance(eos_token_id, (bool, str, bytes)):
         raise err
     if isinstance(eos_token_id, numbers.Integral):
@@ -182,7 +182,8 @@ def generate(model: "SISAForCausalLM", input_ids: Tensor, max_new_tokens: int, t
         raise ValueError(f"top_k = {top_k}: expected a positive integer or None")
     rows = input_ids if input_ids.dim() == 2 else input_ids.unsqueeze(0)
     if rows.dim() != 2 or rows.shape[1] == 0:
-        raise ValueError(f"input_ids must be a non-empty (B, L) or (L,) tensor, got shape {tuple(input_ids.shape)}")
+        raise ValueError(f"generate needs at least one prompt token per row in a (B, L) or (L,) tensor, got shape "
+                         f"{tuple(input_ids.shape)}")
     stops = _eos_ids(eos_token_id)
     stop_ids = torch.tensor(stops, device=rows.device, dtype=rows.dtype) if stops else None
     prompt = rows.shape[1]

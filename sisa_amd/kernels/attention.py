@@ -211,7 +211,7 @@ def kernel_operands(q, k, v, c, b, g, lam, fgate):
                         f"{v.dtype}")
     wide = {n: t.dtype for n, t in (("g", g), ("fgate", fgate)) if t is not None and t.dtype != torch.float32}
     if wide:
-        raise TypeError(f"sisa_attention_hip: g and fgate must be float32, got {wide}")
+        raise TypeError(f"sisa_attention_hip: the cumulative gates are read as float32; got {wide}")
     places = {t.device for t, _ in want.values()}
     if len(places) != 1 or not q.is_cuda:
         raise ValueError(f"sisa_attention_hip: all inputs must be on one GPU, got {sorted(map(str, places))}")

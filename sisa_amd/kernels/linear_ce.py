@@ -37,7 +37,9 @@ __all__ = ["linear_cross_entropy", "reference_linear_cross_entropy", "lmce_rows"
 VOCAB_MULTIPLE = 128
 LOGITS_BUDGET = 1 << 30          # bytes of one chunk of logits (the reference's budget)
 FUSED_K_MULTIPLE = 64            # sisa_lmce_fwd streams the hidden size in 64-wide stages
-_MM_OUT_DTYPE = hasattr(torch.ops.aten.mm, "dtype") and hasattr(torch.ops.aten.addmm, "dtype_out")
+# whether this torch's mm/addmm take an output dtype (a float32 result of 16-bit operands without a cast pass)
+_MM_OUT_DTYPE = ("dtype" in torch.ops.aten.mm.overloads()
+                 and "dtype_out" in torch.ops.aten.addmm.overloads())
 
 
 # ------------------------------------------------------------------------------------------------ pieces

@@ -455,7 +455,7 @@ def test_infer_config_from_shapes():
         assert getattr(cfg, field) == getattr(src.config, field), field
     with pytest.raises(ValueError, match="cannot be overridden"):
         CK.infer_config_from_state_dict(_paper_layout(src), d_ff=100)
-    with pytest.raises(ValueError, match="not a SISA state dict"):
+    with pytest.raises(ValueError, match="does not describe a SISA model"):
         CK.infer_config_from_state_dict({"embed.weight": torch.zeros(3, 4)})
 
 

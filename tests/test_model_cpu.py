@@ -181,7 +181,7 @@ def test_paper_checkpoint_keys(tmp_path):
     assert all(torch.equal(loaded.state_dict()[k], v) for k, v in sd.items())
     with pytest.raises(ValueError, match="cannot be overridden"):
         CK.infer_config_from_state_dict(sd, d_model=64)
-    with pytest.raises(ValueError, match="missing"):
+    with pytest.raises(ValueError, match="is absent"):
         CK.infer_config_from_state_dict({k: v for k, v in sd.items() if "lambda_raw" not in k})
     bad = dict(sd)
     bad["layers.0.attn.W_Q.weight"] = torch.zeros(3, 3)
