@@ -74,7 +74,8 @@ typedef struct {
     float* o32;                /* (B,H,L,64) contiguous fp32 output or NULL (bf16/fp16 only) */
 } sisa_attn_fwd_args;
 
-/* Workspace (bytes) of sisa_attn_bwd: six (B,H,L) fp32 row buffers. */
+/* Workspace (bytes) of sisa_attn_bwd: five (B,H,L) fp32 row buffers, then B*H*ceil(L/16) fp64 dlambda sums of
+ * 16-row groups. Always size the buffer with this function (it is not a multiple of the row-buffer size). */
 int64_t sisa_attn_bwd_workspace_bytes(int32_t B, int32_t H, int32_t L);
 
 /* Backward: dq, dk, dv, dc, db, dg, dF and dlambda, exact-delta scheme by default (`exact`). Two launches; the
@@ -370,6 +371,20 @@ int64_t sisa_decode_workspace_bytes(int32_t B, int32_t H, int32_t M, int32_t N);
 int sisa_decode_attn(const sisa_decode_args* a, void* stream);
 
 /* ------------------------------------------------------------------------------------------------ misc */
+
+/* The library's 16-bit operand rounding over a flat buffer: y[i] = x[i] rounded to nearest even in dtype (the
+ * kernels' pair conversion), and back[i] = y[i] widened to fp32 by the kernels' load conversion (back may be NULL).
+ * Replaces nothing on the call path: it exposes `_bf16x2` / `_bf16x2_f32` (src/sisa/kernels/attention.py:156-173),
+ * which the kernels inline, so that they can be compared bit for bit with tensor.to(dtype) / .float(). */
+typedef struct {
+    int64_t n;                 /* elements (0 is a no-op) */
+    int32_t dtype;             /* SISA_BF16 or SISA_F16 */
+    const float* x;            /* (n,) fp32, 16-byte aligned */
+    void* y;                   /* (n,) dtype output, 16-byte aligned */
+    float* back;               /* (n,) fp32 output or NULL, 16-byte aligned */
+} sisa_round16_args;
+
+int sisa_round16(const sisa_round16_args* a, void* stream);
 
 int sisa_abi_version(void);
 const char* sisa_last_error(void);

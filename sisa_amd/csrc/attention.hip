@@ -10,6 +10,17 @@
 // before log2e, the self-normalised fp32 o'' for the exact delta, and the delta-free diagonal dS_tt. The kernel
 // structure (tiles, wave ownership, MFMA layouts, LDS staging) is this library's own.
 //
+// One rounding point differs from the reference on purpose. The side-term operand of the dc and db products,
+// W_ij = dS_ij * lam * exp(g_i - g_j), is rounded to the 16-bit type for the MFMA. The reference rounds
+// dS * (colf * mid) in its dq kernel and dS * (rowf * mid) in its dkv kernel (attention.py:20-21): the same pair then
+// enters dc_i and db_j with two different roundings. Each pair's rotation terms of dPhi (+ at the query, - at the key)
+// cancel in the reverse scan dtheta_t = sum_{s >= t} dPhi_s only for pairs that straddle t, exactly, when both sides
+// see the same operand value; otherwise every pair past t leaves a residue of the operand's rounding, and the error
+// of dtheta grows with the sequence (measured against fp64: 1.3-2.1e-2 at T = 4096, 2.0-2.8e-2 at T = 16384). Here
+// both kernels round the same fp32 value dS * (rowf_i * (colf_j * mid)) (pairwise lam * exp2(min(...)) inside the
+// query's own block, as before) and apply lam to the sums: dtheta is then as accurate as every other gradient
+// (2.4e-3 at both lengths), for one more multiply per off-block score in each backward kernel.
+//
 // Work decomposition (16 rows per wave: one column group of the 16x16 MFMA blocks; no atomics):
 //   forward: a workgroup of 8 waves owns 128 consecutive queries; key tiles of 64 positions, nearest first, are
 //     staged row-major in LDS while the next tile's global loads are in flight; at most 128 VGPRs, so 4 waves per
@@ -31,9 +42,10 @@ namespace {
 // ------------------------------------------------------------------------------------------------ factors
 // rowf_t = exp2(min((g_t - g_{block start})*log2e, 0)), colf_t = exp2(min((g_{block end} - g_t)*log2e, 0)), and the
 // maximum increase g_t - g_{t-1} per block. Reference: attention.py:129-153.
-__global__ __launch_bounds__(64) void factors_kernel(sisa_factors_args a) {
-    const int p = blockIdx.x;
-    const int bh = blockIdx.y;
+__global__ __launch_bounds__(64) void factors_kernel(sisa_factors_args a, int NT) {
+    // one-dimensional grid (B*H may exceed the 65,536 limit of the second grid dimension): block = bh * NT + p
+    const int p = (int)(blockIdx.x % (unsigned)NT);
+    const int bh = (int)(blockIdx.x / (unsigned)NT);
     const int H = a.H, L = a.L;
     const int b = bh / H, h = bh % H;
     const float* G = (const float*)a.g.ptr + (int64_t)b * a.g.sb + (int64_t)h * a.g.sh;
@@ -56,7 +68,7 @@ __global__ __launch_bounds__(64) void factors_kernel(sisa_factors_args a) {
     const float prv = G[(int64_t)tp * sgl];
     float inc = (msk && t > 0) ? g - prv : -__builtin_inff();
     for (int o = 32; o > 0; o >>= 1) inc = nmax(inc, __shfl_xor(inc, o));
-    if (threadIdx.x == 0) a.mono[(int64_t)bh * gridDim.x + p] = inc;
+    if (threadIdx.x == 0) a.mono[(int64_t)bh * NT + p] = inc;
 }
 
 // ------------------------------------------------------------------------------------------------ forward
@@ -433,8 +445,9 @@ extern "C" int sisa_factors(const sisa_factors_args* a, void* stream) {
     SISA_REQUIRE(a != nullptr, "sisa_factors: null args");
     SISA_REQUIRE(a->B >= 1 && a->H >= 1 && a->L >= 1, "sisa_factors: bad shape B=%d H=%d L=%d", a->B, a->H, a->L);
     SISA_REQUIRE(g_view_ok(a->g) && a->rowf && a->colf && a->mono, "sisa_factors: null pointer");
-    dim3 grid((unsigned)sisa::cdiv(a->L, BLK), (unsigned)(a->B * a->H));
-    factors_kernel<<<grid, 64, 0, (hipStream_t)stream>>>(*a);
+    const int64_t nt = sisa::cdiv(a->L, BLK);
+    SISA_REQUIRE(nt * a->B * a->H < ((int64_t)1 << 31), "sisa_factors: B*H*ceil(L/64) exceeds the grid limit");
+    factors_kernel<<<dim3((unsigned)(nt * a->B * a->H)), 64, 0, (hipStream_t)stream>>>(*a, (int)nt);
     return sisa::launch_status("sisa_factors");
 }
 

@@ -19,7 +19,7 @@ struct __attribute__((aligned(16))) DqLds {
 
 // Per-query row sums of the dq kernel (diagonal excluded): xa = sum dS^ u, ya = sum P u, wa = D = sum dS^,
 // za = Z = sum P, ptt = P_tt, dptt = dP_tt, xd = cb_tt. Off-block tiles accumulate xa, ya without the row factor
-// rowf; a wave's own-block tile is its last one, and rowf (lam*rowf for dc) is applied once before it.
+// rowf; a wave's own-block tile is its last one, and rowf (lam for dc) is applied once before it.
 struct RowSums {
     float xa, ya, wa, za, ptt, dptt, xd;
 };
@@ -32,13 +32,14 @@ struct RowSums {
 // masked for all 16 queries and are skipped.
 template <class T, bool DIAG>
 SISA_DEV void dq_tile(const DqLds<T>& sm, int qblk, int lane, int n0, int q0, int L, const frag8<T> (&qf)[2],
-                      const frag8<T>& cfr, const frag8<T> (&dof)[2], float fq, float rs, float gq, float lse,
+                      const frag8<T>& cfr, const frag8<T> (&dof)[2], float fq, float rf, float gq, float lse,
                       float dhat, float lam, bool exact, RowSums& R, f32x4 (&dqa)[4], f32x4 (&dca)[2], int nkb = 4) {
     constexpr bool F16 = Anchor<T>::on;
     constexpr bool ANCH = F16 && !DIAG;
     const int grp = lane >> 4, lc = lane & 15;
     const int qq = q0 + lc;
     const float* cfm = sm.cfm[qblk];
+    const float rs = lam * rf;                 // row scale lambda * rowf of the off-block scores
     const float ftl = ANCH ? fmaf(fq - sm.fk[63], LOG2E, -lse) : -lse;
     const f32x4 ndh = F16 ? f32x4{-dhat, -dhat, -dhat, -dhat} : zero4();
 #pragma unroll
@@ -106,7 +107,10 @@ SISA_DEV void dq_tile(const DqLds<T>& sm, int qblk, int lane, int n0, int q0, in
                     R.za += pr;
                     R.wa += ds;
                     dsv[hb][i] = ds;
-                    wv[hb][i] = ds * cf[i];
+                    // the dc operand dS * (rowf_i * (colf_j * mid)): the same fp32 value the dkv kernel rounds for
+                    // the pair's db term, so that the pair's two rotation terms of dPhi cancel exactly in the
+                    // reverse scan of dtheta (lambda is applied to the sums)
+                    wv[hb][i] = ds * (rf * cf[i]);
                 }
             }
         }
@@ -285,7 +289,7 @@ void attn_bwd_dq_kernel(sisa_attn_bwd_args a) {
     auto off_tile = [&](int t, const DqLds<T>& sm, DqLds<T>& nxt) {
         advance_into(t, nxt);
         if (live)
-            dq_tile<T, false>(sm, qblk, lane, 64 * t, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, exact, R, dqa,
+            dq_tile<T, false>(sm, qblk, lane, 64 * t, q0, L, qf, cfr, dof, fq, rowfq, gq, lse, dhat, lam, exact, R, dqa,
                               dca);
         if (NBUF == 2) __syncthreads();
     };
@@ -301,20 +305,20 @@ void attn_bwd_dq_kernel(sisa_attn_bwd_args a) {
         for (int t = 0; t < nt; ++t) off_tile(t, smb[0], smb[0]);
     }
     // block 0's own tile (its waves' last tile; an off-block tile for block 1's waves), then block 1's own tile. The
-    // off-block row factors (lam * rowf for dc) are applied once, in fp32, before a wave's own tile.
+    // off-block row factors (rowf for the row sums, lam for dc) are applied once, in fp32, before a wave's own tile.
     auto own_tile = [&](const DqLds<T>& sm, int n0) {
         R.xa *= rowfq;
         R.ya *= rowfq;
-        dca[0] *= rs;
-        dca[1] *= rs;
-        dq_tile<T, true>(sm, qblk, lane, n0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, exact, R, dqa, dca,
+        dca[0] *= lam;
+        dca[1] *= lam;
+        dq_tile<T, true>(sm, qblk, lane, n0, q0, L, qf, cfr, dof, fq, rowfq, gq, lse, dhat, lam, exact, R, dqa, dca,
                          (w & 3) + 1);
     };
     advance_into(nt, smb[(nt + 1) & (NBUF - 1)]);
     if (live) {
         const DqLds<T>& sm = smb[nt & (NBUF - 1)];
         if (qblk == 0) own_tile(sm, tile0);
-        else dq_tile<T, false>(sm, 1, lane, tile0, q0, L, qf, cfr, dof, fq, rs, gq, lse, dhat, lam, exact, R, dqa, dca);
+        else dq_tile<T, false>(sm, 1, lane, tile0, q0, L, qf, cfr, dof, fq, rowfq, gq, lse, dhat, lam, exact, R, dqa, dca);
     }
     if (tile0 + 64 < kend) {
         if (NBUF == 2) __syncthreads();
@@ -393,6 +397,7 @@ struct __attribute__((aligned(16))) DkvLds {
     T ds[64 * DH];               // dO (dP; transposed reads for dv)
     float lse[64], dhat[64], ddel[64], fq[64], gq[64];
     float rq[64];                // rowf * mid for the query block against the workgroup's key block
+    float rf[64];                // rowf (the db operand's row factor)
     float ftl[64];               // (F_i - F_e) log2e - lse_i (16-bit: anchored off-block scores)
     float ndh[64];               // -Delta_i (16-bit: the dO.V MFMA's accumulator input)
 };
@@ -404,8 +409,8 @@ struct __attribute__((aligned(16))) DkvLds {
 // are masked for all 16 keys and are skipped (16-bit types; the fp32 kernel, at its register limit, computes them).
 template <class T, bool PAIR>
 SISA_DEV void dkv_tile(const DkvLds<T>& sm, int lane, int m0, int k0, int L, const frag8<T> (&kf)[2],
-                       const frag8<T> (&vf)[2], const frag8<T>& bfr, float fk, float nfe, float rk, float gk, float dsd,
-                       float lam, bool exact, float& dgu, float& dfs, f32x4 (&dva)[4], f32x4 (&dka)[4],
+                       const frag8<T> (&vf)[2], const frag8<T>& bfr, float fk, float nfe, float rk, float cmk, float gk,
+                       float dsd, float lam, bool exact, float& dgu, float& dfs, f32x4 (&dva)[4], f32x4 (&dka)[4],
                        f32x4 (&dba)[2], int q0b = 0) {
     constexpr bool F16 = Anchor<T>::on;
     constexpr bool ANCH = F16 && !PAIR;
@@ -463,6 +468,7 @@ SISA_DEV void dkv_tile(const DkvLds<T>& sm, int lane, int m0, int k0, int L, con
                 }
             } else {
                 const f32x4 rq = lds4f(&rqm[i0]);
+                const f32x4 rf = lds4f(&sm.rf[i0]);
                 const f32x4 off = ANCH ? lds4f(&sm.ftl[i0]) : zero4();
                 const f32x4 lq = ANCH ? zero4() : lds4f(&sm.lse[i0]);
                 const f32x4 fq = ANCH ? zero4() : lds4f(&sm.fq[i0]);
@@ -480,7 +486,7 @@ SISA_DEV void dkv_tile(const DkvLds<T>& sm, int lane, int m0, int k0, int L, con
                     dfs += dsx;
                     pv[hb][i] = p;
                     kv[hb][i] = dsx;
-                    bv[hb][i] = dsh * rq[i];
+                    bv[hb][i] = dsh * (rf[i] * cmk);   // dS * (rowf_i * (colf_j * mid)), as in the dq kernel
                 }
             }
         }
@@ -603,6 +609,7 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(2))) void 
             d.fq[tid] = pf_f;
             d.gq[tid] = pf_g;
             d.rq[tid] = pf_rowf * exp2_le0((pf_gm - ge) * LOG2E);
+            d.rf[tid] = pf_rowf;
             d.ftl[tid] = fmaf(pf_f - fe, LOG2E, -pf_lse);
             d.ndh[tid] = -pf_dh;
         }
@@ -629,8 +636,11 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(2))) void 
         advance(t);
         if (live) {
             const DkvLds<T>& sm = smb[t & (NBUF - 1)];
-            dkv_tile<T, false>(sm, lane, mlast - 64 * t, k0, L, kf, vf, bfr, fk, nfe, rk, gk, dsd, lam, exact, dgu,
-                               dfs, dva, dka, dba);
+            // colf_j * mid of this query tile: mid from the dq kernel's formula (g at the query block's start,
+            // gq[0], against g at the key block's end)
+            const float cmk = colf * exp2_le0((sm.gq[0] - ge) * LOG2E);
+            dkv_tile<T, false>(sm, lane, mlast - 64 * t, k0, L, kf, vf, bfr, fk, nfe, rk, cmk, gk, dsd, lam, exact,
+                               dgu, dfs, dva, dka, dba);
         }
         if (NBUF == 2) __syncthreads();
     }
@@ -639,10 +649,10 @@ __global__ __launch_bounds__(NTHB) __attribute__((amdgpu_waves_per_eu(2))) void 
         // the block's own tile: apply the off-block column factors once, in fp32, then the pair path
         const DkvLds<T>& sm = smb[nt & (NBUF - 1)];
         dgu *= colf;
-        dba[0] *= rk;
-        dba[1] *= rk;
-        dkv_tile<T, true>(sm, lane, ktile0, k0, L, kf, vf, bfr, fk, nfe, rk, gk, dsd, lam, exact, dgu, dfs, dva, dka,
-                          dba, w);
+        dba[0] *= lam;
+        dba[1] *= lam;
+        dkv_tile<T, true>(sm, lane, ktile0, k0, L, kf, vf, bfr, fk, nfe, rk, 0.f, gk, dsd, lam, exact, dgu, dfs, dva,
+                          dka, dba, w);
     }
     if (w == 0 && b == 0 && ktile == 0) {
         // dlambda_h: the B * ceil(L/16) group sums of head h (written by the dq kernel) added in a fixed order,

@@ -150,17 +150,18 @@ def _eos_ids(eos_token_id: int | Iterable[int] | Tensor | None) -> list[int]:
 
 def _pick(logits: Tensor, do_sample: bool, temperature: float, top_k: int | None,
           generator: torch.Generator | None) -> Tensor:
-    """The next token per row: argmax, or a draw from ``softmax(logits / temperature)`` over the ``top_k`` largest
-    logits (all of them without ``top_k``). The top-k draw normalises over the k candidates only."""
+    """The next token per row: argmax, or a draw from ``softmax(logits / temperature)`` over the whole vocabulary
+    with every logit below the row's ``top_k``-th largest set to -inf (the reference's sampling rule,
+    src/sisa/generation.py:126-135: ties at the k-th value stay candidates, and a seeded generator yields the same
+    draws as the reference's)."""
     scores = logits.float()
     if not do_sample:
         return scores.argmax(dim=-1)
     scores = scores / temperature
-    if top_k is None or top_k >= scores.shape[-1]:
-        return torch.multinomial(scores.softmax(-1), 1, generator=generator).squeeze(-1)
-    best, where = scores.topk(top_k, dim=-1)
-    choice = torch.multinomial(best.softmax(-1), 1, generator=generator)
-    return where.gather(-1, choice).squeeze(-1)
+    if top_k is not None and top_k < scores.shape[-1]:
+        floor = scores.topk(top_k, dim=-1).values[..., -1:]
+        scores = torch.where(scores < floor, torch.full_like(scores, float("-inf")), scores)
+    return torch.multinomial(scores.softmax(-1), 1, generator=generator).squeeze(-1)
 
 
 @torch.no_grad()

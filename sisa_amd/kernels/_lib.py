@@ -111,6 +111,10 @@ class DecodeArgs(Structure):
                 ("out", c_void_p), ("workspace", c_void_p)]
 
 
+class Round16Args(Structure):
+    _fields_ = [("n", c_int64), ("dtype", c_int32), ("x", c_void_p), ("y", c_void_p), ("back", c_void_p)]
+
+
 # exported symbol -> (argument types, return type); the same list the header declares
 SIGNATURES = {
     "sisa_abi_version": ([], c_int),
@@ -140,6 +144,7 @@ SIGNATURES = {
     "sisa_wgrad": ([POINTER(WgradArgs), c_void_p], c_int),
     "sisa_decode_workspace_bytes": ([c_int32, c_int32, c_int32, c_int32], c_int64),
     "sisa_decode_attn": ([POINTER(DecodeArgs), c_void_p], c_int),
+    "sisa_round16": ([POINTER(Round16Args), c_void_p], c_int),
 }
 
 _LOCK = threading.Lock()

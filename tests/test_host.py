@@ -39,7 +39,7 @@ def _header_functions():
 def test_library_exports_every_header_function(lib):
     from sisa_amd.kernels import _lib
     declared = _header_functions()
-    assert len(declared) == 27
+    assert len(declared) == 28
     assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
     out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True, check=True)
     exported = set(re.findall(r"\bT (sisa_\w+)$", out.stdout, re.M))
@@ -54,7 +54,8 @@ def test_struct_layout_matches_c(tmp_path):
              "AttnBwdArgs": "sisa_attn_bwd_args", "PrepFwdArgs": "sisa_prep_fwd_args",
              "PrepBwdArgs": "sisa_prep_bwd_args", "LmceRowsArgs": "sisa_lmce_rows_args",
              "RmsNormArgs": "sisa_rmsnorm_args", "NormArgs": "sisa_norm_args", "SwigluArgs": "sisa_swiglu_args",
-             "DecodeArgs": "sisa_decode_args", "WgradArgs": "sisa_wgrad_args", "LmceFwdArgs": "sisa_lmce_fwd_args"}
+             "DecodeArgs": "sisa_decode_args", "WgradArgs": "sisa_wgrad_args", "LmceFwdArgs": "sisa_lmce_fwd_args",
+             "Round16Args": "sisa_round16_args"}
     lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "sisa_hip.h"', "int main(void) {"]
     expect = []
     for py, c in pairs.items():

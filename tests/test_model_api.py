@@ -15,6 +15,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle import model64 as M64
+from oracle import reference as R
 from model_utils import rel_err, tiny_config, tiny_model, token_ids
 from sisa_amd import PRESETS, SISAAttention, SISABlock, SISAConfig, SISAForCausalLM, sisa_attention
 from sisa_amd import checkpoint as CK
@@ -123,24 +124,39 @@ def test_zero_c_init_is_forgetting_attention():
 
 
 # ------------------------------------------------------------------------------------------------ causality, blocks
-@pytest.mark.parametrize("block_q", [16, 256])
-def test_causality_is_exact(block_q):
+def _first_divergent_position(a: torch.Tensor, b: torch.Tensor) -> int:
+    """The first time index at which two (B, T, V) logits tensors differ anywhere (T if they never do)."""
+    same = (a == b).flatten(2).all(-1).all(0)
+    return int((~same).nonzero()[0]) if bool((~same).any()) else a.shape[1]
+
+
+@pytest.mark.parametrize("block_q", [5, 16, 256])
+def test_logits_never_see_later_tokens(block_q):
+    """Replacing every token from position t on (each by a different token) changes nothing before t, bitwise, and
+    changes position t itself -- for cuts inside, at the edge of and across the torch path's query blocks."""
     model = tiny_model(torch_block_q=block_q)
-    ids = token_ids(2, 50)
-    ref = model(ids).logits
-    ids2 = ids.clone()
-    ids2[:, 23] = (ids2[:, 23] + 7) % V
-    out = model(ids2).logits
-    assert torch.equal(out[:, :23], ref[:, :23]) and not torch.equal(out[:, 23], ref[:, 23])
+    ids = token_ids(2, 48, seed=11)
+    base = model(ids).logits
+    for t in (0, 1, block_q - 1, block_q, 47):
+        if t >= ids.shape[1]:
+            continue
+        other = ids.clone()
+        other[:, t:] = (ids[:, t:] * 31 + 5) % V
+        assert bool((other[:, t:] != ids[:, t:]).all())
+        assert _first_divergent_position(model(other).logits, base) == t, f"cut {t}"
 
 
-def test_prefix_consistency_and_block_size():
-    model = tiny_model()
-    ids = token_ids(2, 70)
+def test_prefix_runs_and_block_sizes_agree():
+    """Running a prefix of the sequence, or the torch path with any query-block size, evaluates the same function:
+    agreement to fp32 summation-order level (1e-5 norm-wise)."""
+    model = tiny_model(seed=4)
+    ids = token_ids(3, 66, seed=4)
     full = model(ids).logits
-    assert rel_err(model(ids[:, :31]).logits, full[:, :31]) < 1e-5
-    model.config.torch_block_q = 9
-    assert rel_err(model(ids).logits, full) < 1e-5
+    for n in (1, 17, 64, 65):
+        assert rel_err(model(ids[:, :n]).logits, full[:, :n]) < 1e-5, f"prefix {n}"
+    for block_q in (3, 9, 40, 1000):
+        model.config.torch_block_q = block_q
+        assert rel_err(model(ids).logits, full) < 1e-5, f"block_q {block_q}"
 
 
 # ------------------------------------------------------------------------------------------------ loss options
@@ -193,15 +209,21 @@ def test_lambda_raw_survives_low_precision_casts():
 
 
 # ------------------------------------------------------------------------------------------------ training utilities
-def test_gradient_checkpointing_gives_the_same_gradients():
-    ids = token_ids(2, 30)
-    grads = []
-    for ckpt in (False, True):
-        model = tiny_model(gradient_checkpointing=ckpt).train()
-        model(ids, labels=ids).loss.backward()
-        grads.append({n: p.grad for n, p in model.named_parameters()})
-    for name, g in grads[0].items():
-        torch.testing.assert_close(grads[1][name], g, rtol=1e-6, atol=1e-8)
+def test_checkpointed_blocks_reproduce_loss_and_gradients():
+    """Recomputing each block in the backward (gradient checkpointing) gives the same loss bitwise and the same
+    gradients for every parameter up to reassociation (flattened vector, 1e-6 norm-wise)."""
+    ids = token_ids(2, 30, seed=6)
+    plain = tiny_model(seed=6).train()
+    ckpt = tiny_model(seed=6, gradient_checkpointing=True).train()
+    ckpt.load_state_dict(plain.state_dict())
+    losses, flat = [], []
+    for m in (plain, ckpt):
+        loss = m(ids, labels=ids).loss
+        loss.backward()
+        losses.append(loss.detach())
+        flat.append(torch.cat([p.grad.flatten() for _, p in sorted(m.named_parameters())]))
+    assert torch.equal(losses[0], losses[1])
+    assert rel_err(flat[1], flat[0]) < 1e-6
 
 
 def test_parameter_counts_and_compile_common():
@@ -238,37 +260,35 @@ def test_backend_selection_on_cpu():
 
 # ------------------------------------------------------------------------------------------------ torch functional
 def _dense64(q, k, v, c, b, g, lam, f):
-    """Dense float64 SISA attention (the formula of src/sisa/functional.py:1-36)."""
-    q, k, v, c, b, g, lam = (t.double() for t in (q, k, v, c, b, g, lam))
-    L = q.shape[2]
-    causal = torch.ones(L, L, dtype=torch.bool).tril()
-    dg = (g[..., :, None] - g[..., None, :]).masked_fill(~causal, 0.0)
-    s = q @ k.transpose(-1, -2) / math.sqrt(q.shape[-1]) + lam.view(1, -1, 1, 1) * dg.exp() * (c @ b.transpose(-1, -2))
-    if f is not None:
-        s = s + f.double()[..., :, None] - f.double()[..., None, :]
-    return s.masked_fill(~causal, float("-inf")).softmax(-1) @ v
+    """The oracle's dense evaluation of the SISA formula in float64 (oracle/reference.py: dense_attention)."""
+    to64 = (lambda t: None if t is None else t.detach().double())  # noqa: E731
+    return R.dense_attention(*(to64(t) for t in (q, k, v, c, b, g, lam, f)))
 
 
 def _inputs(seed, bsz=1, h=2, L=300, d=64, s=32, with_f=True):
-    gen = torch.Generator().manual_seed(seed)
-    q, k, v = (torch.randn(bsz, h, L, d, generator=gen) for _ in range(3))
-    c, b = (torch.randn(bsz, h, L, s, generator=gen) for _ in range(2))
-    g = torch.cumsum(-0.5 * torch.rand(bsz, h, L, generator=gen), 2)
-    lam = torch.rand(h, generator=gen) + 0.1
-    f = torch.cumsum(F.logsigmoid(torch.randn(bsz, h, L, generator=gen) + 1), 2) if with_f else None
+    """Seeded attention inputs: unit normal q/k/v/c/b, g from log-decays -softplus(N(-2, 1)), lambda on a grid in
+    [0.2, 1.4], F from log-forget gates logsigmoid(N(2, 1))."""
+    gen = torch.Generator().manual_seed(100 + seed)
+    normal = (lambda *shape: torch.randn(*shape, generator=gen))  # noqa: E731
+    q, k, v, c, b = normal(bsz, h, L, d), normal(bsz, h, L, d), normal(bsz, h, L, d), normal(bsz, h, L, s), \
+        normal(bsz, h, L, s)
+    g = torch.cumsum(-F.softplus(normal(bsz, h, L) - 2.0), 2)
+    lam = torch.linspace(0.2, 1.4, h)
+    f = torch.cumsum(F.logsigmoid(normal(bsz, h, L) + 2.0), 2) if with_f else None
     return q, k, v, c, b, g, lam, f
 
 
 @pytest.mark.parametrize("with_f", [False, True])
-@pytest.mark.parametrize("shape", [(1, 1, 1, 64, 32), (2, 3, 37, 16, 6), (1, 2, 130, 64, 32)])
+@pytest.mark.parametrize("shape", [(1, 1, 1, 64, 32), (1, 3, 41, 16, 8), (2, 2, 133, 64, 32), (1, 1, 90, 32, 2)])
 def test_torch_attention_against_dense_fp64(shape, with_f):
     bsz, h, L, d, s = shape
-    ins = _inputs(1, bsz, h, L, d, s, with_f)
-    ref = _dense64(*ins)
-    for block_q in (7, 256):
-        out = sisa_attention_torch(*ins, block_q=block_q)
-        assert out.dtype == torch.float32 and out.shape == ins[2].shape and rel_err(out, ref) < 1e-5
-    assert torch.equal(sisa_attention(*ins, impl="auto"), sisa_attention_torch(*ins))
+    ins = _inputs(7, bsz, h, L, d, s, with_f)
+    truth = _dense64(*ins)
+    outs = {bq: sisa_attention_torch(*ins, block_q=bq) for bq in (1, 13, 256)}
+    for bq, out in outs.items():
+        assert (out.dtype, out.shape) == (torch.float32, truth.shape), bq
+        assert rel_err(out, truth) < 1e-5, f"block_q {bq}: {rel_err(out, truth):.2e}"
+    assert torch.equal(sisa_attention(*ins, impl="auto"), outs[256])   # auto is the torch path on the CPU
 
 
 def test_torch_attention_bf16_inputs_and_gradients():
@@ -280,19 +300,20 @@ def test_torch_attention_bf16_inputs_and_gradients():
     assert all(t.grad is not None and torch.isfinite(t.grad).all() for t in ins)
 
 
-@pytest.mark.parametrize("block_q", [64, 512])
-def test_torch_attention_is_fp32_under_autocast(block_q):
-    ins = _inputs(3)
-    plain = sisa_attention_torch(*ins, block_q=block_q)
-    with torch.autocast("cpu", dtype=torch.bfloat16):
-        out = sisa_attention_torch(*ins, block_q=block_q)
-    assert out.dtype == torch.float32 and rel_err(out, _dense64(*ins)) < 1e-5
-    torch.testing.assert_close(out, plain, rtol=1e-6, atol=1e-6)
-    low = [t.bfloat16() for t in ins[:5]] + list(ins[5:])
-    plain = sisa_attention_torch(*low, block_q=block_q)
-    with torch.autocast("cpu", dtype=torch.bfloat16):
-        out = sisa_attention_torch(*low, block_q=block_q)
-    assert out.dtype == torch.bfloat16 and torch.equal(out, plain)
+@pytest.mark.parametrize("block_q", [48, 300])
+def test_torch_attention_ignores_autocast(block_q):
+    """The torch path turns autocast off inside: under CPU bf16 autocast it returns exactly what it returns without
+    it, for fp32 inputs (fp32 result, within 1e-5 of fp64) and for bf16 inputs (bf16 result)."""
+    for cast in (None, torch.bfloat16):
+        ins = list(_inputs(3, h=3, L=200))
+        if cast is not None:
+            ins[:5] = [t.to(cast) for t in ins[:5]]
+        eager = sisa_attention_torch(*ins, block_q=block_q)
+        with torch.autocast("cpu", dtype=torch.bfloat16):
+            under = sisa_attention_torch(*ins, block_q=block_q)
+        assert under.dtype == (cast or torch.float32) and torch.equal(under, eager)
+        if cast is None:
+            assert rel_err(under, _dense64(*ins)) < 1e-5
 
 
 def test_decode_rows_are_fp32_under_autocast():
@@ -362,6 +383,30 @@ def test_greedy_generation_equals_the_uncached_argmax_loop():
     assert one.shape == (9,) and torch.equal(model.generate(prompt[0], 0), prompt[0])
     with pytest.raises(ValueError):
         model.generate(prompt, 2, do_sample=True, top_k=0)
+
+
+def test_top_k_sampling_rule():
+    """Sampling masks every logit below the k-th largest to -inf and draws from the softmax over the full vocabulary
+    (src/sisa/generation.py:126-135): with the same seeded generator the draws equal that rule's draws; tokens tied at
+    the k-th value stay candidates; top_k >= V and top_k = None sample from the plain softmax."""
+    from sisa_amd.generation import _pick
+
+    def rule(logits, temperature, k, gen):
+        x = logits.float() / temperature
+        if k is not None and k < x.shape[-1]:
+            x = x.masked_fill(x < torch.topk(x, k, dim=-1).values[..., -1:], float("-inf"))
+        return torch.multinomial(torch.softmax(x, -1), 1, generator=gen).squeeze(-1)
+
+    logits = torch.randn(200, 97, generator=torch.Generator().manual_seed(5))
+    for k, temp in ((1, 1.0), (5, 0.7), (96, 1.3), (97, 1.0), (500, 1.0), (None, 0.9)):
+        got = _pick(logits, True, temp, k, torch.Generator().manual_seed(11))
+        want = rule(logits, temp, k, torch.Generator().manual_seed(11))
+        assert torch.equal(got, want), (k, temp)
+    tied = torch.zeros(4000, 6)
+    tied[:, 0] = 2.0                                  # one leader, then five logits tied at the 2nd value
+    draws = _pick(tied, True, 1.0, 2, torch.Generator().manual_seed(2))
+    assert set(draws.tolist()) == set(range(6))       # every tied token can be drawn
+    assert torch.equal(_pick(tied, False, 1.0, 2, None), torch.zeros(4000, dtype=torch.int64))
 
 
 def test_cache_slabs_grow_and_match_concatenation():

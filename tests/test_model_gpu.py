@@ -254,8 +254,15 @@ def test_hip_determinism_and_fused_ce():
     ref = _run(model, ids, "hip_fused")
     fused = _run(model, ids, "hip_fused", fused_ce=True)
     assert fused[1] is None and abs(fused[0] - ref[0]) < 1e-2
-    for grp, (g1, g2) in zip(_GROUPS, zip(_grouped(fused[2]).values(), _grouped(ref[2]).values())):
-        assert rel_err(g1, g2) < 2e-2, grp
+    # the fused-CE gradients judged like every HIP path: against the fp64 model, per parameter group, within the
+    # integration gate of the torch path (a direct comparison of two bf16 paths is ill-conditioned for groups whose
+    # entries nearly cancel, such as the four lambda_raw gradients)
+    loss64, _, grads64 = M64.loss_and_grads64(model, ids, ids)
+    t_loss, _, t_grads = _run(model, ids, "torch")
+    assert abs(fused[0] - loss64) <= max(2.0 * abs(t_loss - loss64), 2e-3)
+    ref_g, tor_g, fus_g = _grouped(grads64), _grouped(t_grads), _grouped(fused[2])
+    for grp in _GROUPS:
+        assert rel_err(fus_g[grp], ref_g[grp]) <= 3.0 * rel_err(tor_g[grp], ref_g[grp]) + 2e-3, grp
 
 
 def test_compile_common_logits_free_loss():
@@ -398,3 +405,56 @@ def test_deferred_residual_bitwise():
         assert torch.equal(res[True][0], res[False][0])
         bad = [n for n, g in res[True][1].items() if not torch.equal(g, res[False][1][n])]
         assert not bad, f"autocast={autocast}: gradients differ for {bad[:5]}"
+
+
+# ------------------------------------------------------------------------------------------------ on-disk formats
+def _paper_keys(state: dict) -> dict:
+    """The paper training code's key layout (flat attention keys, torch.compile's _orig_mod level on the compiled
+    submodules, DDP's module. prefix), the layout src/sisa/checkpoint.py:41-120 maps from."""
+    import re
+    flat, compiled = re.compile(r"^layers\.(\d+)\.attn\."), re.compile(r"^(layers\.\d+\.(?:attn_norm|ffn_norm|ffn)|final_norm)\.")
+    return {"module." + compiled.sub(r"\1._orig_mod.", flat.sub(r"layers.\1.", k)): v.detach().cpu().clone()
+            for k, v in state.items()}
+
+
+def _train_step(model, ids):
+    """One bf16-autocast training step on the fused HIP path: loss, logits and gradients, then one AdamW update."""
+    loss, logits, grads = _run(model, ids, "hip_fused")
+    torch.optim.AdamW(model.parameters(), lr=1e-3, weight_decay=0.1).step()
+    return loss, logits, grads, {n: p.detach().clone() for n, p in model.state_dict().items()}
+
+
+def test_checkpoints_load_into_the_hip_fused_model(tmp_path):
+    """save_pretrained -> from_pretrained (safetensors and pytorch_model.bin) and a paper-layout training checkpoint
+    through the weights-only loader (src/sisa/checkpoint.py:156-250), each put on the GPU under attn_impl="hip_fused":
+    the loss, logits, every gradient and the weights after one AdamW step are bitwise those of the model that was
+    saved; the loaded model passes the integration gates against the fp64 model."""
+    from sisa_amd import checkpoint as CK
+
+    src = tiny_model(seed=8, theta_scale=0.25, attn_impl="hip_fused").to(DEV)
+    ids = token_ids(2, 96, seed=8).to(DEV)
+    CK.save_pretrained(src, tmp_path / "safetensors")
+    CK.save_pretrained(src, tmp_path / "bin", safe_serialization=False)
+    torch.save({"model": _paper_keys(src.state_dict()), "step": 3}, tmp_path / "paper.pt")
+    loaders = {"safetensors": lambda: CK.from_pretrained(tmp_path / "safetensors"),
+               "bin": lambda: CK.from_pretrained(tmp_path / "bin"),
+               "paper": lambda: CK.load_paper_checkpoint(tmp_path / "paper.pt", attn_impl="hip_fused")}
+    fresh = loaders["safetensors"]().to(DEV)
+    loss64, logits64, grads64 = M64.loss_and_grads64(fresh, ids, ids)
+    t_loss, t_logits, t_grads = _run(fresh, ids, "torch")
+    h_loss, h_logits, h_grads = _run(fresh, ids, "hip_fused")
+    assert abs(h_loss - loss64) <= max(2.0 * abs(t_loss - loss64), 2e-3)
+    assert rel_err(h_logits, logits64) <= 2.0 * rel_err(t_logits, logits64) + 1e-3
+    ref_g, tor_g, hip_g = _grouped(grads64), _grouped(t_grads), _grouped(h_grads)
+    for grp in _GROUPS:
+        assert rel_err(hip_g[grp], ref_g[grp]) <= 3.0 * rel_err(tor_g[grp], ref_g[grp]) + 2e-3, grp
+    want = _train_step(src, ids)
+    for name, load in loaders.items():
+        model = load().to(DEV)
+        print(f"[checkpoint] {name}: attn_impl={model.config.attn_impl}", flush=True)
+        assert model.config.attn_impl == "hip_fused" and not model.training
+        model.train()
+        got = _train_step(model, ids)
+        assert got[0] == want[0] and torch.equal(got[1], want[1]), f"{name}: loss or logits differ"
+        assert all(torch.equal(got[2][n], want[2][n]) for n in want[2]), f"{name}: gradients differ"
+        assert all(torch.equal(got[3][n], want[3][n]) for n in want[3]), f"{name}: weights after the step differ"

@@ -45,14 +45,19 @@ def _backward(entry: str, ins: dict, exact: bool = True) -> list[torch.Tensor]:
     return [t for t in (dq, dk, dv, dc, db, dg, dF, dlam) if t is not None]
 
 
-@pytest.mark.parametrize("shapes", [((2, 8, 1500, 11), (1, 3, 200, 12)), ((1, 12, 4096, 13), (3, 2, 65, 14))])
+# the last case fills the scratch to its last element: B*H*L = SISA_NOALLOC_MAX_BHL at L = 1, where the fp64 dlambda
+# group sums (one per (batch, head, 16 rows)) are largest
+@pytest.mark.parametrize("shapes", [((2, 8, 1500, 11), (1, 3, 200, 12)), ((1, 12, 4096, 13), (3, 2, 65, 14)),
+                                    ((4096, 256, 1, 16), (1024, 64, 15, 17))])
 def test_noalloc_matches_workspace_entry(shapes):
     from sisa_amd.kernels import _lib
 
     _lib.load()
     for B, H, L, seed in shapes:        # the second call is smaller: the scratch holds the first call's rows
         print(f"[noalloc] B={B} H={H} L={L} seed={seed}", flush=True)
-        ins = R.make_attention_inputs(dict(B=B, H=H, L=L, dtype="bf16", seed=seed), DEV)
+        assert B * H * L <= NOALLOC_MAX_BHL
+        heads = [R.MIX12[h % 12] for h in range(H)]     # the judge's head mix, repeated past 12 heads
+        ins = R.make_attention_inputs(dict(B=B, H=H, L=L, dtype="bf16", seed=seed, heads=heads), DEV)
         got = _backward("sisa_attn_bwd_noalloc", ins)
         ref = _backward("sisa_attn_bwd", ins)
         names = ("dq", "dk", "dv", "dc", "db", "dg", "dF", "dlam")
