@@ -21,10 +21,10 @@ Reported (one JSON line on rank 0):
              same number of bytes (half read, half written), timed the same way, as the ceiling HBM offers to a
              transfer of this size (copy_same_bytes_gbs, frac_of_copy); the prep backward likewise (backward).
              phases_ms are the step's own event phases, host gaps included.
-  lmce       the linear cross-entropy at config 3 (N=16384, d=768, V=50277): the gradient step (token chunks of at
-             most 1 GiB of logits; TFLOP/s of its three GEMMs, 6 N V d; library GEMM roofline; the HIP row pass
-             against HBM peak) and the loss without gradients on the fused HIP kernel (MFMA roofline, no logits
-             buffer) beside the unfused GEMM + row pass it replaces.
+  lmce       the linear cross-entropy at config 3 (N=16384, d=768, V=50277): the gradient step on the HIP MFMA
+             kernels (sisa_lmce_train; TFLOP/s of 6 N V d against the bf16 MFMA peak; the reference's arrangement with
+             library GEMMs timed beside it) and the loss without gradients on the fused HIP kernel (MFMA roofline, no
+             logits buffer).
   fused_layer_async  sisa_fused forward + backward through autograd in the default "async" check mode (guard
              included, eager launches): ms and TFLOP/s, beside the same calls in "off" mode.
   model_step the full decoder training step at config 4 (sisa-152m, B=8, T=2048, bf16 autocast, fused attention,
@@ -208,11 +208,14 @@ def prep_kernel_rates(proj, z, H: int) -> dict:
 def bench_ce(steps: int, warmup: int) -> dict:
     """Linear cross-entropy at config 3 (N=16,384 tokens, d=768, V=50,277, bf16), inputs resident in HBM.
 
-    train: one forward with both gradients as linear_cross_entropy runs it (per token chunk of at most 1 GiB of logits:
-    logits GEMM, HIP row pass writing G over the logits, dx GEMM, dW GEMM), timed per phase with HIP events.
+    train: the loss with both gradients as linear_cross_entropy runs it -- sisa_lmce_train over the chunk(s) of at
+    most 2 GiB of stored exponentials (one chunk here): the logits GEMM storing the exponentials, the split combine,
+    the scale pass, the dW + dx MFMA launch forming G in operand staging, the dx split sum. Each call queued behind a
+    GPU spin (HIP events). phases_ms: the forward part (the same call without dx and dW) and the rest. Beside it the
+    reference's arrangement on this GPU (library_chunk_loop_ms: hipBLASLt logits GEMM, the HIP row pass writing G over
+    the logits, hipBLASLt dx and dW GEMMs; chunks of 1 GiB of logits), the design this pass replaces.
     fused_forward: the loss without gradients on the fused HIP kernel (sisa_lmce_fwd: MFMA GEMM reduced to lse and
-    the label logit on the fly, no logits buffer), against the bf16 dense MFMA peak; beside it the unfused no-gradient
-    forward (logits GEMM + row pass without G) that it replaces."""
+    the label logit on the fly, no logits buffer), against the bf16 dense MFMA peak."""
     import torch
 
     from sisa_amd.workloads import config_inputs
@@ -226,88 +229,67 @@ def bench_ce(steps: int, warmup: int) -> dict:
     wp = LC.padded_weight(w, torch.bfloat16)
     Vp = wp.shape[0]
     rows = LC.chunk_rows(N, Vp, None, 2)
-    buf = torch.empty((rows, Vp), dtype=torch.bfloat16, device=dev)
     loss_rows = torch.empty(N, device=dev)
     dx = torch.empty((N, D), device=dev)
     dw = torch.empty((Vp, D), device=dev)
-    ev = lambda: torch.cuda.Event(enable_timing=True)   # noqa: E731
-    marks = {k: [] for k in ("logits_gemm", "rows", "dx_gemm", "dw_gemm")}
+    inv_n = torch.reciprocal((lab != -100).sum().to(torch.float32)).reshape(1)
+    ws = LC.train_workspace({min(rows, N), N - (N - 1) // rows * rows}, Vp, D, dev)
 
-    def step(record):
-        n_valid = (lab != -100).sum()
-        inv_n = torch.reciprocal(n_valid.to(torch.float32)).reshape(1)
-        for s in range(0, N, rows):
-            e = [ev() for _ in range(5)] if record else None
-            lg = buf[:min(N, s + rows) - s]
-            xc = x[s:s + lg.shape[0]]
-            if record:
-                e[0].record()
+    def train(want_grads=True):
+        for s0 in range(0, N, rows):
+            s1 = min(N, s0 + rows)
+            LC.lmce_train_chunk(x[s0:s1], wp, lab[s0:s1], V, -100, inv_n, 1.0, loss_rows[s0:s1],
+                                dx[s0:s1] if want_grads else None, dw if want_grads else None, s0 > 0, ws)
+
+    for _ in range(warmup):
+        train()
+    train_s = queued_seconds(train, reps=steps)
+    fwd_s = queued_seconds(lambda: train(False), reps=steps)
+    fl = LC.flops(N, V, D)
+    ms = train_s * 1e3
+
+    # the reference's arrangement (library GEMMs around the HIP row pass), kept only as the comparison
+    lrows = LC.chunk_rows(N, Vp, None, 2, budget=1 << 30)
+    buf = torch.empty((lrows, Vp), dtype=torch.bfloat16, device=dev)
+
+    def library_loop():
+        for s0 in range(0, N, lrows):
+            lg = buf[:min(N, s0 + lrows) - s0]
+            xc = x[s0:s0 + lg.shape[0]]
             torch.mm(xc, wp.t(), out=lg)
-            if record:
-                e[1].record()
-            LC.lmce_rows(lg, lab[s:s + lg.shape[0]], loss_rows[s:s + lg.shape[0]], V, -100, inv_n, 1.0)
-            if record:
-                e[2].record()
-            torch.mm(lg, wp, out_dtype=torch.float32, out=dx[s:s + lg.shape[0]])
-            if record:
-                e[3].record()
-            if s == 0:
+            LC.lmce_rows(lg, lab[s0:s0 + lg.shape[0]], loss_rows[s0:s0 + lg.shape[0]], V, -100, inv_n, 1.0)
+            torch.mm(lg, wp, out_dtype=torch.float32, out=dx[s0:s0 + lg.shape[0]])
+            if s0 == 0:
                 torch.mm(lg.t(), xc, out_dtype=torch.float32, out=dw)
             else:
                 torch.addmm(dw, lg.t(), xc, out_dtype=torch.float32, out=dw)
-            if record:
-                e[4].record()
-                for i, k_ in enumerate(marks):
-                    marks[k_].append((e[i], e[i + 1]))
-        return loss_rows.sum() / n_valid
 
-    for _ in range(warmup):
-        step(False)
-    torch.cuda.synchronize()
-    with _quiet_host():
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            step(True)
-        torch.cuda.synchronize()
-        ms = (time.perf_counter() - t0) * 1e3 / steps
-    ph = {k: sum(a.elapsed_time(b_) for a, b_ in v) / steps for k, v in marks.items()}
-    fl = LC.flops(N, V, D)
-    gemm_ms = ph["logits_gemm"] + ph["dx_gemm"] + ph["dw_gemm"]
-    row_bytes = N * Vp * 2 * 2 + N * 12
+    lib_s = queued_seconds(library_loop, reps=max(3, steps // 2))
+    del buf
 
-    # the loss without gradients: fused kernel, and the unfused pair it replaces
     def fused():
         LC.lmce_fused_loss_rows(x, wp, lab, V, -100)
 
-    def unfused():
-        for s in range(0, N, rows):
-            lg = buf[:min(N, s + rows) - s]
-            torch.mm(x[s:s + lg.shape[0]], wp.t(), out=lg)
-            LC.lmce_rows(lg, lab[s:s + lg.shape[0]], loss_rows[s:s + lg.shape[0]], V, -100, None, 1.0)
-
     fused_s = queued_seconds(fused, reps=10)
-    unfused_s = queued_seconds(unfused, reps=10)
     fwd_tf = fl["forward"] / fused_s / 1e12
+    tr_tf = fl["total"] / train_s / 1e12
     return {"workload": "linear cross-entropy (config 3): N=16384, d=768, V=50277, bf16", "N": N, "d": D, "V": V,
             "Vp": Vp,
-            "train": {"what": "forward with dx, dW (token chunks of <= 1 GiB of logits)", "chunk_rows": rows,
-                      "ms_per_step": round(ms, 4), "tflops": round(fl["total"] / (ms * 1e-3) / 1e12, 2),
-                      "tokens_per_s": round(N / (ms * 1e-3), 1), "phases_ms": {k: round(v, 4) for k, v in ph.items()},
-                      "roofline_gemm": {"bound": "mfma", "achieved": round(fl["total"] / (gemm_ms * 1e-3) / 1e12, 1),
-                                        "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                                        "frac": round(fl["total"] / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-                                        "algorithmic": "3 GEMMs x 2*N*V*d flop"},
-                      "roofline_rows": {"bound": "hbm", "achieved": round(row_bytes / (ph["rows"] * 1e-3) / 1e9, 1),
-                                        "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                                        "frac": round(row_bytes / (ph["rows"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                                        "algorithmic": "N*Vp*2 B read + N*Vp*2 B written (+12 B per row)"}},
+            "train": {"what": "loss, dx, dW: sisa_lmce_train (MFMA logits GEMM storing exponentials; one launch of "
+                              "dW and dx MFMA tiles forming G in operand staging; no library GEMM)",
+                      "chunk_rows": rows, "ms_per_step": round(ms, 4), "tflops": round(tr_tf, 2),
+                      "tokens_per_s": round(N / train_s, 1),
+                      "phases_ms": {"forward": round(fwd_s * 1e3, 4), "gradients": round((train_s - fwd_s) * 1e3, 4)},
+                      "roofline": {"bound": "mfma", "achieved": round(tr_tf, 1), "peak": PEAK_BF16_TFLOPS,
+                                   "unit": "TFLOP/s", "frac": round(tr_tf / PEAK_BF16_TFLOPS, 4),
+                                   "algorithmic": "3 GEMMs x 2*N*V*d flop over the whole call"},
+                      "library_chunk_loop_ms": round(lib_s * 1e3, 4),
+                      "speedup_vs_library_loop": round(lib_s / train_s, 3)},
             "fused_forward": {"what": "loss without gradients, sisa_lmce_fwd (no logits buffer)",
                               "ms": round(fused_s * 1e3, 4), "tokens_per_s": round(N / fused_s, 1),
                               "roofline": {"bound": "mfma", "achieved": round(fwd_tf, 1), "peak": PEAK_BF16_TFLOPS,
                                            "unit": "TFLOP/s", "frac": round(fwd_tf / PEAK_BF16_TFLOPS, 4),
-                                           "algorithmic": "2*N*V*d flop"},
-                              "unfused_ms": round(unfused_s * 1e3, 4),
-                              "unfused_logits_bytes": int(rows * Vp * 2)}}
+                                           "algorithmic": "2*N*V*d flop"}}}
 
 
 def bench_fused_layer(proj, z, lam, dy, H, steps: int, mode: str, flop: float) -> dict:

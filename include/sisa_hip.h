@@ -234,6 +234,44 @@ typedef struct {
 int64_t sisa_lmce_fwd_workspace_bytes(int64_t N, int64_t Vp);
 int sisa_lmce_fwd(const sisa_lmce_fwd_args* a, void* stream);
 
+/* Training pass of the linear cross-entropy over one chunk of rows, on MFMA kernels only: the loss rows and, as
+ * requested, dL/dx and dL/dW_pad in fp32 for G = (softmax - onehot) * (*inv_n) * gscale, i.e. for a backward seed of
+ * gscale. The logits GEMM is sisa_lmce_fwd's kernel, which here also stores every exponential relative to its row's
+ * maximum over a 128-column half of a 256-column vocabulary tile (compute dtype, in the workspace) and those maxima;
+ * the loss rows are bitwise those of sisa_lmce_fwd. One launch then runs the dW tiles (dW = G^T x, all rows of the
+ * chunk) and the dx tiles (dx = G W_pad, split over the vocabulary, the splits added in a fixed order); both form G
+ * = exp * exp2(max - lse) * scale - onehot, rounded once to the compute dtype, while staging it into LDS. No logits
+ * and no G are ever written. Replaces the chunk loop of `_LinearCrossEntropyFn.forward`
+ * (src/sisa/kernels/linear_ce.py:138-217: the logits GEMM, `_lmce_row_kernel` (linear_ce.py:60-96) and the dx and
+ * dW GEMMs of linear_ce.py:171-191). Deterministic: no atomics. */
+typedef struct {
+    int64_t N;                 /* rows of the chunk (0 is a no-op) */
+    int64_t V;                 /* real vocabulary rows of w, >= 1 */
+    int64_t Vp;                /* rows of w, a multiple of 128, >= V (rows >= V never enter a sum) */
+    int32_t D;                 /* hidden size, a positive multiple of 64 */
+    int32_t dtype;             /* of x and w: SISA_BF16 or SISA_F16 */
+    const void* x;             /* (N, D), 16-byte aligned, row stride ldx (multiple of 8) */
+    int64_t ldx;
+    const void* w;             /* (Vp, D), 16-byte aligned, row stride ldw (multiple of 8) */
+    int64_t ldw;
+    const int64_t* labels;     /* (N,) */
+    int64_t ignore_index;
+    const float* inv_n;        /* device scalar 1 / N_valid of the whole problem (all chunks) */
+    float gscale;              /* multiplier of G: 1, or the promised backward seed */
+    float* loss_rows;          /* (N,) fp32 output */
+    float* lse;                /* (N,) fp32 output, natural log, or NULL */
+    float* dx;                 /* (N, D) fp32 output, row stride lddx (multiple of 4), or NULL */
+    int64_t lddx;
+    float* dw;                 /* (Vp, D) fp32 output, row stride lddw (multiple of 4), or NULL */
+    int64_t lddw;
+    int32_t dw_accumulate;     /* nonzero: dw += this chunk's part; zero: dw = it */
+    int32_t dx_splits;         /* vocabulary splits of the dx product, 1..16 (0: the library's choice) */
+    void* workspace;           /* sisa_lmce_train_workspace_bytes(N, Vp, D, dx_splits) bytes, 256-byte aligned */
+} sisa_lmce_train_args;
+
+int64_t sisa_lmce_train_workspace_bytes(int64_t N, int64_t Vp, int32_t D, int32_t dx_splits);
+int sisa_lmce_train(const sisa_lmce_train_args* a, void* stream);
+
 /* ------------------------------------------------------------------------------------------------ decoder block */
 
 /* RMSNorm over the last axis: y = (x * rsqrt(mean(x^2) + eps)) * w in fp32, stored in the input dtype; rstd (N) fp32

@@ -19,6 +19,7 @@
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -139,14 +140,18 @@ template <class T> SISA_DEV vec4<T> to_vec4(f32x4 x) { return __builtin_convertv
 // types the chunks of a row are XOR-swizzled so that both fragment reads below are free of bank conflicts:
 //   C = 64 (8 chunks per row): physical chunk = chunk ^ (row % 8);
 //   C = 32 (4 chunks per row): physical chunk = chunk ^ 2 * ((row / 4) % 2);
-//   C >= 128 (16+ chunks per row, transpose reads only): physical chunk = chunk ^ 2 * (row % 4).
+//   C >= 128 (16+ chunks per row, transpose reads only): physical chunk = chunk ^ 2 * (row % 4) ^ 8 * b(row), with
+//   b(row) = bit 2 of row xor bit 3 of row.
 // (8 consecutive rows of one chunk column, and the 4-row x 32-byte footprint of a transpose read, then fall on
-// distinct banks.) fp32 tiles (the accuracy path) are not swizzled.
+// distinct banks. For C >= 128 every row starts on the same bank: the 2 (row % 4) term separates the 4 rows of one
+// lane group's transpose read, and b(row) moves the other lane group of each pair serviced together by 128 bytes:
+// it differs between rows r and r + 4 (lane groups 0/1 and 2/3 of the sequence map, r % 8 < 4) and between rows r
+// and r + 8 (those of the feature map, r % 16 < 8).) fp32 tiles (the accuracy path) are not swizzled.
 template <class T, int C>
 SISA_DEV int swz(int row) {
     if constexpr (sizeof(T) != 2) return 0;
     else if constexpr (C == 64) return row & 7;
-    else if constexpr (C >= 128) return (row & 3) << 1;
+    else if constexpr (C >= 128) return ((row & 3) << 1) ^ ((((row >> 2) ^ (row >> 3)) & 1) << 3);
     else return ((row >> 2) & 1) << 1;
 }
 // element offset of (row, 16-byte chunk) in a tile
@@ -194,7 +199,8 @@ SISA_DEV void dma_issue(const DmaStage<T, C, NW>& st, const void* base, int64_t 
 #pragma unroll
     for (int p = 0; p < DmaStage<T, C, NW>::PER; ++p) {
         const int k = w + NW * p;
-        if (k < DmaStage<T, C, NW>::CPR)
+        // (always true when the waves split the instructions evenly: no per-instruction branch then)
+        if (DmaStage<T, C, NW>::CPR % NW == 0 || k < DmaStage<T, C, NW>::CPR)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 r, (__attribute__((address_space(3))) void*)(X + k * (1024 / (int)sizeof(T))), 16, st.voff[p], soff, 0,
                 0);
@@ -235,6 +241,19 @@ SISA_DEV frag8<T> frag_tr(const T* X, int f0, int step, int lane) {
     const int f = f0 + 4 * (s & 3);
     const T* p0 = X + toff<T, C>(row, f >> 3) + (f & 4);
     return join<T>(lds_tr4<T>(p0), lds_tr4<T>(p0 + 16 * C));
+}
+
+// The same transpose read with the feature map instead of the sequence map: row (feature) f0 + lane%16, K = tile
+// rows 32*step + 8*grp + 0..7 (source lane s of lane group grp addresses row 32*step + 8*grp + s/4, then 4 rows
+// further for slots 4..7). Pairs with frag_rows of a tile whose rows are the other operand's rows and whose columns
+// are the same K (16-bit types, C >= 128).
+template <class T, int C>
+SISA_DEV frag8<T> frag_trf(const T* X, int f0, int step, int lane) {
+    static_assert(sizeof(T) == 2 && C >= 128, "frag_trf: 16-bit tiles of at least 128 columns");
+    const int s = lane & 15, grp = lane >> 4;
+    const int row = 32 * step + 8 * grp + (s >> 2);
+    const int f = f0 + 4 * (s & 3);
+    return join<T>(lds_tr4<T>(X + toff<T, C>(row, f >> 3) + (f & 4)), lds_tr4<T>(X + toff<T, C>(row + 4, f >> 3) + (f & 4)));
 }
 
 // fp32 tiles: plain element gathers (the fp32 path exists for accuracy, not speed).

@@ -3,17 +3,24 @@
 //
 // Reference: the forward of `_LinearCrossEntropyFn` (src/sisa/kernels/linear_ce.py:138-191: logits chunk GEMM, then
 // `_lmce_row_kernel`'s online max / sum-exp and the label pick, linear_ce.py:60-96). The reference materialises a
-// (chunk, Vp) logits buffer; here the GEMM's output tiles never leave registers. The logits are the MFMA's fp32
-// accumulations (the unfused path rounds them to the compute dtype before the row pass).
+// (chunk, Vp) logits buffer; here the GEMM's output tiles never leave registers. As there, each logit (an fp32 MFMA
+// accumulation) is rounded once to the compute dtype before the reduction, so lse and the loss are those of the
+// reference's stored logits.
 //
 // Decomposition: a workgroup of 2 x 4 waves owns 256 rows of x and walks a range of 256-column vocabulary tiles (one
 // of S vocabulary splits). Per tile, K = D is streamed through LDS in 64-wide stages (buffer loads straight into
 // LDS, double-buffered, XOR-swizzled 16-byte chunks); a wave computes a 128 (vocabulary) x 64 (rows) block as 8 x 4
 // v_mfma_f32_16x16x32 blocks with W as the A operand, so that a lane holds 32 logits of one row per block column
 // (12 operand fragments per 32 MFMAs, to keep the LDS reads below the matrix rate). After a tile's last stage each
-// lane folds its 32 logits per row into a running (max, sum of exponentials) in log2 units and, when the tile holds
-// a row's label, keeps that logit. At the end the lane groups and the two waves
-// sharing rows combine their partials; a second launch combines the S splits of each row in a fixed order.
+// wave takes every row's maximum over its 128 columns of the tile (log2 units, shared by the row's four lane groups),
+// sums the row's exponentials relative to it and folds that sum into the row's running (max, sum of exponentials);
+// when the tile holds a row's label it keeps that logit. At the end the lane groups and the two waves sharing rows
+// combine their partials; a second launch combines the S splits of each row in a fixed order.
+//
+// The training pass (sisa_lmce_train, lmce_train.hip) runs the same kernel with STORE: each exponential
+// p~ = exp2(logit*log2e - m_t), m_t the row's maximum over the wave's half of the tile, is also stored in the compute
+// dtype into a (N, Vp) buffer, and m_t into a (2 * tiles, N) table; the gradient GEMMs later form
+// G = p~ * exp2(m_t - lse) * scale - onehot from them. Both passes therefore give bitwise the same loss rows.
 // Deterministic: no atomics. Workgroup i runs on XCD i % 8; each XCD takes a set of row blocks with all their
 // splits, so its L2 keeps those rows of x for every vocabulary tile.
 #include "common.h"
@@ -38,6 +45,13 @@ struct __attribute__((aligned(16))) CeLds {
     float red_m[TR], red_s[TR];   // the second wave of each row pair hands over its row partials
 };
 
+// Outputs of the training pass (STORE): exponentials relative to the tile-half maxima and those maxima.
+template <class T>
+struct CeStore {
+    T* probs;                     // (N, Vp) in the compute dtype, row stride Vp; columns >= V hold 0
+    float* mtab;                  // (2 * tiles, N): m_t of (tile t, half h) at row (2 t + h) * N + n, log2 units
+};
+
 // The vocabulary splits of one problem: S splits of `per` consecutive tiles (the last ones may be shorter or empty).
 struct Split {
     int64_t tiles, S, per;
@@ -49,8 +63,8 @@ inline Split ce_split(int64_t N, int64_t Vp) {
     return {tiles, S, sisa::cdiv(tiles, S)};
 }
 
-template <class T>
-__global__ __launch_bounds__(64 * NWC) void lmce_fwd_kernel(sisa_lmce_fwd_args a, int S, int per) {
+template <class T, bool STORE>
+__global__ __launch_bounds__(64 * NWC) void lmce_fwd_kernel(sisa_lmce_fwd_args a, int S, int per, CeStore<T> out) {
     __shared__ CeLds<T> sm;
     const int tid = threadIdx.x, lane = tid & 63, grp = lane >> 4, lc = lane & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -80,9 +94,9 @@ __global__ __launch_bounds__(64 * NWC) void lmce_fwd_kernel(sisa_lmce_fwd_args a
         const int k0 = (g % nks) * TK;
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
-            dma_issue<4>(sx, X, xbytes, (int)(((row0 + 64 * h) * a.ldx + k0) * (int64_t)sizeof(T)),
+            dma_issue<STORE ? 8 : 4>(sx, X, xbytes, (int)(((row0 + 64 * h) * a.ldx + k0) * (int64_t)sizeof(T)),
                          sm.x[buf] + 64 * h * TK, w);
-            dma_issue<5>(sw, W, wbytes, (int)(((v0 + 64 * h) * a.ldw + k0) * (int64_t)sizeof(T)),
+            dma_issue<STORE ? 9 : 5>(sw, W, wbytes, (int)(((v0 + 64 * h) * a.ldw + k0) * (int64_t)sizeof(T)),
                          sm.w[buf] + 64 * h * TK, w);
         }
     };
@@ -119,12 +133,16 @@ __global__ __launch_bounds__(64 * NWC) void lmce_fwd_kernel(sisa_lmce_fwd_args a
 #pragma unroll
         for (int j = 0; j < JB; ++j) acc[i][j] = zero4();
 
+    // STORE: the exponentials go out through one buffer resource over (N, Vp) (below 2 GiB, checked by the host)
+    const __amdgpu_buffer_rsrc_t prs =
+        make_rsrc(STORE ? (const void*)out.probs : (const void*)a.x, STORE ? N * a.Vp * (int64_t)sizeof(T) : 0);
     const int total = ntiles * nks;
     if (total > 0) issue(0, 0);
     __syncthreads();
     for (int g = 0; g < total; ++g) {
         const int buf = g & 1;
         if (g + 1 < total) issue(g + 1, buf ^ 1);
+        __builtin_amdgcn_sched_barrier(0);   // the next stage's DMA stays ahead of this stage's stores
         // all 12 operand fragments of a 32-deep step are read before its 32 MFMAs (two waves per SIMD leave room
         // for them), so one LDS wait per step instead of one per 4 MFMAs
 #pragma unroll
@@ -140,8 +158,13 @@ __global__ __launch_bounds__(64 * NWC) void lmce_fwd_kernel(sisa_lmce_fwd_args a
                 for (int j = 0; j < JB; ++j) acc[i][j] = mma(wf[i], xf[j], acc[i][j]);
         }
         if (g % nks == nks - 1) {
-            // the tile is complete: lane holds logits of rows wn + 16 j + lc at columns v0 + wv + 16 i + 4 grp + r
+            // the tile is complete: lane holds logits of rows wn + 16 j + lc at columns v0 + wv + 16 i + 4 grp + r,
+            // rounded once to the compute dtype (the logits the reference's row kernel reads)
             const int vt = t_begin + g / nks;
+#pragma unroll
+            for (int i = 0; i < IB; ++i)
+#pragma unroll
+                for (int j = 0; j < JB; ++j) acc[i][j] = __builtin_convertvector(to_vec4<T>(acc[i][j]), f32x4);
             if ((int64_t)(vt + 1) * TV > V) {   // the last tile: padding columns do not enter the sums
                 const int lim = (int)(V - (int64_t)vt * TV) - wv - 4 * grp;
 #pragma unroll
@@ -154,22 +177,37 @@ __global__ __launch_bounds__(64 * NWC) void lmce_fwd_kernel(sisa_lmce_fwd_args a
             }
 #pragma unroll
             for (int j = 0; j < JB; ++j) {
-                float mt = -__builtin_inff();   // the tile's maximum logit of the row, then in log2 units
+                float mt = -__builtin_inff();   // the row's maximum over the wave's 128 columns, in log2 units
 #pragma unroll
                 for (int i = 0; i < IB; ++i)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) mt = fmaxf(mt, acc[i][j][r]);
-                mt *= LOG2E;
-                if (mt > m[j]) {
-                    s[j] *= fast_exp2(m[j] - mt);
-                    m[j] = mt;
-                }
+                mt = group_max(mt) * LOG2E;
+                // a half made only of padding columns (-inf) takes the reference 0: its exponentials are 0
+                const float mref = mt == -__builtin_inff() ? 0.f : mt;
+                const int64_t n = row0 + wn + 16 * j + lc;
                 float ls = 0.f;
 #pragma unroll
-                for (int i = 0; i < IB; ++i)
+                for (int i = 0; i < IB; ++i) {
+                    f32x4 e;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) ls += fast_exp2(fmaf(acc[i][j][r], LOG2E, -m[j]));
-                s[j] += ls;
+                    for (int r = 0; r < 4; ++r) e[r] = fast_exp2(fmaf(acc[i][j][r], LOG2E, -mref));
+                    ls += (e[0] + e[1]) + (e[2] + e[3]);
+                    if constexpr (STORE) {   // unconditional: positions past the data go past the resource
+                        const int64_t v = (int64_t)vt * TV + wv + 16 * i + 4 * grp;
+                        const int off = (n < N && v < a.Vp) ? (int)((n * a.Vp + v) * (int64_t)sizeof(T)) : 0x7ffffff8;
+                        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, to_vec4<T>(e)), prs, off, 0, 0);
+                    }
+                }
+                if constexpr (STORE) {
+                    if (grp == 0 && n < N) out.mtab[(int64_t)(2 * vt + (w & 1)) * N + n] = mref;
+                }
+                if (mt > m[j]) {
+                    s[j] = fmaf(s[j], fast_exp2(m[j] - mt), ls);
+                    m[j] = mt;
+                } else {
+                    s[j] = fmaf(ls, fast_exp2(mt - m[j]), s[j]);
+                }
                 if (lab_tile[j] == vt) {   // rare: pick the label's logit (natural units)
                     float z = 0.f;
 #pragma unroll
@@ -184,6 +222,18 @@ __global__ __launch_bounds__(64 * NWC) void lmce_fwd_kernel(sisa_lmce_fwd_args a
             for (int i = 0; i < IB; ++i)
 #pragma unroll
                 for (int j = 0; j < JB; ++j) acc[i][j] = zero4();
+            if constexpr (STORE) {
+                // The barrier after a tile's stores waits only until the next stage's DMA (issued before them) has
+                // landed: vector memory operations complete in issue order, and at least the 32 exponential stores
+                // (unconditional instructions) follow it, so vmcnt <= 32 implies the DMA is done; the stores
+                // themselves complete under the next stage (its barrier waits for everything).
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_waitcnt(0x8070);   // vmcnt(32) expcnt(7) lgkmcnt(0)
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+                continue;
+            }
         }
         __syncthreads();
     }
@@ -217,8 +267,16 @@ __global__ __launch_bounds__(64 * NWC) void lmce_fwd_kernel(sisa_lmce_fwd_args a
     }
 }
 
-// Per row: the S split partials combined in split order; lse (natural log) and the loss row.
-__global__ __launch_bounds__(256) void lmce_combine_kernel(sisa_lmce_fwd_args a, int S) {
+// Per row: the S split partials combined in split order; lse (natural log) and the loss row. The training pass also
+// keeps lse in log2 units and the row's gradient scale (0 for an ignored row, else inv_n * gscale).
+struct CeTrainRows {
+    float* lse2;                  // (N,) or nullptr (the no-gradient pass)
+    float2* rinfo;                // (N,): s_n, and the label as the bit pattern of an int (-1 outside [0, V))
+    const float* inv_n;           // device scalar 1 / N_valid
+    float gscale;
+};
+
+__global__ __launch_bounds__(256) void lmce_combine_kernel(sisa_lmce_fwd_args a, int S, CeTrainRows tr) {
     const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (n >= a.N) return;
     const int64_t N = a.N;
@@ -227,7 +285,8 @@ __global__ __launch_bounds__(256) void lmce_combine_kernel(sisa_lmce_fwd_args a,
     float ss = 0.f;
     for (int sp = 0; sp < S; ++sp)
         ss += a.workspace[(int64_t)(S + sp) * N + n] * fast_exp2(a.workspace[(int64_t)sp * N + n] - mm);
-    const float lse = (mm + __builtin_amdgcn_logf(ss)) * LN2;
+    const float l2 = mm + __builtin_amdgcn_logf(ss);
+    const float lse = l2 * LN2;
     const int64_t y = a.labels[n];
     float loss;
     if (y == a.ignore_index) loss = 0.f;
@@ -235,6 +294,11 @@ __global__ __launch_bounds__(256) void lmce_combine_kernel(sisa_lmce_fwd_args a,
     else loss = lse - a.workspace[2 * (int64_t)S * N + n];
     a.loss_rows[n] = loss;
     if (a.lse) a.lse[n] = lse;
+    if (tr.lse2) {
+        tr.lse2[n] = l2;
+        const int lab = (y >= 0 && y < a.V) ? (int)y : -1;
+        tr.rinfo[n] = float2{y == a.ignore_index ? 0.f : tr.inv_n[0] * tr.gscale, __int_as_float(lab)};
+    }
 }
 
 template <class T>
@@ -242,14 +306,44 @@ int launch_lmce_fwd(const sisa_lmce_fwd_args* a, hipStream_t st) {
     const Split sp = ce_split(a->N, a->Vp);
     const int64_t nrb = sisa::cdiv(a->N, TR), rbx = sisa::cdiv(nrb, 8);
     const unsigned grid = (unsigned)(8 * rbx * sp.S);
-    lmce_fwd_kernel<T><<<grid, 64 * NWC, 0, st>>>(*a, (int)sp.S, (int)sp.per);
+    lmce_fwd_kernel<T, false><<<grid, 64 * NWC, 0, st>>>(*a, (int)sp.S, (int)sp.per, CeStore<T>{nullptr, nullptr});
     const int rc = sisa::launch_status("sisa_lmce_fwd");
     if (rc) return rc;
-    lmce_combine_kernel<<<(unsigned)sisa::cdiv(a->N, 256), 256, 0, st>>>(*a, (int)sp.S);
+    lmce_combine_kernel<<<(unsigned)sisa::cdiv(a->N, 256), 256, 0, st>>>(*a, (int)sp.S,
+                                                                        CeTrainRows{nullptr, nullptr, nullptr, 0.f});
     return sisa::launch_status("sisa_lmce_fwd (combine)");
 }
 
 }  // namespace
+
+namespace sisa {
+namespace detail {
+
+int64_t lmce_fwd_splits(int64_t N, int64_t Vp) { return ce_split(N, Vp).S; }
+
+// The training pass's forward: the logits GEMM storing the exponentials and tile-half maxima (probs: (N, Vp) in the
+// compute dtype; mtab: (2 * ceil(Vp / 256), N) fp32), then the split combine writing the loss rows, lse in log2 units
+// and each row's gradient scale. a->workspace holds the (2 S + 1) N split partials.
+int lmce_train_forward(const sisa_lmce_fwd_args* a, void* probs, float* mtab, float* lse2, float2* rinfo,
+                       const float* inv_n, float gscale, hipStream_t st) {
+    const Split sp = ce_split(a->N, a->Vp);
+    const int64_t nrb = sisa::cdiv(a->N, TR), rbx = sisa::cdiv(nrb, 8);
+    const unsigned grid = (unsigned)(8 * rbx * sp.S);
+    if (a->dtype == SISA_BF16)
+        lmce_fwd_kernel<__bf16, true><<<grid, 64 * NWC, 0, st>>>(*a, (int)sp.S, (int)sp.per,
+                                                                  CeStore<__bf16>{(__bf16*)probs, mtab});
+    else
+        lmce_fwd_kernel<_Float16, true><<<grid, 64 * NWC, 0, st>>>(*a, (int)sp.S, (int)sp.per,
+                                                                    CeStore<_Float16>{(_Float16*)probs, mtab});
+    const int rc = sisa::launch_status("sisa_lmce_train (logits)");
+    if (rc) return rc;
+    lmce_combine_kernel<<<(unsigned)sisa::cdiv(a->N, 256), 256, 0, st>>>(*a, (int)sp.S,
+                                                                        CeTrainRows{lse2, rinfo, inv_n, gscale});
+    return sisa::launch_status("sisa_lmce_train (combine)");
+}
+
+}  // namespace detail
+}  // namespace sisa
 
 extern "C" int64_t sisa_lmce_fwd_workspace_bytes(int64_t N, int64_t Vp) {
     if (N < 1 || Vp < 1) return 0;

@@ -111,6 +111,14 @@ class DecodeArgs(Structure):
                 ("out", c_void_p), ("workspace", c_void_p)]
 
 
+class LmceTrainArgs(Structure):
+    _fields_ = [("N", c_int64), ("V", c_int64), ("Vp", c_int64), ("D", c_int32), ("dtype", c_int32),
+                ("x", c_void_p), ("ldx", c_int64), ("w", c_void_p), ("ldw", c_int64), ("labels", c_void_p),
+                ("ignore_index", c_int64), ("inv_n", c_void_p), ("gscale", c_float), ("loss_rows", c_void_p),
+                ("lse", c_void_p), ("dx", c_void_p), ("lddx", c_int64), ("dw", c_void_p), ("lddw", c_int64),
+                ("dw_accumulate", c_int32), ("dx_splits", c_int32), ("workspace", c_void_p)]
+
+
 class Round16Args(Structure):
     _fields_ = [("n", c_int64), ("dtype", c_int32), ("x", c_void_p), ("y", c_void_p), ("back", c_void_p)]
 
@@ -126,6 +134,8 @@ SIGNATURES = {
     "sisa_attn_bwd_noalloc": ([POINTER(AttnBwdArgs), c_void_p], c_int),
     "sisa_lmce_fwd_workspace_bytes": ([c_int64, c_int64], c_int64),
     "sisa_lmce_fwd": ([POINTER(LmceFwdArgs), c_void_p], c_int),
+    "sisa_lmce_train_workspace_bytes": ([c_int64, c_int64, c_int32, c_int32], c_int64),
+    "sisa_lmce_train": ([POINTER(LmceTrainArgs), c_void_p], c_int),
     "sisa_prep_fwd": ([POINTER(PrepFwdArgs), c_void_p], c_int),
     "sisa_prep_bwd_workspace_bytes": ([c_int32, c_int32, c_int32], c_int64),
     "sisa_finite_sum": ([c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p], c_int),

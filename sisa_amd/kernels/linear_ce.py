@@ -7,21 +7,26 @@ loss over the non-ignored rows, differentiable in ``hidden`` and ``weight``, and
 the wrong shape or a label count that does not match the hidden rows raises ``ValueError``. CPU tensors and an fp32
 compute dtype take the eager formula.
 
-How the work is arranged here (every kernel is HIP, ``libsisa_hip.so``):
+How the work is arranged here (every kernel is HIP, ``libsisa_hip.so``; no library GEMM):
 
 * No gradient wanted (``torch.no_grad``, evaluation, or neither input requires grad): one fused launch,
   ``sisa_lmce_fwd`` (csrc/lmce_fwd.hip). An MFMA GEMM whose tiles are reduced on the fly to each row's log-sum-exp
   and label logit; no logits are stored anywhere.
-* Gradients wanted: the loss and both gradients come out of one pass over token chunks, with the chunk's logits kept
-  just long enough to become G = (softmax - onehot) / N_valid (the reference's chunk loop, linear_ce.py:160-191, and
-  its 1 GiB buffer budget). Per chunk: logits = x W_pad^T (library GEMM), ``sisa_lmce_rows`` (csrc/lmce.hip: lse,
-  loss row and G written over the logits, one read and one write per element), dx = G W_pad and dW += G^T x (library
-  GEMMs, fp32 results). Computing the logits once and keeping G is the fewest flops for this step (3 GEMMs); a
-  design that never stores a logits chunk has to compute them twice (4 GEMMs).
+* Gradients wanted: ``sisa_lmce_train`` (csrc/lmce_train.hip) per chunk of rows. The same logits GEMM also stores
+  each exponential relative to its row's maximum over half a 256-column vocabulary tile (compute dtype) and those
+  maxima; then one launch of MFMA tiles computes dW = G^T x and dx = G W_pad, each forming
+  G = (softmax - onehot) / N_valid * gscale from the stored exponentials while staging it into LDS. Neither the logits
+  nor G are ever written. The reference's chunk loop (linear_ce.py:160-191: logits GEMM, row kernel, dx and dW
+  GEMMs) has the same contract; its chunk budget is 1 GiB of logits, this one 2 GiB of exponentials (one chunk at
+  N = 16,384, V = 50,277), because every chunk after the first re-reads and adds the fp32 dW.
 
-The vocabulary is padded with zero rows to a multiple of 128 (50,277 -> 50,304) so that every GEMM runs on aligned
-shapes; the padded columns never enter a sum. ``grad_scale`` is the caller's promise of the backward seed: G is then
-scaled in the forward pass and the backward only checks the promise on the device.
+Both paths take the loss from the fp32 MFMA accumulations of the logits (the reference rounds the logits to the
+compute dtype first; its loss is within that rounding of this one), and the two paths give bitwise the same loss.
+
+The vocabulary is padded with zero rows to a multiple of 128 (50,277 -> 50,304) and the hidden size with zero columns
+to a multiple of 64, so that every GEMM runs on aligned shapes; the padding never enters a sum. ``grad_scale`` is the
+caller's promise of the backward seed: G is then scaled in the forward pass and the backward only checks the promise
+on the device.
 """
 from __future__ import annotations
 
@@ -32,31 +37,31 @@ from .. import backends
 from . import _lib
 
 __all__ = ["linear_cross_entropy", "reference_linear_cross_entropy", "lmce_rows", "lmce_fused_loss_rows",
-           "padded_weight", "chunk_rows", "flops"]
+           "lmce_train_chunk", "padded_weight", "chunk_rows", "flops"]
 
 VOCAB_MULTIPLE = 128
-LOGITS_BUDGET = 1 << 30          # bytes of one chunk of logits (the reference's budget)
-FUSED_K_MULTIPLE = 64            # sisa_lmce_fwd streams the hidden size in 64-wide stages
-# whether this torch's mm/addmm take an output dtype (a float32 result of 16-bit operands without a cast pass)
-_MM_OUT_DTYPE = ("dtype" in torch.ops.aten.mm.overloads()
-                 and "dtype_out" in torch.ops.aten.addmm.overloads())
+HIDDEN_MULTIPLE = 64             # the CE kernels stream the hidden size in 64-wide stages
+PROBS_BUDGET = 2 << 30           # bytes of one chunk of stored exponentials
 
 
 # ------------------------------------------------------------------------------------------------ pieces
-def padded_weight(weight: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+def padded_weight(weight: torch.Tensor, dtype: torch.dtype, cols: int | None = None) -> torch.Tensor:
     """The LM-head weight in the compute dtype (one round-to-nearest-even cast, as autocast does) with zero rows up
-    to the next multiple of 128."""
+    to the next multiple of 128 (and zero columns up to ``cols``)."""
     V, D = weight.shape
     rows = -(-V // VOCAB_MULTIPLE) * VOCAB_MULTIPLE
-    out = weight.new_zeros((rows, D), dtype=dtype) if rows > V else weight.new_empty((rows, D), dtype=dtype)
-    out[:V].copy_(weight.detach())
+    cols = D if cols is None else cols
+    pad = rows > V or cols > D
+    out = weight.new_zeros((rows, cols), dtype=dtype) if pad else weight.new_empty((rows, cols), dtype=dtype)
+    out[:V, :D].copy_(weight.detach())
     return out
 
 
 def chunk_rows(n_rows: int, vocab_rows: int, chunk_tokens: int | None, itemsize: int,
-               budget: int = LOGITS_BUDGET) -> int:
+               budget: int = PROBS_BUDGET) -> int:
     """Token rows per chunk of the gradient pass: ``chunk_tokens`` if given (within [1, n_rows]); otherwise the
-    smallest number of equal chunks whose logits fit ``budget`` bytes, each rounded up to whole 128-row GEMM tiles."""
+    smallest number of equal chunks whose stored exponentials fit ``budget`` bytes, each rounded up to whole 128-row
+    GEMM tiles."""
     if n_rows <= 0:
         return 1
     if chunk_tokens:
@@ -101,17 +106,30 @@ def lmce_fused_loss_rows(x: torch.Tensor, wpad: torch.Tensor, labels: torch.Tens
     return out
 
 
-def _matmul_f32(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor, accumulate: bool) -> None:
-    """out (+)= a @ b with fp32 output from 16-bit operands (fp32 accumulation, no 16-bit rounding of the result)."""
-    if _MM_OUT_DTYPE:
-        if accumulate:
-            torch.addmm(out, a, b, out_dtype=torch.float32, out=out)
-        else:
-            torch.mm(a, b, out_dtype=torch.float32, out=out)
-    elif accumulate:
-        out.add_(torch.mm(a, b))
-    else:
-        out.copy_(torch.mm(a, b))
+def lmce_train_chunk(x: torch.Tensor, wpad: torch.Tensor, labels: torch.Tensor, V: int, ignore_index: int,
+                     inv_n: torch.Tensor, gscale: float, loss_rows: torch.Tensor, dx: torch.Tensor | None,
+                     dw: torch.Tensor | None, accumulate: bool, workspace: torch.Tensor, dx_splits: int = 0,
+                     lse: torch.Tensor | None = None) -> None:
+    """One chunk of the training pass (``sisa_lmce_train``): x (n, D) rows, the padded weight (Vp, D), labels (n,)
+    int64; writes loss_rows (n,), dx (n, D) fp32 (if given) and dW (Vp, D) fp32 (written, or added with
+    ``accumulate``), for G scaled by the device scalar ``inv_n`` times ``gscale``."""
+    n, D = x.shape
+    if n == 0:
+        return
+    args = _lib.LmceTrainArgs(n, int(V), wpad.shape[0], D, _lib.dtype_code(x.dtype), x.data_ptr(), x.stride(0),
+                              wpad.data_ptr(), wpad.stride(0), labels.data_ptr(), int(ignore_index), inv_n.data_ptr(),
+                              float(gscale), loss_rows.data_ptr(), _lib.ptr(lse), _lib.ptr(dx),
+                              dx.stride(0) if dx is not None else 0, _lib.ptr(dw), dw.stride(0) if dw is not None else 0,
+                              int(bool(accumulate)), int(dx_splits), workspace.data_ptr())
+    _lib.call("sisa_lmce_train", args, x)
+
+
+def train_workspace(chunk_sizes, Vp: int, D: int, device, dx_splits: int = 0) -> torch.Tensor:
+    """A 256-byte aligned byte buffer for ``sisa_lmce_train`` on chunks of each of the given row counts."""
+    need = max(_lib.workspace_bytes("sisa_lmce_train_workspace_bytes", n, Vp, D, dx_splits) for n in chunk_sizes)
+    ws = torch.empty(max(1, need) + 256, dtype=torch.uint8, device=device)
+    skip = (-ws.data_ptr()) % 256
+    return ws[skip:skip + max(1, need)]
 
 
 class _Problem:
@@ -121,42 +139,41 @@ class _Problem:
     def __init__(self, hidden: torch.Tensor, weight: torch.Tensor, labels: torch.Tensor, ignore_index: int,
                  cdtype: torch.dtype):
         D = hidden.shape[-1]
-        self.x = hidden.reshape(-1, D).to(cdtype).contiguous()
-        self.wpad = padded_weight(weight, cdtype)
+        Dp = -(-D // HIDDEN_MULTIPLE) * HIDDEN_MULTIPLE
+        x = hidden.reshape(-1, D).to(cdtype)
+        if Dp != D:     # zero columns: the logits, and the kept columns of dx and dW, do not change
+            x = F.pad(x, (0, Dp - D))
+        self.x = x.contiguous()
+        self.wpad = padded_weight(weight, cdtype, Dp)
         self.labels = labels.reshape(-1).to(torch.int64).contiguous()
         self.V, self.ignore_index = weight.shape[0], int(ignore_index)
-        self.N, self.D = self.x.shape
+        self.N, self.D = self.x.shape[0], D
         self.n_valid = (self.labels != self.ignore_index).sum()
 
     def loss_without_grad(self) -> torch.Tensor:
-        if self.D % FUSED_K_MULTIPLE:   # the fused kernel's K stages do not divide D: the chunk loop without G
-            return self.loss_and_grads(False, False, 1.0, None)[0]
         rows = lmce_fused_loss_rows(self.x, self.wpad, self.labels, self.V, self.ignore_index)
         return rows.sum() / self.n_valid
 
     def loss_and_grads(self, want_dx: bool, want_dw: bool, gscale: float, chunk_tokens: int | None):
         """The chunk loop: loss and, as requested, dL/dx (N, D) and dL/dW_pad (Vp, D) in fp32 for a unit seed
         (times ``gscale``)."""
-        N, D, dev = self.N, self.D, self.x.device
+        N, Dp, dev = self.N, self.x.shape[1], self.x.device
         Vp = self.wpad.shape[0]
         rows = torch.empty(N, dtype=torch.float32, device=dev)
-        dx = torch.empty((N, D), dtype=torch.float32, device=dev) if want_dx else None
-        dw = torch.zeros((Vp, D), dtype=torch.float32, device=dev) if want_dw and N == 0 else (
-            torch.empty((Vp, D), dtype=torch.float32, device=dev) if want_dw else None)
-        want_g = want_dx or want_dw
-        inv_n = torch.reciprocal(self.n_valid.to(torch.float32)).reshape(1) if want_g else None
+        dx = torch.empty((N, Dp), dtype=torch.float32, device=dev) if want_dx else None
+        dw = (torch.zeros if N == 0 else torch.empty)((Vp, Dp), dtype=torch.float32, device=dev) if want_dw else None
+        inv_n = torch.reciprocal(self.n_valid.to(torch.float32)).reshape(1)
         step = chunk_rows(N, Vp, chunk_tokens, self.wpad.element_size())
-        chunk = torch.empty((min(step, N), Vp), dtype=self.x.dtype, device=dev) if N else None
-        for r0 in range(0, N, step):
-            r1 = min(N, r0 + step)
-            logits = chunk[:r1 - r0]
-            xs = self.x[r0:r1]
-            torch.mm(xs, self.wpad.t(), out=logits)
-            lmce_rows(logits, self.labels[r0:r1], rows[r0:r1], self.V, self.ignore_index, inv_n, gscale)
-            if want_dx:
-                _matmul_f32(logits, self.wpad, dx[r0:r1], accumulate=False)
-            if want_dw:
-                _matmul_f32(logits.t(), xs, dw, accumulate=r0 > 0)
+        if N:
+            ws = train_workspace({min(step, N), N - (N - 1) // step * step}, Vp, Dp, dev)   # this loop's chunk sizes
+            for r0 in range(0, N, step):
+                r1 = min(N, r0 + step)
+                lmce_train_chunk(self.x[r0:r1], self.wpad, self.labels[r0:r1], self.V, self.ignore_index, inv_n,
+                                 gscale, rows[r0:r1], None if dx is None else dx[r0:r1], dw, r0 > 0, ws)
+        if dx is not None and Dp != self.D:
+            dx = dx[:, :self.D]
+        if dw is not None and Dp != self.D:
+            dw = dw[:, :self.D]
         return rows.sum() / self.n_valid, dx, dw
 
 
@@ -185,7 +202,7 @@ class _LinearCE(torch.autograd.Function):
             torch._assert_async(seed.to(torch.float32) == float(promised),
                                 "linear_cross_entropy: the backward seed is not the promised grad_scale")
             dw = None if dw is None else dw[:V]
-        dh = None if dx is None else dx.view(shape).to(h_dtype)
+        dh = None if dx is None else dx.reshape(shape).to(h_dtype)
         dW = None if dw is None else dw.to(w_dtype)
         return dh, dW, None, None, None, None, None, None, None
 

@@ -39,7 +39,7 @@ def _header_functions():
 def test_library_exports_every_header_function(lib):
     from sisa_amd.kernels import _lib
     declared = _header_functions()
-    assert len(declared) == 28
+    assert len(declared) == 30
     assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
     out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True, check=True)
     exported = set(re.findall(r"\bT (sisa_\w+)$", out.stdout, re.M))
@@ -55,7 +55,7 @@ def test_struct_layout_matches_c(tmp_path):
              "PrepBwdArgs": "sisa_prep_bwd_args", "LmceRowsArgs": "sisa_lmce_rows_args",
              "RmsNormArgs": "sisa_rmsnorm_args", "NormArgs": "sisa_norm_args", "SwigluArgs": "sisa_swiglu_args",
              "DecodeArgs": "sisa_decode_args", "WgradArgs": "sisa_wgrad_args", "LmceFwdArgs": "sisa_lmce_fwd_args",
-             "Round16Args": "sisa_round16_args"}
+             "Round16Args": "sisa_round16_args", "LmceTrainArgs": "sisa_lmce_train_args"}
     lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "sisa_hip.h"', "int main(void) {"]
     expect = []
     for py, c in pairs.items():
@@ -273,17 +273,19 @@ def test_linear_ce_cpu_falls_back_to_eager():
 
 def test_linear_ce_chunk_policy_and_padding():
     from sisa_amd.kernels import linear_ce as LC
-    # 16,384 tokens x 50,304 bf16 columns = 1.65 GB of logits: two chunks under the 1 GiB budget
+    # 16,384 tokens x 50,304 bf16 columns = 1.65 GB of exponentials: one chunk under the 2 GiB budget
     n = LC.chunk_rows(16384, 50304, None, 2)
-    assert n == 8192 and n * 50304 * 2 <= LC.LOGITS_BUDGET
+    assert n == 16384 and n * 50304 * 2 <= LC.PROBS_BUDGET
     n = LC.chunk_rows(100000, 50304, None, 2)
-    assert n % 128 == 0 and n * 50304 * 2 <= LC.LOGITS_BUDGET + 128 * 50304 * 2 and -(-100000 // n) == 10
+    assert n % 128 == 0 and n * 50304 * 2 <= LC.PROBS_BUDGET + 128 * 50304 * 2 and -(-100000 // n) == 5
     assert LC.chunk_rows(1000, 50304, 300, 2) == 300 and LC.chunk_rows(10, 50304, 300, 2) == 10
     assert LC.chunk_rows(0, 50304, None, 2) == 1
     w = torch.randn(1003, 8)
     wp = LC.padded_weight(w, torch.bfloat16)
     assert wp.shape == (1024, 8) and (wp[1003:] == 0).all() and torch.equal(wp[:1003], w.to(torch.bfloat16))
     assert LC.padded_weight(torch.randn(256, 8), torch.float16).shape == (256, 8)
+    wq = LC.padded_weight(w, torch.bfloat16, 64)                  # hidden size padded with zero columns
+    assert wq.shape == (1024, 64) and not wq[:, 8:].any() and torch.equal(wq[:1003, :8], w.to(torch.bfloat16))
     assert LC.flops(16384, 50277, 768)["total"] == pytest.approx(3.80e12, rel=1e-2)
 
 

@@ -6,8 +6,10 @@ autocast rounds them) and oracle.lmce_rows64 (the fp64 row pass on stored logits
   * row pass (sisa_lmce_rows): lse and loss rows to fp32 accuracy; G within one unit in the last place of the
     compute dtype; pad columns and ignored rows exactly zero; NaN / inf / out-of-range labels as the reference.
   * fused forward (sisa_lmce_fwd, used when no gradient is wanted): loss rows and lse against the fp64 row pass of the
-    fp64 logits of the rounded inputs, |err| <= 2e-5 max(1, |lse|) (its logits are fp32 accumulations); no logits
-    buffer (the peak device memory of the call stays below the logits' size); labels, padding and NaN as above.
+    fp64 logits of the rounded inputs, themselves rounded once to the compute dtype as the reference's logits are,
+    |err| <= 2e-5 max(1, |lse|) plus what one-unit flips of logits within 3e-5 of a rounding midpoint can move (the
+    kernel's fp32 accumulation order differs from fp64's); no logits buffer (the peak device memory of the call stays
+    below the logits' size); labels, padding and NaN as above.
   * gradient path: loss, dL/dh and dL/dW against both fp64 truths, each no worse than 2 x the error of the eager
     autocast formula F.cross_entropy(F.linear(h, W).float(), y) + 1e-7 -- the acceptance rule of the reference's
     tests/test_linear_ce.py:106-121 (restated); chunking, grad_scale, dtypes, ignored rows, determinism.
@@ -198,15 +200,30 @@ def test_rows_kernel_validation():
 
 
 # ------------------------------------------------------------------------------------------------ fused forward
-def _fused_truth(x16: torch.Tensor, wpad: torch.Tensor, labels: torch.Tensor, V: int, ignore_index=-100):
-    """fp64 lse and loss rows of the rounded inputs, from the fp64 logits in row chunks."""
-    lses, losses = [], []
+def _fused_truth(x16: torch.Tensor, wpad: torch.Tensor, labels: torch.Tensor, V: int, ignore_index=-100,
+                 tau: float = 3e-5):
+    """fp64 lse and loss rows of the rounded inputs, from the fp64 logits rounded once to the compute dtype (the
+    logits the reference's row kernel reads), in row chunks; and per row the rounding-flip allowance. The kernel rounds
+    its fp32 accumulations, whose summation order differs from fp64's by about 1e-6: a logit lying within ``tau`` of a
+    rounding midpoint may come out one unit away. The allowance is what such flips can move: sum p_v ulp_v over those
+    logits for lse, plus the label logit's unit when the label logit is one of them (for the loss row)."""
+    lses, losses, slack_lse, slack_row = [], [], [], []
     for r0 in range(0, x16.shape[0], 2048):
         z = x16[r0:r0 + 2048].double() @ wpad.double().t()
-        lse, loss, _ = R.lmce_rows64(z, labels[r0:r0 + 2048], V, ignore_index=ignore_index)
+        zr = z.to(x16.dtype).double()
+        lab = labels[r0:r0 + 2048]
+        lse, loss, _ = R.lmce_rows64(zr, lab, V, ignore_index=ignore_index)
+        u = R.ulp(z, x16.dtype)
+        near = (0.5 * u - (z - zr).abs()) <= tau
+        p = torch.softmax(zr[:, :V], 1)
+        sl = (p * u[:, :V] * near[:, :V]).sum(1)
+        idx = lab.clamp(0, z.shape[1] - 1).unsqueeze(1)
+        lab_flip = (near.gather(1, idx) * u.gather(1, idx)).squeeze(1)
         lses.append(lse)
         losses.append(loss)
-    return torch.cat(lses), torch.cat(losses)
+        slack_lse.append(sl)
+        slack_row.append(sl + lab_flip)
+    return torch.cat(lses), torch.cat(losses), torch.cat(slack_lse), torch.cat(slack_row)
 
 
 def _fused_call(h, w, labels, dtype=torch.bfloat16, ignore_index=-100):
@@ -229,10 +246,12 @@ def test_fused_forward_vs_fp64(N, D, V, dtype):
     lab = lab.clone()
     lab.view(-1)[::13] = -100
     x, wpad, lab1, lse, rows = _fused_call(h, w, lab, dtype)
-    lse_ref, loss_ref = _fused_truth(x, wpad, lab1, V)
-    tol = 2e-5 * lse_ref.abs().clamp_min(1.0)
+    lse_ref, loss_ref, flip_lse, flip_row = _fused_truth(x, wpad, lab1, V)
+    tol = 2e-5 * lse_ref.abs().clamp_min(1.0) + flip_lse
     assert ((lse.double() - lse_ref).abs() <= tol).all(), float(((lse.double() - lse_ref).abs() / tol).max())
-    assert ((rows.double() - loss_ref).abs() <= tol).all(), float(((rows.double() - loss_ref).abs() / tol).max())
+    tol_rows = 2e-5 * lse_ref.abs().clamp_min(1.0) + flip_row
+    assert ((rows.double() - loss_ref).abs() <= tol_rows).all(), \
+        float(((rows.double() - loss_ref).abs() / tol_rows).max())
     assert (rows[lab1 == -100] == 0).all()
     again = _fused_call(h, w, lab, dtype)
     assert torch.equal(again[4], rows) and torch.equal(again[3], lse)
@@ -284,9 +303,9 @@ def test_fused_and_gradient_paths_agree():
         fused = lce(h, w, lab)
     grad = train_pass(lce, h, w, lab, 1.0).loss
     exact = truths(h, w, lab, 1.0, only_exact=True)["fp64"].loss
-    # both within bf16 rounding of the logits of each other; the fused loss (fp32 logits) no farther from fp64
-    assert abs(fused.item() - grad.item()) < 1e-3 * abs(grad.item())
-    assert abs(fused.item() - exact.item()) <= abs(grad.item() - exact.item()) + 1e-4
+    # one logits GEMM and one reduction serve both paths: the same loss, bit for bit
+    assert torch.equal(fused, grad)
+    assert abs(fused.item() - exact.item()) < 1e-3 * abs(exact.item())
 
 
 # ------------------------------------------------------------------------------------------------ gradient path
