@@ -152,7 +152,7 @@ def queued_seconds(launch, reps: int = 20) -> float:
 
 
 def prep_kernel_rates(proj, z, H: int) -> dict:
-    """The prep forward (prep_sums + prep_fwd) and backward (prep_bsums + prep_bwd) launches through the C-ABI with
+    """The prep forward (prep_sums + prep_fwd) and backward (prep_bwd, one launch) through the C-ABI with
     prepared arguments, timed by queued_seconds, against HBM peak; beside them a plain device copy moving the same
     number of bytes (half read, half written) as the ceiling HBM offers to a transfer of that size."""
     import ctypes
@@ -169,16 +169,16 @@ def prep_kernel_rates(proj, z, H: int) -> dict:
                           _lib.ptr(z), z.stride(0), z.stride(1), pf.cr.data_ptr(), pf.br.data_ptr(),
                           pf.g.data_ptr(), _lib.ptr(pf.f), pf.rowf.data_ptr(), pf.colf.data_ptr(),
                           pf.totals.data_ptr())
+    xch = FP.exchange_workspace(proj, B, L, H)
     gen = torch.Generator().manual_seed(9)
     dg, dF = (torch.randn(B, H, L, generator=gen).to(dev) for _ in range(2))
     DCR, DBR = (torch.randn(B, L, H, 32, generator=gen).to(dev) for _ in range(2))
     DP = torch.zeros_like(proj)
     DZ = torch.empty(B, L, H, device=dev)
-    ws = torch.empty((_lib.workspace_bytes("sisa_prep_bwd_workspace_bytes", B, L, H),), device=dev, dtype=torch.uint8)
     ba = _lib.PrepBwdArgs(B, L, H, _lib.dtype_code(proj.dtype), proj.data_ptr(), proj.stride(0), proj.stride(1),
                           _lib.ptr(z), z.stride(0), z.stride(1), pf.totals.data_ptr(), dg.data_ptr(), dF.data_ptr(),
                           DCR.data_ptr(), DBR.data_ptr(), DP.data_ptr(), DP.stride(0), DP.stride(1), DZ.data_ptr(),
-                          DZ.stride(0), DZ.stride(1), ws.data_ptr())
+                          DZ.stride(0), DZ.stride(1), xch.data_ptr())
 
     def call(name, args):
         def go():

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SISA_ABI_VERSION 3
+#define SISA_ABI_VERSION 4
 
 enum sisa_dtype { SISA_F32 = 0, SISA_BF16 = 1, SISA_F16 = 2, SISA_F64 = 3 };
 
@@ -147,7 +147,11 @@ typedef struct {
     float* tot;                /* (B*H, ceil(L/64), 18) contiguous block totals */
 } sisa_prep_fwd_args;
 
-/* Workspace (bytes) of sisa_prep_bwd: fp64 block totals (B*H, ceil(L/64), 18). */
+/* Workspace of sisa_prep_bwd. The backward runs as one launch whose workgroups hand their 64-row block totals to each
+ * other through the workspace, so it must be zero-filled once before its first use and then kept: it carries a launch
+ * counter from call to call (no per-call clearing). One workspace serves any shape up to its size; calls that overlap
+ * in time on one workspace race. Bytes 8..11 (uint32) are nonzero after a call in which a workgroup's bounded wait for
+ * another's totals ran out (results invalid; not expected to happen). */
 int64_t sisa_prep_bwd_workspace_bytes(int32_t B, int32_t L, int32_t H);
 
 /* Backward prep: reverse scans (fp64) for d alpha, dz, d theta; inverse rotation of dC~/dB~; zero pad columns.
@@ -169,7 +173,7 @@ typedef struct {
     int64_t s_db, s_dl;
     float* dz;                 /* (B,L,H) fp32 or NULL */
     int64_t s_dzb, s_dzl;
-    void* workspace;           /* sisa_prep_bwd_workspace_bytes(B,L,H) bytes */
+    void* workspace;           /* sisa_prep_bwd_workspace_bytes(B,L,H) bytes, 16-byte aligned, zero-filled once */
 } sisa_prep_bwd_args;
 
 int sisa_prep_fwd(const sisa_prep_fwd_args* a, void* stream);

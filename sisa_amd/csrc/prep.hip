@@ -8,18 +8,21 @@
 // Reference: src/sisa/kernels/fused_prep.py (Triton): layout :71-96, element formulas :188-213 (torch's formulas,
 // softplus threshold 20), _prep_sums :247-274, _prep_fwd :277-352, _prep_bsums :385-411, _prep_bwd :414-494.
 //
-// Scan scheme (deterministic reduce-then-scan over 64-row chunks): pass 1 writes per-chunk totals TOT; pass 2 adds
-// the totals of the preceding chunks in sequence order to a sequential in-chunk scan. The chunk total is produced by
-// the same sequential loop as the last in-chunk value, so carry_{c+1} = carry_c + TOT_c equals the last g of chunk c
-// bit for bit and g is non-increasing across chunk boundaries. The backward runs the same scheme in reverse with
-// fp64 accumulators.
+// Scan scheme (deterministic reduce-then-scan over 64-row chunks): chunk totals first, then the left fold of the
+// preceding chunks' totals (the carry) added to a two-level in-chunk scan: four 16-row sub-chunks scanned in row order
+// by separate threads, then each value offset by the fold of the preceding sub-chunk totals. The chunk total is formed
+// by the same code, so carry_{c+1} = carry_c + TOT_c equals the last value of chunk c bit for bit, and for
+// non-positive inputs (g, F) every level of the nesting carry + (P_s + v_r) is non-increasing: g never increases,
+// inside a chunk or across a boundary. The backward runs the same scheme in reverse with fp64 accumulators.
 //
-// Decomposition: one 256-thread workgroup per (64-row chunk, batch row, group of HG = 4 heads). Every global access is
-// issued up front as 16-byte vectors (theta 8 vectors per row; C, B, dC~, dB~ 16 per row), element functions are
-// evaluated by all threads before the 72 scan lanes (head, component) run their sequential 64-row scans out of LDS,
-// and the totals of the preceding (following) chunks are staged through LDS with one parallel load before each lane
-// folds them in chunk order. The backward's first pass also applies the inverse rotation and keeps dPhi rows in the
-// workspace, so its second pass reads only dg, dF, dPhi, alpha and z.
+// Decomposition: one 512-thread workgroup per (64-row chunk, batch row, group of HG = 4 heads); 288 scan tasks (head,
+// component, sub-chunk) run out of LDS while 72 other threads fold the carry from totals staged through LDS.
+//   forward   two launches: prep_sums writes the chunk totals TOT; prep_fwd loads the totals and the scan inputs
+//             (cached by prep_sums) first and has waves 0..3 move C and B straight into LDS, so the carry fold and
+//             the scans run while C and B are in flight (LDS-only barriers until the rotation).
+//   backward  one launch, prep_bwd: Phi recomputed from theta and TOT, dPhi and the inverse rotation, the fp64 chunk
+//             totals of (dg, dF, dPhi) handed to the other workgroups of the launch through the workspace (the total
+//             exchange below), the reverse scans. No dPhi rows leave the chip.
 #include "common.h"
 #include "host.h"
 
@@ -86,12 +89,55 @@ SISA_DEV Unit cb_unit(int v) { return Unit{v >> 4, (v >> 2) & 3, v & 3}; }
 template <class T>
 SISA_DEV frag8<T> load8_if(const T* p, bool ok) { return ok ? load8<T>(p) : zero8<T>(); }
 
-// Scan lanes: x[hl*NCOMP + comp][r] holds the element values of chunk row r (0 beyond L), then the inclusive scan plus
-// the carry of the preceding chunks. Rows padded to 65 floats: the 72 scanning lanes read one row each without bank
-// conflicts.
+// Scan columns: x[hl*NCOMP + comp][r] holds the element values of chunk row r (0 beyond L), then the inclusive scan
+// plus the carry of the preceding chunks. Rows padded to 65 floats: the scan tasks of a wave, on consecutive columns,
+// read without bank conflicts.
 struct ScanLds {
     float x[HC][CH + 1];
 };
+
+// Two-level in-chunk scans: NSUB sub-chunks of SUB rows. Scan task t < NTASK owns (column t % HC, sub-chunk t / HC)
+// and runs its SUB rows in order; thread NTASK + l folds the carry of column l meanwhile (carry_of below).
+constexpr int SUB = 16, NSUB = CH / SUB, NTASK = HC * NSUB;
+static_assert(NTASK + HC <= NT, "scan tasks and carry lanes on distinct threads");
+template <class Acc>
+struct SubLds {
+    Acc sub[NSUB][HC];   // sub-chunk totals
+    Acc carry[HC];       // carry of the preceding (forward) or following (reverse) chunks
+};
+
+// Forward scan, phase 1, in place: x[SUB*s + r] <- v_r = x[SUB*s] + ... + x[SUB*s + r] summed in row order; the
+// sub-chunk total is v_{SUB-1}.
+SISA_DEV void fwd_sub_scan(ScanLds& sm, SubLds<float>& sl, int t) {
+    const int col = t % HC, s = t / HC;
+    float* x = sm.x[col] + SUB * s;
+    float v[SUB];
+#pragma unroll
+    for (int r = 0; r < SUB; ++r) v[r] = x[r];
+#pragma unroll
+    for (int r = 1; r < SUB; ++r) v[r] += v[r - 1];
+#pragma unroll
+    for (int r = 1; r < SUB; ++r) x[r] = v[r];
+    sl.sub[s][col] = v[SUB - 1];
+}
+// P_n: the left fold, from 0, of the first n sub-chunk totals of column col. The chunk total is P_NSUB.
+SISA_DEV float fwd_sub_prefix(const SubLds<float>& sl, int col, int n) {
+    float p = 0.f;
+#pragma unroll
+    for (int j = 0; j < NSUB; ++j)
+        if (j < n) p += sl.sub[j][col];
+    return p;
+}
+// Forward scan, phase 2: x[SUB*s + r] = carry + (P_s + v_r). For non-positive inputs each level is non-increasing
+// and ends on the first partial sum of the level above (v[SUB-1] + P_s = P_{s+1}; carry_c + P_NSUB = carry_{c+1}),
+// so the result is non-increasing over the chunk and across chunk boundaries.
+SISA_DEV void fwd_sub_finish(ScanLds& sm, const SubLds<float>& sl, int t) {
+    const int col = t % HC, s = t / HC;
+    const float p = fwd_sub_prefix(sl, col, s), carry = sl.carry[col];
+    float* x = sm.x[col] + SUB * s;
+#pragma unroll
+    for (int r = 0; r < SUB; ++r) x[r] = carry + (p + x[r]);
+}
 
 // Staging loads of one thread: theta vector `tid` of the chunk (row tid>>3, head (tid>>1)&3, pairs 8*(tid&1)..+7)
 // and, for tid < 256, alpha and z of (row tid>>2, head tid&3). Split from the LDS stores so that a kernel issues
@@ -134,6 +180,14 @@ SISA_DEV void stage_store(ScanLds& sm, const StageVals<T>& s, int nrows, int hn,
         sm.x[hl * NCOMP + 0][row] = ok ? neg_softplus(s.al) : 0.f;
         sm.x[hl * NCOMP + 1][row] = (ok && has_z) ? logsigmoid(s.zv) : 0.f;
     }
+}
+
+// Workgroup barrier that orders LDS only: global loads and buffer->LDS transfers a wave has in flight stay in flight
+// across it (a plain barrier waits for all of them first).
+SISA_DEV void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // Carries of the scans: the left fold, in chunk order, of the chunk totals of a range of chunks [c0, c1) (the
@@ -180,44 +234,197 @@ SISA_DEV Acc tot_fold(const TotLds<Acc>& tl, int hl, int comp, int n, Acc acc) {
     }
     return acc;
 }
-// The carry of scan lane tid (when `lane`) over chunks [c0, c1). The caller has loaded the first batch into v with
+// The carry of column li (when `lane`) over chunks [c0, c1). The caller has loaded the first batch into v with
 // tot_load(v, ..., c0, min(c1, c0 + TB)), stored it (tot_store) and passed a barrier. Further batches are loaded and
 // folded here; every thread of the workgroup calls this (it has barriers when c1 - c0 > TB).
 template <class Acc>
 SISA_DEV Acc carry_of(TotLds<Acc>& tl, Acc (&v)[TPT], const Acc* tot, int bh0, int hn, int NCH, int c0, int c1,
-                      bool lane, int tid) {
-    const int hl = tid / NCOMP, comp = tid % NCOMP;
+                      bool lane, int li, int tid) {
+    const int hl = li / NCOMP, comp = li % NCOMP;
     Acc acc = lane ? tot_fold(tl, hl, comp, (c1 - c0 < TB) ? c1 - c0 : TB, (Acc)0) : (Acc)0;
     for (int cb = c0 + TB; cb < c1; cb += TB) {
         const int ce = (c1 - cb < TB) ? c1 : cb + TB;
         tot_load(v, tot, bh0, hn, NCH, cb, ce, tid);
-        __syncthreads();   // every lane is done with the previous batch
+        lds_barrier();   // every lane is done with the previous batch
         tot_store(tl, v, tid);
-        __syncthreads();
+        lds_barrier();
         if (lane) acc = tot_fold(tl, hl, comp, ce - cb, acc);
     }
     return acc;
 }
 
-// In-chunk inclusive scan of one lane with the carry added: x[r] = carry + sum_{i <= r} x[i] (sequential order).
-SISA_DEV void scan_lane(float* x, float carry) {
-    float v[CH];
+// ------------------------------------------------------------------------------------------------ total exchange
+// The backward's workgroups hand their fp64 chunk totals to each other through the workspace instead of through a
+// second launch. A total travels as two 64-bit words (its low and high 32 bits) whose upper halves are the launch's
+// tag, written and polled with relaxed device-scope atomics: a word is read whole, so a half and its tag always belong
+// together and no fence is needed, and a word left by an earlier launch carries an older tag. The tag is the
+// workspace's epoch + 1. Every workgroup reads the epoch before it counts itself in `arrivals` (at its end); the last
+// to arrive resets the count and advances the epoch, which the next launch on the stream then reads. A zeroed
+// workspace starts at epoch 0 with no word tagged 1.
+//
+// Progress: the workgroups are numbered chunk-major from the last chunk down (the last chunk of every sequence before
+// the one below it), each publishes its totals before it waits, and it waits only for workgroups of lower number,
+// which the hardware dispatches first, so the lowest unfinished workgroup never waits. The wait is bounded all the
+// same: after SPIN_LIMIT polls the `error` word is set, the missing totals count as zero and the launch ends.
+struct XchHeader {
+    uint32_t epoch, arrivals, error;
+};
+constexpr int64_t XCH_HEADER = 256;   // bytes before the words
+constexpr int SPIN_LIMIT = 1 << 15;
+constexpr int XW = 2;                 // words per total
+
+__host__ __device__ inline int64_t xch_bytes(int B, int L, int H) {
+    const int64_t seqs = (int64_t)B * ((H + HG - 1) / HG), chunks = (L + CH - 1) / CH;
+    return XCH_HEADER + seqs * chunks * HC * XW * (int64_t)sizeof(uint64_t);
+}
+
+SISA_DEV uint64_t tagged(uint32_t tag, uint32_t bits) { return ((uint64_t)tag << 32) | bits; }
+SISA_DEV void xch_put(uint64_t* w, uint32_t tag, double v) {
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    __hip_atomic_store(w, tagged(tag, (uint32_t)u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(w + 1, tagged(tag, (uint32_t)(u >> 32)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+SISA_DEV uint64_t xch_load(const uint64_t* w) {
+    return __hip_atomic_load(const_cast<uint64_t*>(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Exchanged totals of up to TB chunks, [chunk - first][column].
+struct XLds {
+    double t[TB][HC];
+};
+constexpr int GPT = (TB * HC) / NT;   // totals per thread and batch
+static_assert(GPT * NT == TB * HC && GPT <= 32 && (TB & (TB - 1)) == 0, "gathered totals split evenly");
+
+// The totals of chunks [c0, c1) (at most TB) of one sequence's words (laid out [chunk][column][2]) into xl (zero for
+// columns of absent heads), each polled until both its words carry `tag`; thread t takes the totals t, t + NT, ... of
+// the range. All loads of a poll are issued before the first is examined; a total goes to LDS as soon as it has
+// arrived.
+SISA_DEV void xch_gather(XLds& xl, const uint64_t* seqw, int hn, int c0, int c1, uint32_t tag, uint32_t* err, int t) {
+    const int n = (c1 - c0) * HC;
+    double* dst = &xl.t[0][0];
+    const uint64_t* src = seqw + ((int64_t)c0 * HC + t) * XW;
+    uint32_t pending = 0;
 #pragma unroll
-    for (int r = 0; r < CH; ++r) v[r] = x[r];
-    float incl = 0.f;
+    for (int q = 0; q < GPT; ++q) {
+        const int e = t + NT * q;
+        if (e < n && (e % HC) / NCOMP < hn)
+            pending |= 1u << q;
+        else
+            dst[e] = 0.0;
+    }
+    for (int it = 0; pending != 0; ++it) {
+        uint64_t lo[GPT], hi[GPT];
 #pragma unroll
-    for (int r = 0; r < CH; ++r) {
-        incl += v[r];
-        x[r] = carry + incl;
+        for (int q = 0; q < GPT; ++q)
+            if (pending & (1u << q)) {
+                lo[q] = xch_load(src + NT * XW * q);
+                hi[q] = xch_load(src + NT * XW * q + 1);
+            }
+#pragma unroll
+        for (int q = 0; q < GPT; ++q)
+            if ((pending & (1u << q)) && (uint32_t)(lo[q] >> 32) == tag && (uint32_t)(hi[q] >> 32) == tag) {
+                dst[t + NT * q] = __longlong_as_double((long long)((hi[q] << 32) | (lo[q] & 0xffffffffull)));
+                pending &= ~(1u << q);
+            }
+        if (pending == 0) break;
+        if (it == SPIN_LIMIT) {
+            __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int q = 0; q < GPT; ++q)
+                if (pending & (1u << q)) dst[t + NT * q] = 0.0;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(4);
+    }
+}
+
+// The left fold, in chunk order, of the exchanged totals of chunks [c0, c1) for column li (when `lane`). Every thread
+// of the workgroup calls this: it gathers through LDS, TB chunks per batch; the reads of FB chunks are issued before
+// their adds.
+SISA_DEV double carry_xch(XLds& xl, const uint64_t* seqw, int hn, int c0, int c1, uint32_t tag, uint32_t* err,
+                          bool lane, int li, int tid) {
+    constexpr int FB = 16;
+    double acc = 0.0;
+    for (int cb = c0; cb < c1; cb += TB) {
+        const int ce = (c1 - cb < TB) ? c1 : cb + TB;
+        if (cb > c0) __syncthreads();   // every lane is done with the previous batch
+        xch_gather(xl, seqw, hn, cb, ce, tag, err, tid);
+        __syncthreads();
+        if (lane) {
+            for (int k0 = 0; k0 < ce - cb; k0 += FB) {
+                double buf[FB];
+#pragma unroll
+                for (int k = 0; k < FB; ++k) buf[k] = xl.t[(k0 + k) & (TB - 1)][li];
+#pragma unroll
+                for (int k = 0; k < FB; ++k) acc += (k0 + k < ce - cb) ? buf[k] : 0.0;
+            }
+        }
+    }
+    return acc;
+}
+
+// The launch's arrival (thread 0, at its end): the last workgroup to arrive resets the count and advances the epoch.
+SISA_DEV void xch_arrive(XchHeader* xh, uint32_t epoch, unsigned nwg) {
+    const uint32_t before = __hip_atomic_fetch_add(&xh->arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (before == nwg - 1) {
+        __hip_atomic_store(&xh->arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&xh->epoch, epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Workgroup w of a launch: sequence seq = w % NSEQ (batch row seq / NHG, heads of group seq % NHG), chunk index
+// w / NSEQ counted from the first chunk (forward) or from the last (backward).
+struct Geo {
+    int c, b, h0, hn, nrows, NCH, seq;
+};
+SISA_DEV Geo geo_of(int B, int L, int H, bool reverse) {
+    Geo g;
+    const int NHG = (H + HG - 1) / HG, NSEQ = B * NHG;
+    g.NCH = (L + CH - 1) / CH;
+    g.seq = (int)blockIdx.x % NSEQ;
+    const int k = (int)blockIdx.x / NSEQ;
+    g.c = reverse ? g.NCH - 1 - k : k;
+    g.b = g.seq / NHG;
+    g.h0 = (g.seq % NHG) * HG;
+    g.hn = (H - g.h0 < HG) ? H - g.h0 : HG;
+    g.nrows = (L - g.c * CH < CH) ? L - g.c * CH : CH;
+    return g;
+}
+
+// Stores of outputs that no later step of the launch reads: non-temporal, so that they stream to memory while the
+// kernel runs instead of waiting in L2 for the write-back at its end (1.5 us of the forward pass at the north-star
+// shape).
+template <class V>
+SISA_DEV void store_nt(V* p, const V& v) {
+    __builtin_nontemporal_store(v, p);
+}
+
+// Buffer->LDS staging of a chunk's C and B columns of the workgroup's heads into cbl = [C, B][CH rows][CB_ROW]: wave
+// instruction k (0..31, eight for each of waves 0..3) moves 1 KB, four rows of one block, lane i one 16-byte piece.
+// Rows past the chunk's valid rows read as zero (the buffer's extent ends there).
+constexpr int CB_ROW = HG * DS;   // elements of a staged row
+template <int KERNEL, class T>
+SISA_DEV void cb_dma(const T* P, int64_t s_pl, int nrows, const Layout& off, int h0, T* cbl, int tid) {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(P, (int64_t)nrows * s_pl * (int64_t)sizeof(T));
+    const int w = tid >> 6, lane = tid & 63;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        const int k = w + 4 * p;
+        const int pi = 64 * (k & 15) + lane;   // piece of the block: row pi / 16, 16-byte column pi % 16
+        const int voff = (int)(((pi >> 4) * s_pl + ((k >> 4) ? off.B : off.C) + h0 * DS) * (int64_t)sizeof(T)) +
+                         16 * (pi & 15);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            r, (__attribute__((address_space(3))) void*)(cbl + k * (1024 / (int)sizeof(T))), 16, voff, 0, 0, 0);
     }
 }
 
 // ------------------------------------------------------------------------------------------------ forward
-// Pass 1: TOT[bh][c][comp] = sequential sum of the chunk's element values (the same loop as the pass-2 scan, so the
-// total equals the chunk's last inclusive value bit for bit).
+// Two launches. Pass 1: TOT[bh][c][comp] = the chunk total P_NSUB of the element values, formed by the code of the
+// pass-2 scan, so that it equals the chunk's last scanned value bit for bit.
 template <class T>
 __global__ __launch_bounds__(NT) void prep_sums_kernel(sisa_prep_fwd_args a) {
     __shared__ ScanLds sm;
+    __shared__ SubLds<float> sl;
     const int c = blockIdx.x, b = blockIdx.y, h0 = blockIdx.z * HG;
     const int H = a.H, L = a.L, NCH = gridDim.x;
     const int hn = (H - h0 < HG) ? H - h0 : HG;
@@ -229,19 +436,21 @@ __global__ __launch_bounds__(NT) void prep_sums_kernel(sisa_prep_fwd_args a) {
     stage_store<T, true>(sm, stage_load<T>(P, a.s_pl, Z, a.s_zl, nrows, hn, off, h0, tid), nrows, hn, Z != nullptr,
                          tid);
     __syncthreads();
-    if (tid < HC && tid / NCOMP < hn) {
-        float incl = 0.f;
-#pragma unroll 16
-        for (int r = 0; r < CH; ++r) incl += sm.x[tid][r];
-        a.tot[((int64_t)(b * H + h0 + tid / NCOMP) * NCH + c) * NCOMP + tid % NCOMP] = incl;
-    }
+    if (tid < NTASK) fwd_sub_scan(sm, sl, tid);
+    __syncthreads();
+    if (tid < HC && tid / NCOMP < hn)
+        a.tot[((int64_t)(b * H + h0 + tid / NCOMP) * NCH + c) * NCOMP + tid % NCOMP] = fwd_sub_prefix(sl, tid, NSUB);
 }
 
-// Pass 2: scans (carry of the preceding chunks + in-chunk inclusive scan), g/F/rowf/colf, rotation of C and B.
+// Pass 2: scans (carry of the preceding chunks + the two-level in-chunk scan), g/F/rowf/colf, rotation of C and B.
+// The totals and scan inputs (cached by pass 1) are loaded first, then waves 0..3 move C and B straight into LDS;
+// every barrier until the rotation orders LDS only, so the carry fold and the scans run while C and B are in flight.
 template <class T>
 __global__ __launch_bounds__(NT) void prep_fwd_kernel(sisa_prep_fwd_args a) {
     __shared__ ScanLds sm;
     __shared__ TotLds<float> tl;
+    __shared__ SubLds<float> sl;
+    __shared__ __attribute__((aligned(16))) T cbl[2 * CH * CB_ROW];
     const int c = blockIdx.x, b = blockIdx.y, h0 = blockIdx.z * HG;
     const int H = a.H, L = a.L, NCH = gridDim.x;
     const int hn = (H - h0 < HG) ? H - h0 : HG;
@@ -250,27 +459,21 @@ __global__ __launch_bounds__(NT) void prep_fwd_kernel(sisa_prep_fwd_args a) {
     const int tid = threadIdx.x;
     const T* P = (const T*)a.proj + (int64_t)b * a.s_pb + (int64_t)c * CH * a.s_pl;
     const float* Z = a.z ? a.z + (int64_t)b * a.s_zb + (int64_t)c * CH * a.s_zl : nullptr;
-    // Every global load is issued before the first wait, in the order of use: the staged scan inputs, the totals of
-    // the preceding chunks, then the C and B vectors this thread rotates.
-    const StageVals<T> sv = stage_load<T>(P, a.s_pl, Z, a.s_zl, nrows, hn, off, h0, tid);
-    const bool lane = tid < HC && tid / NCOMP < hn;
     float tv[TPT];
     tot_load(tv, a.tot, b * H + h0, hn, NCH, 0, c < TB ? c : TB, tid);
-    frag8<T> cv[NU], bv[NU];
-#pragma unroll
-    for (int i = 0; i < NU; ++i) {
-        const Unit u = cb_unit(tid + NT * i);
-        const bool ok = u.row < nrows && u.hl < hn;
-        const T* prow = P + (int64_t)u.row * a.s_pl + (h0 + u.hl) * DS + 8 * u.q;
-        cv[i] = load8_if<T>(prow + off.C, ok);
-        bv[i] = load8_if<T>(prow + off.B, ok);
-    }
+    const StageVals<T> sv = stage_load<T>(P, a.s_pl, Z, a.s_zl, nrows, hn, off, h0, tid);
+    if (tid < 256) cb_dma<0, T>(P, a.s_pl, nrows, off, h0, cbl, tid);
     stage_store<T, true>(sm, sv, nrows, hn, Z != nullptr, tid);
     tot_store(tl, tv, tid);
-    __syncthreads();
-    const float carry = carry_of(tl, tv, a.tot, b * H + h0, hn, NCH, 0, c, lane, tid);
-    if (lane) scan_lane(sm.x[tid], carry);
-    __syncthreads();
+    lds_barrier();
+    if (tid < NTASK) fwd_sub_scan(sm, sl, tid);
+    const int li = tid - NTASK;   // carry lane of column li
+    const bool lane = li >= 0 && li < HC && li / NCOMP < hn;
+    const float carry = carry_of(tl, tv, a.tot, b * H + h0, hn, NCH, 0, c, lane, li, tid);
+    if (li >= 0 && li < HC) sl.carry[li] = carry;
+    lds_barrier();
+    if (tid < NTASK) fwd_sub_finish(sm, sl, tid);
+    lds_barrier();
     // g, F, rowf, colf: (B,H,L) rows, one (head, row) per thread, coalesced along L
     {
         const int hh = tid >> 6, r = tid & 63;
@@ -278,12 +481,13 @@ __global__ __launch_bounds__(NT) void prep_fwd_kernel(sisa_prep_fwd_args a) {
             const int64_t o = ((int64_t)(b * H + h0 + hh)) * L + c * CH + r;
             const float* gx = sm.x[hh * NCOMP];
             const float g = gx[r];
-            a.g[o] = g;
-            a.rowf[o] = exp2_le0((g - gx[0]) * LOG2E);
-            a.colf[o] = exp2_le0((gx[CH - 1] - g) * LOG2E);   // rows >= L added 0: the last valid g
-            if (a.z) a.f[o] = sm.x[hh * NCOMP + 1][r];
+            store_nt(a.g + o, g);
+            store_nt(a.rowf + o, exp2_le0((g - gx[0]) * LOG2E));
+            store_nt(a.colf + o, exp2_le0((gx[CH - 1] - g) * LOG2E));   // rows >= L added 0: the last valid g
+            if (a.z) store_nt(a.f + o, sm.x[hh * NCOMP + 1][r]);
         }
     }
+    __syncthreads();   // C and B have landed in LDS
     // rotation of C and B by Phi (fp32, one rounding to T); 4 pairs per vector
     T* CR = (T*)a.cr;
     T* BR = (T*)a.br;
@@ -291,13 +495,15 @@ __global__ __launch_bounds__(NT) void prep_fwd_kernel(sisa_prep_fwd_args a) {
     for (int i = 0; i < NU; ++i) {
         const Unit u = cb_unit(tid + NT * i);
         if (u.row >= nrows || u.hl >= hn) continue;
+        const T* src = cbl + u.row * CB_ROW + u.hl * DS + 8 * u.q;
+        const frag8<T> cv = load8<T>(src), bv = load8<T>(src + CH * CB_ROW);
         f32x4 clo, chi, blo, bhi;
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             float sn, cs;
             sincos_rev(sm.x[u.hl * NCOMP + 2 + 4 * u.q + p][u.row], &sn, &cs);
-            const float ce = (float)cv[i][2 * p], co = (float)cv[i][2 * p + 1];
-            const float be = (float)bv[i][2 * p], bo = (float)bv[i][2 * p + 1];
+            const float ce = (float)cv[2 * p], co = (float)cv[2 * p + 1];
+            const float be = (float)bv[2 * p], bo = (float)bv[2 * p + 1];
             const float c0 = ce * cs - co * sn, c1 = ce * sn + co * cs;
             const float b0 = be * cs - bo * sn, b1 = be * sn + bo * cs;
             if (p < 2) {
@@ -307,43 +513,52 @@ __global__ __launch_bounds__(NT) void prep_fwd_kernel(sisa_prep_fwd_args a) {
             }
         }
         const int64_t o = (((int64_t)b * L + c * CH + u.row) * H + h0 + u.hl) * DS + 8 * u.q;
-        *reinterpret_cast<frag8<T>*>(CR + o) = pack8<T>(clo, chi);
-        *reinterpret_cast<frag8<T>*>(BR + o) = pack8<T>(blo, bhi);
+        store_nt(reinterpret_cast<frag8<T>*>(CR + o), pack8<T>(clo, chi));
+        store_nt(reinterpret_cast<frag8<T>*>(BR + o), pack8<T>(blo, bhi));
     }
 }
 
 // ------------------------------------------------------------------------------------------------ backward
-// Workspace: fp64 chunk totals BT (B*H, NCH, 18), then dPhi rows (B, L, H, 16) fp32 written by pass 1.
-__host__ __device__ inline int64_t bt_bytes(int B, int L, int H) {
-    return ((int64_t)B * H * ((L + CH - 1) / CH) * NCOMP * (int64_t)sizeof(double) + 255) / 256 * 256;
-}
-
-// Pass 1: recompute Phi (the forward scan of theta), then per (row, head, 4 pairs): dPhi = sum over {C, B} of
-// dout_odd * out_even - dout_even * out_odd, the inverse rotation dC = R(-Phi) dC~, dB = R(-Phi) dB~ into dproj, dPhi
-// rows into the workspace, and the fp64 chunk totals of (dg, dF, dPhi[16]).
+// One launch, the chunks in reverse order: Phi recomputed (the forward scan of theta, its carry folded from the
+// forward's TOT), then per (row, head, 4 pairs) dPhi = sum over {C, B} of dout_odd * out_even - dout_even * out_odd and
+// the inverse rotation dC = R(-Phi) dC~, dB = R(-Phi) dB~ into dproj; the fp64 chunk totals of (dg, dF, dPhi[16])
+// published; their carry folded from the following chunks; the reverse scans into d alpha, dz, d theta; pad columns
+// set to zero. d alpha = -suffix * softplus'(alpha) and dz = suffix * logsigmoid'(z) are formed by the threads that
+// loaded alpha and z.
 template <class T>
-__global__ __launch_bounds__(NT) void prep_bsums_kernel(sisa_prep_bwd_args a) {
-    __shared__ ScanLds sm;
-    __shared__ TotLds<float> tl;
-    const int c = blockIdx.x, b = blockIdx.y, h0 = blockIdx.z * HG;
-    const int H = a.H, L = a.L, NCH = gridDim.x;
-    const int hn = (H - h0 < HG) ? H - h0 : HG;
-    const int nrows = (L - c * CH < CH) ? L - c * CH : CH;
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 8))) void prep_bwd_kernel(sisa_prep_bwd_args a) {
+    __shared__ ScanLds sm;   // theta, then Phi
+    __shared__ ScanLds sq;   // dg, dF and dPhi, then their reverse scans
+    __shared__ union {
+        TotLds<float> f;   // forward totals of the preceding chunks (Phi carry)
+        XLds d;            // exchanged totals of the following chunks (reverse carry)
+    } tu;
+    __shared__ SubLds<float> sl;
+    __shared__ SubLds<double> sd;
+    __shared__ uint32_t s_tag;
+    const int H = a.H, L = a.L;
+    const Geo G = geo_of(a.B, L, H, true);
+    const int c = G.c, b = G.b, h0 = G.h0, hn = G.hn, nrows = G.nrows, NCH = G.NCH;
     const Layout off = layout_of(H);
     const int tid = threadIdx.x;
+    XchHeader* xh = (XchHeader*)a.workspace;
+    uint64_t* seqw = (uint64_t*)((char*)a.workspace + XCH_HEADER) + (int64_t)G.seq * NCH * HC * XW;
     const T* P = (const T*)a.proj + (int64_t)b * a.s_pb + (int64_t)c * CH * a.s_pl;
-    // Every global load is issued before the first wait, in the order of use: theta, dg and dF, the forward totals
-    // of the preceding chunks, then the C, B, dC~ and dB~ vectors of this thread.
+    // Every global load but alpha and z is issued before the first wait, in the order of use: the epoch, theta, dg
+    // and dF, the forward totals of the preceding chunks, then the C, B, dC~ and dB~ vectors of this thread. Alpha and
+    // z are loaded while the workgroup waits for the following chunks' totals.
+    uint32_t epoch = 0;
+    if (tid == 0) epoch = __hip_atomic_load(&xh->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const StageVals<T> sv = stage_load<T, false>(P, a.s_pl, nullptr, 0, nrows, hn, off, h0, tid);
-    float dgv = 0.f, dfv = 0.f;   // dg and dF of (head tid>>6, row tid&63)
+    float dgv = 0.f, dfv = 0.f;
     if (tid < CH * HG) {
-        const int hh = tid >> 6, r = tid & 63;
-        const bool ok = hh < hn && r < nrows;
-        const int64_t o = (int64_t)(b * H + h0 + hh) * L + c * CH + r;
-        if (ok) dgv = a.dg[o];
-        if (ok && a.df) dfv = a.df[o];
+        const int hh = tid >> 6, r = tid & 63;   // dg, dF of (head hh, row r): coalesced along L
+        if (hh < hn && r < nrows) {
+            const int64_t o = (int64_t)(b * H + h0 + hh) * L + c * CH + r;
+            dgv = a.dg[o];
+            if (a.df) dfv = a.df[o];
+        }
     }
-    const bool lane = tid < HC && tid / NCOMP < hn && tid % NCOMP >= 2;   // Phi lanes (components 2..17)
     float tv[TPT];
     tot_load(tv, a.tot, b * H + h0, hn, NCH, 0, c < TB ? c : TB, tid);
     frag8<T> cv[NU], bv[NU];
@@ -365,17 +580,26 @@ __global__ __launch_bounds__(NT) void prep_bsums_kernel(sisa_prep_bwd_args a) {
     stage_store<T, false>(sm, sv, nrows, hn, false, tid);
     if (tid < CH * HG) {
         const int hh = tid >> 6, r = tid & 63;
-        sm.x[(hh & 3) * NCOMP + 0][r] = dgv;
-        sm.x[(hh & 3) * NCOMP + 1][r] = dfv;
+        sq.x[hh * NCOMP + 0][r] = dgv;
+        sq.x[hh * NCOMP + 1][r] = dfv;
     }
-    tot_store(tl, tv, tid);
-    __syncthreads();
-    const float carry = carry_of(tl, tv, a.tot, b * H + h0, hn, NCH, 0, c, lane, tid);
-    if (lane) scan_lane(sm.x[tid], carry);   // Phi: the forward scan of theta
-    __syncthreads();
+    tot_store(tu.f, tv, tid);
+    if (tid == 0) s_tag = epoch + 1;
+    // LDS-only barriers until the rotation: the Phi scan runs while C, B, dC~ and dB~ are in flight (issued last, so
+    // the waits for theta, dg, dF and the totals do not wait for them).
+    lds_barrier();
+    const int li = tid - NTASK;   // carry lane of column li
+    {   // Phi: the forward scan of theta (components 2..17), by the forward's code
+        const bool phi_task = tid < NTASK && (tid % HC) % NCOMP >= 2;
+        const bool phi_lane = li >= 0 && li < HC && li / NCOMP < hn && li % NCOMP >= 2;
+        if (phi_task) fwd_sub_scan(sm, sl, tid);
+        const float carry = carry_of(tu.f, tv, a.tot, b * H + h0, hn, NCH, 0, c, phi_lane, li, tid);
+        if (li >= 0 && li < HC) sl.carry[li] = carry;
+        lds_barrier();
+        if (phi_task) fwd_sub_finish(sm, sl, tid);
+    }
+    lds_barrier();
     T* DP = (T*)a.dproj + (int64_t)b * a.s_db + (int64_t)c * CH * a.s_dl;
-    float* DPHI = (float*)((char*)a.workspace + bt_bytes(a.B, L, H));
-    float dphi[NU][4];
 #pragma unroll
     for (int i = 0; i < NU; ++i) {
         const Unit u = cb_unit(tid + NT * i);
@@ -393,7 +617,7 @@ __global__ __launch_bounds__(NT) void prep_bsums_kernel(sisa_prep_bwd_args a) {
             const float boe = be * cs - bo * sn, boo = be * sn + bo * cs;
             const float d1 = dc1 * coe - dc0 * coo;
             const float d2 = db1 * boe - db0 * boo;
-            dphi[i][p] = ok ? d1 + d2 : 0.f;
+            sq.x[u.hl * NCOMP + 2 + 4 * u.q + p][u.row] = ok ? d1 + d2 : 0.f;
             const float x0 = dc0 * cs + dc1 * sn, x1 = dc1 * cs - dc0 * sn;
             const float y0 = db0 * cs + db1 * sn, y1 = db1 * cs - db0 * sn;
             if (p < 2) {
@@ -406,100 +630,53 @@ __global__ __launch_bounds__(NT) void prep_bsums_kernel(sisa_prep_bwd_args a) {
             T* drow = DP + (int64_t)u.row * a.s_dl + (h0 + u.hl) * DS + 8 * u.q;
             *reinterpret_cast<frag8<T>*>(drow + off.C) = pack8<T>(xlo, xhi);
             *reinterpret_cast<frag8<T>*>(drow + off.B) = pack8<T>(ylo, yhi);
-            const int64_t o = (((int64_t)b * L + c * CH + u.row) * H + h0 + u.hl) * S2 + 4 * u.q;
-            *reinterpret_cast<f32x4*>(DPHI + o) = f32x4{dphi[i][0], dphi[i][1], dphi[i][2], dphi[i][3]};
         }
-    }
-    __syncthreads();   // every Phi read is done before the lanes are overwritten with dPhi
-#pragma unroll
-    for (int i = 0; i < NU; ++i) {
-        const Unit u = cb_unit(tid + NT * i);
-#pragma unroll
-        for (int p = 0; p < 4; ++p) sm.x[u.hl * NCOMP + 2 + 4 * u.q + p][u.row] = dphi[i][p];
     }
     __syncthreads();
-    double* BT = (double*)a.workspace;
-    if (tid < HC && tid / NCOMP < hn) {
-        double s = 0.0;
-#pragma unroll 16
-        for (int r = 0; r < CH; ++r) s += (double)sm.x[tid][r];
-        BT[((int64_t)(b * H + h0 + tid / NCOMP) * NCH + c) * NCOMP + tid % NCOMP] = s;
-    }
-}
-
-// Pass 2: reverse scans (fp64 carry of the following chunks + in-chunk reverse sums) into d alpha, dz, d theta; pad
-// columns set to zero. d alpha = -suffix * softplus'(alpha) and dz = suffix * logsigmoid'(z) are formed by the
-// threads that loaded alpha and z, when they write them.
-template <class T>
-__global__ __launch_bounds__(NT) void prep_bwd_kernel(sisa_prep_bwd_args a) {
-    __shared__ ScanLds sm;
-    __shared__ TotLds<double> tl;
-    const int c = blockIdx.x, b = blockIdx.y, h0 = blockIdx.z * HG;
-    const int H = a.H, L = a.L, NCH = gridDim.x;
-    const int hn = (H - h0 < HG) ? H - h0 : HG;
-    const int nrows = (L - c * CH < CH) ? L - c * CH : CH;
-    const Layout off = layout_of(H);
-    const int tid = threadIdx.x;
-    const T* P = (const T*)a.proj + (int64_t)b * a.s_pb + (int64_t)c * CH * a.s_pl;
-    const float* DPHI = (const float*)((const char*)a.workspace + bt_bytes(a.B, L, H));
-    const double* BT = (const double*)a.workspace;
-    // Every global load is issued before the first wait: dPhi rows (written by pass 1; one (row, head, 4 pairs)
-    // vector per thread and iteration), dg and dF, alpha and z, and the fp64 totals of the following chunks.
-    f32x4 dph[NU];
+    if (tid < NTASK) {   // fp64 sub-chunk sums
+        const float* x = sq.x[tid % HC] + SUB * (tid / HC);
+        double acc = 0.0;
 #pragma unroll
-    for (int i = 0; i < NU; ++i) {
-        const Unit u = cb_unit(tid + NT * i);
-        const bool ok = u.row < nrows && u.hl < hn;
-        const int64_t o = (((int64_t)b * L + c * CH + u.row) * H + h0 + u.hl) * S2 + 4 * u.q;
-        dph[i] = ok ? *reinterpret_cast<const f32x4*>(DPHI + o) : zero4();
+        for (int r = 0; r < SUB; ++r) acc += (double)x[r];
+        sd.sub[tid / HC][tid % HC] = acc;
     }
-    float dgv = 0.f, dfv = 0.f, al = 0.f, zv = 0.f;
+    __syncthreads();
+    const uint32_t tag = s_tag;
+    if (tid < HC && tid / NCOMP < hn) {   // chunk totals, in a fixed order, published
+        double t = 0.0;
+#pragma unroll
+        for (int j = 0; j < NSUB; ++j) t += sd.sub[j][tid];
+        xch_put(seqw + ((int64_t)c * HC + tid) * XW, tag, t);
+    }
+    float al = 0.f, zv = 0.f;   // alpha, z of (row tid>>2, head tid&3): contiguous in the row
     if (tid < CH * HG) {
-        const int hh = tid >> 6, r = tid & 63;   // dg, dF of (head hh, row r): coalesced along L
-        if (hh < hn && r < nrows) {
-            const int64_t o = (int64_t)(b * H + h0 + hh) * L + c * CH + r;
-            dgv = a.dg[o];
-            if (a.df) dfv = a.df[o];
-        }
-        const int row = tid >> 2, hl = tid & 3;   // alpha, z of (row, head hl): contiguous in the row
+        const int row = tid >> 2, hl = tid & 3;
         if (row < nrows && hl < hn) {
             al = (float)P[(int64_t)row * a.s_pl + off.A + h0 + hl];
             if (a.z) zv = a.z[(int64_t)b * a.s_zb + (int64_t)(c * CH + row) * a.s_zl + h0 + hl];
         }
     }
-    // fp64 totals of the following chunks (carries of the reverse scans)
-    const int c0 = c + 1;
-    double tv[TPT];
-    tot_load(tv, BT, b * H + h0, hn, NCH, c0, (NCH - c0 < TB) ? NCH : c0 + TB, tid);
-#pragma unroll
-    for (int i = 0; i < NU; ++i) {
-        const Unit u = cb_unit(tid + NT * i);
-#pragma unroll
-        for (int p = 0; p < 4; ++p) sm.x[u.hl * NCOMP + 2 + 4 * u.q + p][u.row] = dph[i][p];
-    }
-    if (tid < CH * HG) {
-        const int hh = tid >> 6, r = tid & 63;
-        sm.x[hh * NCOMP + 0][r] = dgv;
-        sm.x[hh * NCOMP + 1][r] = dfv;
-    }
-    tot_store(tl, tv, tid);
-    const bool lane = tid < HC && tid / NCOMP < hn;
+    // Reverse scans in two levels (fp64, fixed order): the carry of the following chunks, then each value = (carry +
+    // following sub-chunk totals) + its suffix within the sub-chunk.
+    const bool lane = li >= 0 && li < HC && li / NCOMP < hn;
+    const double sa = carry_xch(tu.d, seqw, hn, c + 1, NCH, tag, &xh->error, lane, li, tid);
+    if (li >= 0 && li < HC) sd.carry[li] = sa;
     __syncthreads();
-    const double sa = carry_of(tl, tv, BT, b * H + h0, hn, NCH, c0, NCH, lane, tid);
-    if (lane) {
-        float* x = sm.x[tid];
-        float v[CH];
+    if (tid < NTASK) {
+        const int col = tid % HC, s0 = tid / HC;
+        double p = sd.carry[col];
 #pragma unroll
-        for (int r = 0; r < CH; ++r) v[r] = x[r];
-        double rev = 0.0;
+        for (int j = NSUB - 1; j > 0; --j)
+            if (j > s0) p += sd.sub[j][col];
+        float* x = sq.x[col] + SUB * s0;
+        double acc = 0.0;
 #pragma unroll
-        for (int r = CH - 1; r >= 0; --r) {
-            rev += (double)v[r];
-            x[r] = (float)(sa + rev);   // the suffix sum; d alpha and dz take their element derivative below
+        for (int r = SUB - 1; r >= 0; --r) {
+            acc += (double)x[r];
+            x[r] = (float)(p + acc);   // the suffix sum; d alpha and dz take their element derivative below
         }
     }
     __syncthreads();
-    T* DP = (T*)a.dproj + (int64_t)b * a.s_db + (int64_t)c * CH * a.s_dl;
     // d theta: 8 columns per vector
 #pragma unroll
     for (int i = 0; i < 512 / NT; ++i) {
@@ -509,8 +686,8 @@ __global__ __launch_bounds__(NT) void prep_bwd_kernel(sisa_prep_bwd_args a) {
         f32x4 lo, hi;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            lo[j] = sm.x[hl * NCOMP + 2 + 8 * half + j][row];
-            hi[j] = sm.x[hl * NCOMP + 6 + 8 * half + j][row];
+            lo[j] = sq.x[hl * NCOMP + 2 + 8 * half + j][row];
+            hi[j] = sq.x[hl * NCOMP + 6 + 8 * half + j][row];
         }
         *reinterpret_cast<frag8<T>*>(DP + (int64_t)row * a.s_dl + off.TH + (h0 + hl) * S2 + 8 * half) =
             pack8<T>(lo, hi);
@@ -518,20 +695,21 @@ __global__ __launch_bounds__(NT) void prep_bwd_kernel(sisa_prep_bwd_args a) {
     if (tid < CH * HG) {
         const int row = tid >> 2, hl = tid & 3;
         if (row < nrows && hl < hn) {
-            DP[(int64_t)row * a.s_dl + off.A + h0 + hl] = cvt<T>(-sm.x[hl * NCOMP + 0][row] * softplus_grad(al));
+            DP[(int64_t)row * a.s_dl + off.A + h0 + hl] = cvt<T>(-sq.x[hl * NCOMP + 0][row] * softplus_grad(al));
             if (a.dz)
                 a.dz[(int64_t)b * a.s_dzb + (int64_t)(c * CH + row) * a.s_dzl + h0 + hl] =
-                    sm.x[hl * NCOMP + 1][row] * logsigmoid_grad(zv);
+                    sq.x[hl * NCOMP + 1][row] * logsigmoid_grad(zv);
         }
     }
     // zero padding columns (they multiply the zero rows of W_cat; keeps NaN out of dX)
-    if (blockIdx.z == 0 && off.NPAD > off.NTOT) {
+    if (h0 == 0 && off.NPAD > off.NTOT) {
         const int npad = off.NPAD - off.NTOT;
         for (int idx = tid; idx < CH * npad; idx += NT) {
             const int r = idx / npad, j = idx % npad;
             if (r < nrows) DP[(int64_t)r * a.s_dl + off.NTOT + j] = cvt<T>(0.f);
         }
     }
+    if (tid == 0) xch_arrive(xh, epoch, gridDim.x);
 }
 
 // ------------------------------------------------------------------------------------------------ non-finite guard
@@ -576,6 +754,11 @@ __global__ __launch_bounds__(GT) void finite_sum_kernel(const float* a, int64_t 
     }
 }
 
+// One workgroup per (chunk, sequence), numbered chunk-major (geo_of).
+inline unsigned prep_grid(int B, int L, int H) {
+    return (unsigned)((int64_t)sisa::cdiv(L, CH) * B * sisa::cdiv(H, HG));
+}
+
 template <class T>
 int launch_prep_fwd(const sisa_prep_fwd_args* a, hipStream_t st) {
     dim3 grid((unsigned)sisa::cdiv(a->L, CH), (unsigned)a->B, (unsigned)sisa::cdiv(a->H, HG));
@@ -588,19 +771,22 @@ int launch_prep_fwd(const sisa_prep_fwd_args* a, hipStream_t st) {
 
 template <class T>
 int launch_prep_bwd(const sisa_prep_bwd_args* a, hipStream_t st) {
-    dim3 grid((unsigned)sisa::cdiv(a->L, CH), (unsigned)a->B, (unsigned)sisa::cdiv(a->H, HG));
-    prep_bsums_kernel<T><<<grid, NT, 0, st>>>(*a);
-    int rc = sisa::launch_status("sisa_prep_bwd (sums)");
-    if (rc) return rc;
-    prep_bwd_kernel<T><<<grid, NT, 0, st>>>(*a);
+    prep_bwd_kernel<T><<<prep_grid(a->B, a->L, a->H), NT, 0, st>>>(*a);
     return sisa::launch_status("sisa_prep_bwd");
+}
+
+// A launch's workspace: the exchange header and words of every (sequence, chunk, column), one word per fp32 total
+// (forward) or two per fp64 total (backward). Checked against the grid limit.
+inline bool prep_shape_ok(int B, int L, int H) {
+    return (int64_t)sisa::cdiv(L, CH) * B * sisa::cdiv(H, HG) < (int64_t)1 << 31;
 }
 
 }  // namespace
 
 extern "C" int sisa_prep_fwd(const sisa_prep_fwd_args* a, void* stream) {
     SISA_REQUIRE(a != nullptr, "sisa_prep_fwd: null args");
-    SISA_REQUIRE(a->B >= 1 && a->L >= 1 && a->H >= 1, "sisa_prep_fwd: bad shape B=%d L=%d H=%d", a->B, a->L, a->H);
+    SISA_REQUIRE(a->B >= 1 && a->L >= 1 && a->H >= 1 && prep_shape_ok(a->B, a->L, a->H),
+                 "sisa_prep_fwd: bad shape B=%d L=%d H=%d", a->B, a->L, a->H);
     SISA_REQUIRE(a->dtype == SISA_BF16 || a->dtype == SISA_F16, "sisa_prep_fwd: proj dtype must be bf16/fp16");
     SISA_REQUIRE(a->proj && a->cr && a->br && a->g && a->rowf && a->colf && a->tot, "sisa_prep_fwd: null pointer");
     SISA_REQUIRE(a->z == nullptr || a->f != nullptr, "sisa_prep_fwd: f is required with z");
@@ -622,12 +808,13 @@ extern "C" int sisa_finite_sum(const float* a, int64_t na, const float* b, int64
 }
 
 extern "C" int64_t sisa_prep_bwd_workspace_bytes(int32_t B, int32_t L, int32_t H) {
-    return bt_bytes(B, L, H) + (int64_t)B * L * H * S2 * (int64_t)sizeof(float);
+    return (B >= 1 && L >= 1 && H >= 1) ? xch_bytes(B, L, H) : 0;
 }
 
 extern "C" int sisa_prep_bwd(const sisa_prep_bwd_args* a, void* stream) {
     SISA_REQUIRE(a != nullptr, "sisa_prep_bwd: null args");
-    SISA_REQUIRE(a->B >= 1 && a->L >= 1 && a->H >= 1, "sisa_prep_bwd: bad shape B=%d L=%d H=%d", a->B, a->L, a->H);
+    SISA_REQUIRE(a->B >= 1 && a->L >= 1 && a->H >= 1 && prep_shape_ok(a->B, a->L, a->H),
+                 "sisa_prep_bwd: bad shape B=%d L=%d H=%d", a->B, a->L, a->H);
     SISA_REQUIRE(a->dtype == SISA_BF16 || a->dtype == SISA_F16, "sisa_prep_bwd: proj dtype must be bf16/fp16");
     SISA_REQUIRE(a->proj && a->tot && a->dg && a->dcr && a->dbr && a->dproj && a->workspace,
                  "sisa_prep_bwd: null pointer");

@@ -15,7 +15,7 @@ from ctypes import POINTER, Structure, c_char_p, c_float, c_int, c_int32, c_int6
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "libsisa_hip.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 F32, BF16, F16, F64 = 0, 1, 2, 3
 _DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.float64: F64}

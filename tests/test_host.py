@@ -127,7 +127,11 @@ def test_workspace_sizes(lib):
     B, H, L = 2, 3, 1000
     # five fp32 (B,H,L) row buffers and the fp64 dlambda sums of 16-row groups (B*H*L even: no alignment pad)
     assert lib.sisa_attn_bwd_workspace_bytes(B, H, L) == 5 * 4 * B * H * L + 8 * B * H * -(-L // 16)
-    assert lib.sisa_prep_bwd_workspace_bytes(B, L, H) > 0
+    # prep backward exchange: a 256-byte header, then per (batch row, group of 4 heads, 64-row chunk) 72 fp64 totals
+    # of two 8-byte words each
+    words = B * -(-H // 4) * -(-L // 64) * 72
+    assert lib.sisa_prep_bwd_workspace_bytes(B, L, H) == 256 + 16 * words
+    assert lib.sisa_prep_bwd_workspace_bytes(0, L, H) == 0
     assert lib.sisa_rmsnorm_bwd_workspace_bytes(16384, 768) >= (16384 // 8 + 64) * 768 * 4
     assert lib.sisa_norm_bwd_workspace_bytes(16384, 768, 12) >= (16384 // 8 + 64 + 64 * 16) * 768 * 4
 

@@ -59,6 +59,38 @@ def test_prep_accuracy(B, L, H, seed, hasf, kw):
     factors = A.compute_factors(P.g)[:2]
     assert torch.equal(factors[0], P.rowf) and torch.equal(factors[1], P.colf), \
         "rowf/colf of the fused prep differ from the factor kernel on the same g"
+    assert FP().exchange_errors() == 0, "a prep launch's wait for another workgroup's chunk totals ran out"
+
+
+def _prep_both(proj, z, H, seed):
+    """Forward and backward prep outputs of one call each (the backward on seeded upstream gradients)."""
+    B, L, _ = proj.shape
+    pf = FP().prep_forward(proj, z, H)
+    gen = torch.Generator().manual_seed(seed)
+    dg = torch.randn(B, H, L, generator=gen).to(DEV)
+    dF = torch.randn(B, H, L, generator=gen).to(DEV) if z is not None else None
+    dcr, dbr = (torch.randn(B, L, H, 32, generator=gen).to(DEV) for _ in range(2))
+    dproj = torch.zeros_like(proj)
+    dz = FP().prep_backward(proj, z, pf.totals, dg, dF, dcr, dbr, dproj, H)
+    outs = [pf.cr, pf.br, pf.g, pf.rowf, pf.colf, pf.totals, dproj] + ([pf.f, dz] if z is not None else [])
+    return [t.clone() for t in outs]
+
+
+def test_exchange_workspace_reuse():
+    """The prep backward hands chunk totals between the workgroups of its one launch through a kept workspace whose
+    launch counter advances every call. Calls of several shapes (up to 141 chunks per sequence, beyond one batch of
+    gathered totals) reusing one workspace give the same bits, forward and backward outputs alike, as the same calls
+    on a fresh zeroed workspace, and no bounded wait runs out."""
+    cases = [(1, 700, 8, True), (2, 4096, 8, True), (1, 64, 3, False), (1, 9000, 4, True), (1, 1, 8, True)]
+    for B, L, H, hasf in cases:
+        proj, z, _ = R.make_proj(B, L, H, 40 + L, device=DEV)
+        z = z if hasf else None
+        kept = [_prep_both(proj, z, H, 5) for _ in range(2)]
+        FP()._EXCHANGE.clear()
+        fresh = _prep_both(proj, z, H, 5)
+        for run in kept:
+            assert all(torch.equal(x, y) for x, y in zip(run, fresh)), f"prep outputs depend on the workspace {B, L, H}"
+    assert FP().exchange_errors() == 0
 
 
 # ------------------------------------------------------------------------------------------------ fused gradients
