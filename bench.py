@@ -95,16 +95,18 @@ def profiled_traffic(kernels, name: str = "hbm_traffic_ns_ce.txt") -> float | No
     return sum(found.values()) if len(found) == len(kernels) else None
 
 
-def profiled_mfma_busy(name: str = "counters_attention_ns.txt") -> dict | None:
+def profiled_mfma_busy(name: str = "counters_ns_ce.txt") -> dict | None:
     """Per-kernel and time-weighted MFMA busy percentages of the attention kernels from the committed counter profile
-    (rows: kernel  us  valu_busy_pct  mfma_busy_pct ...); None when absent."""
-    rows = {}
+    (a table whose header row starts with ``kernel`` and names ``us`` and ``mfma_busy_pct``); None when absent."""
+    rows, cols = {}, None
     try:
         with open(os.path.join(PROFILES, name)) as f:
             for line in f:
                 parts = line.split()
-                if len(parts) >= 4 and parts[0] in ("attn_fwd", "attn_bwd_dq", "attn_bwd_dkv"):
-                    rows[parts[0]] = (float(parts[1]), float(parts[3]))
+                if parts and parts[0] == "kernel" and "mfma_busy_pct" in parts:
+                    cols = (parts.index("us"), parts.index("mfma_busy_pct"))
+                elif cols and len(parts) > max(cols) and parts[0] in ("attn_fwd", "attn_bwd_dq", "attn_bwd_dkv"):
+                    rows[parts[0]] = (float(parts[cols[0]]), float(parts[cols[1]]))
     except (OSError, ValueError):
         return None
     if len(rows) != 3:
@@ -112,7 +114,7 @@ def profiled_mfma_busy(name: str = "counters_attention_ns.txt") -> dict | None:
     t = sum(us for us, _ in rows.values())
     out = {k: v[1] for k, v in rows.items()}
     out["time_weighted"] = round(sum(us * b for us, b in rows.values()) / t, 2)
-    out["source"] = f"profiles/{name}"
+    out["source"] = f"profiles/{name} (rocprofv3 counter passes of this build, not measured in this run)"
     return out
 
 
@@ -773,6 +775,8 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": profiled_traffic(ATTN_KERNELS) if cfg == "ns" else None,
+                     "traffic_source": "profiles/hbm_traffic_ns_ce.txt (rocprofv3 FETCH_SIZE / WRITE_SIZE passes of this "
+                                       "build, not measured in this run)" if cfg == "ns" else None,
                      "kernel": "attention fwd + bwd launches (attn_fwd, attn_bwd_dq, attn_bwd_dkv)",
                      "algorithmic": f"1152 flop per causal pair x {fl['pairs']:.4g} pairs per step"},
         "roofline_prep": {"bound": "hbm", "achieved": round(prep_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
