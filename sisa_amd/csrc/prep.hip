@@ -284,8 +284,13 @@ SISA_DEV void xch_put(uint64_t* w, uint32_t tag, double v) {
     __hip_atomic_store(w, tagged(tag, (uint32_t)u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(w + 1, tagged(tag, (uint32_t)(u >> 32)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-SISA_DEV uint64_t xch_load(const uint64_t* w) {
-    return __hip_atomic_load(const_cast<uint64_t*>(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// A poll of a word: the first of a gather at workgroup scope (a plain load, which the caches may serve and which may
+// return an older copy of the line), every later one at device scope (coherent across the XCDs' L2s). Either way a
+// word carrying this launch's tag holds its final value (each word is written once per launch), so a cached copy is
+// used when it is current and polled again coherently when it is not.
+SISA_DEV uint64_t xch_load(const uint64_t* w, bool coherent) {
+    return coherent ? __hip_atomic_load(const_cast<uint64_t*>(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                    : __hip_atomic_load(const_cast<uint64_t*>(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // Exchanged totals of up to TB chunks, [chunk - first][column].
@@ -298,7 +303,8 @@ static_assert(GPT * NT == TB * HC && GPT <= 32 && (TB & (TB - 1)) == 0, "gathere
 // The totals of chunks [c0, c1) (at most TB) of one sequence's words (laid out [chunk][column][2]) into xl (zero for
 // columns of absent heads), each polled until both its words carry `tag`; thread t takes the totals t, t + NT, ... of
 // the range. All loads of a poll are issued before the first is examined; a total goes to LDS as soon as it has
-// arrived.
+// arrived. The first poll may be served by the caches (the totals of chunks whose workgroups finished before this
+// one started are then read from L2 rather than from memory, once per XCD).
 SISA_DEV void xch_gather(XLds& xl, const uint64_t* seqw, int hn, int c0, int c1, uint32_t tag, uint32_t* err, int t) {
     const int n = (c1 - c0) * HC;
     double* dst = &xl.t[0][0];
@@ -317,8 +323,8 @@ SISA_DEV void xch_gather(XLds& xl, const uint64_t* seqw, int hn, int c0, int c1,
 #pragma unroll
         for (int q = 0; q < GPT; ++q)
             if (pending & (1u << q)) {
-                lo[q] = xch_load(src + NT * XW * q);
-                hi[q] = xch_load(src + NT * XW * q + 1);
+                lo[q] = xch_load(src + NT * XW * q, it > 0);
+                hi[q] = xch_load(src + NT * XW * q + 1, it > 0);
             }
 #pragma unroll
         for (int q = 0; q < GPT; ++q)
