@@ -527,8 +527,10 @@ def make_attention_inputs(spec: dict, device="cpu") -> dict:
     return {n: (t.to(device) if t is not None else None) for n, t in out.items()}
 
 
-def make_proj(B, L, H, seed=0, dt=torch.bfloat16, alpha_mu=-3.0, alpha_sd=2.0, th_mu=0.02, th_sd=0.2, device="cpu"):
-    """Seeded fused projection + forget logits (tests/test_fused_prep.py:79-88)."""
+def make_proj(B, L, H, seed=0, dt=torch.bfloat16, alpha_mu=-3.0, alpha_sd=2.0, th_mu=0.02, th_sd=0.2, device="cpu",
+              z_mu=4.0, z_sd=1.5):
+    """Seeded fused projection + forget logits (tests/test_fused_prep.py:79-88; the defaults are that test's draws,
+    the keyword arguments give BASELINE.json's: alpha ~ N(-5, 0.5^2), theta ~ N(0, 0.01^2), z ~ N(4, 0.5^2))."""
     gen = torch.Generator().manual_seed(seed)
     off = layout(H)
     P = torch.zeros(B, L, off["NPAD"])
@@ -536,7 +538,7 @@ def make_proj(B, L, H, seed=0, dt=torch.bfloat16, alpha_mu=-3.0, alpha_sd=2.0, t
     P[..., off["B"]:off["TH"]] *= 0.6
     P[..., off["TH"]:off["A"]] = th_mu + th_sd * torch.randn(B, L, H * 16, generator=gen)
     P[..., off["A"]:off["NTOT"]] = alpha_mu + alpha_sd * torch.randn(B, L, H, generator=gen)
-    z = (4.0 + 1.5 * torch.randn(B, L, H, generator=gen)).contiguous()
+    z = (z_mu + z_sd * torch.randn(B, L, H, generator=gen)).contiguous()
     return P.to(dt).contiguous().to(device), z.to(device), off
 
 

@@ -36,7 +36,10 @@ def torch_glue(proj, z, H):
     (2, 2048, 8, 1, True, {}), (1, 300, 12, 2, True, {}), (1, 1, 8, 3, True, {}), (1, 129, 8, 4, False, {}),
     (1, 2048, 8, 6, True, dict(alpha_mu=-8.0, alpha_sd=0.5)), (1, 1000, 16, 7, True, {}), (1, 65, 5, 8, True, {}),
     (1, 8300, 6, 9, True, {}), (1, 16384, 16, 10, True, dict(alpha_mu=-7.0, alpha_sd=1.0)),
-    (4, 4096, 8, 11, True, dict(alpha_mu=-5.0, alpha_sd=0.5, th_mu=0.0, th_sd=0.01))])
+    (4, 4096, 8, 11, True, dict(alpha_mu=-5.0, alpha_sd=0.5, th_mu=0.0, th_sd=0.01, z_mu=4.0, z_sd=0.5)),
+    (2, 2048, 8, 12, True, dict(alpha_mu=-5.0, alpha_sd=0.5, th_mu=0.0, th_sd=0.01, z_mu=4.0, z_sd=0.5)),
+    (1, 300, 12, 13, True, dict(alpha_mu=-5.0, alpha_sd=0.5, th_mu=0.0, th_sd=0.01, z_mu=4.0, z_sd=0.5)),
+    (1, 8300, 6, 14, False, dict(alpha_mu=-5.0, alpha_sd=0.5, th_mu=0.0, th_sd=0.01))])
 def test_prep_accuracy(B, L, H, seed, hasf, kw):
     from sisa_amd.kernels import attention as A
     proj, z, off = R.make_proj(B, L, H, seed, device=DEV, **kw)
@@ -160,15 +163,18 @@ def judge(candidate, proj, z, lam, H, dy) -> tuple[dict, torch.Tensor, torch.Ten
     return errs, dP, dz
 
 
-# the last two cases draw alpha and theta as BASELINE.json's configs do (a ~ N(-5, 0.5^2), theta ~ N(0, 0.01^2))
-BASELINE_DRAW = dict(alpha_mu=-5.0, alpha_sd=0.5, th_mu=0.0, th_sd=0.01)
+# cases drawing alpha, theta and z as BASELINE.json's configs do (a ~ N(-5, 0.5^2), theta ~ N(0, 0.01^2),
+# z ~ N(4, 0.5^2))
+BASELINE_DRAW = dict(alpha_mu=-5.0, alpha_sd=0.5, th_mu=0.0, th_sd=0.01, z_mu=4.0, z_sd=0.5)
 
 
 @pytest.mark.parametrize("B,L,H,seed,hasf,kw", [(1, 1, 4, 31, True, {}), (1, 190, 4, 32, True, {}),
                                                  (1, 257, 4, 33, False, {}), (2, 640, 4, 34, True, {}),
                                                  (1, 1500, 8, 35, True, {}), (1, 4200, 4, 36, True, {}),
                                                  (1, 2048, 8, 37, True, BASELINE_DRAW),
-                                                 (1, 4096, 4, 38, True, BASELINE_DRAW)])
+                                                 (1, 4096, 4, 38, True, BASELINE_DRAW),
+                                                 (2, 640, 4, 39, True, BASELINE_DRAW),
+                                                 (1, 190, 8, 40, False, BASELINE_DRAW)])
 def test_fused_gradients_against_fp64_and_glue(B, L, H, seed, hasf, kw):
     print(f"[fused grads] B={B} L={L} H={H} seed={seed} forget={hasf} {kw}", flush=True)
     proj, z, off = R.make_proj(B, L, H, seed, device=DEV, **kw)
