@@ -23,11 +23,11 @@
 // G and the logits are never written to memory; the only large buffer is the chunk's exponentials (read once per
 // output column tile). Deterministic: no atomics.
 //
-// Tile arithmetic: a workgroup of 2 x 2 waves, one wave per SIMD; a wave owns 128 hidden x 128 rows (dx) or 128
-// hidden x 128 vocabulary (dW) as 8 x 8 blocks of v_mfma_f32_16x16x32 (256 accumulators: half the LDS fragment
-// bytes per MAC of a 128 x 64 wave tile, which is what the LDS bandwidth needs at this MFMA rate; the wave's own VALU
-// work of forming G issues between its MFMAs), hidden on the A side so that a lane's 4 results are 4 consecutive
-// hidden values (16-byte stores). dx reads W_pad as A with the feature-map transpose read (K = vocabulary, W_pad
+// Tile arithmetic: a workgroup of 2 x 4 waves, two waves per SIMD (247 VGPRs); a wave owns 128 hidden x 64 rows
+// (dx) or 128 hidden x 64 vocabulary (dW) as 8 x 4 blocks of v_mfma_f32_16x16x32 (128 accumulators; all 12 operand
+// fragments of a 32-deep step are read before its 32 MFMAs), hidden on the A side so that a lane's 4 results are 4
+// consecutive hidden values (16-byte stores). The next stage's exponentials are loaded into registers before a
+// stage's MFMAs and formed into G in LDS after them. dx reads W_pad as A with the feature-map transpose read (K = vocabulary, W_pad
 // rows) and G as B with direct 16-byte fragment reads (K = vocabulary along G rows); dW reads x and G both with the
 // sequence-map transpose read (K = rows). Workgroup i runs on XCD i % 8; each XCD takes consecutive work items, so
 // the three hidden tiles that share a G tile run on one L2.
