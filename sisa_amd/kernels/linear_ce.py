@@ -20,8 +20,9 @@ How the work is arranged here (every kernel is HIP, ``libsisa_hip.so``; no libra
   GEMMs) has the same contract; its chunk budget is 1 GiB of logits, this one 2 GiB of exponentials (one chunk at
   N = 16,384, V = 50,277), because every chunk after the first re-reads and adds the fp32 dW.
 
-Both paths take the loss from the fp32 MFMA accumulations of the logits (the reference rounds the logits to the
-compute dtype first; its loss is within that rounding of this one), and the two paths give bitwise the same loss.
+Both paths round each logit, accumulated in fp32 by the MFMAs, once to the compute dtype before the log-sum-exp, as
+the reference's row kernel reads bf16/fp16 logits (linear_ce.py:166-170), so the loss has the reference's rounding
+point, and the two paths give bitwise the same loss.
 
 The vocabulary is padded with zero rows to a multiple of 128 (50,277 -> 50,304) and the hidden size with zero columns
 to a multiple of 64, so that every GEMM runs on aligned shapes; the padding never enters a sum. ``grad_scale`` is the
