@@ -378,18 +378,17 @@ SISA_DEV void xch_arrive(XchHeader* xh, uint32_t epoch, unsigned nwg) {
     }
 }
 
-// Workgroup w of a launch: sequence seq = w % NSEQ (batch row seq / NHG, heads of group seq % NHG), chunk index
-// w / NSEQ counted from the first chunk (forward) or from the last (backward).
+// Workgroup w of the backward's launch: sequence seq = w % NSEQ (batch row seq / NHG, heads of group seq % NHG),
+// chunk NCH - 1 - w / NSEQ (chunk-major from the last chunk down, the order the total exchange waits in).
 struct Geo {
     int c, b, h0, hn, nrows, NCH, seq;
 };
-SISA_DEV Geo geo_of(int B, int L, int H, bool reverse) {
+SISA_DEV Geo bwd_geo(int B, int L, int H) {
     Geo g;
     const int NHG = (H + HG - 1) / HG, NSEQ = B * NHG;
     g.NCH = (L + CH - 1) / CH;
     g.seq = (int)blockIdx.x % NSEQ;
-    const int k = (int)blockIdx.x / NSEQ;
-    g.c = reverse ? g.NCH - 1 - k : k;
+    g.c = g.NCH - 1 - (int)blockIdx.x / NSEQ;
     g.b = g.seq / NHG;
     g.h0 = (g.seq % NHG) * HG;
     g.hn = (H - g.h0 < HG) ? H - g.h0 : HG;
@@ -543,7 +542,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     __shared__ SubLds<double> sd;
     __shared__ uint32_t s_tag;
     const int H = a.H, L = a.L;
-    const Geo G = geo_of(a.B, L, H, true);
+    const Geo G = bwd_geo(a.B, L, H);
     const int c = G.c, b = G.b, h0 = G.h0, hn = G.hn, nrows = G.nrows, NCH = G.NCH;
     const Layout off = layout_of(H);
     const int tid = threadIdx.x;
@@ -760,7 +759,7 @@ __global__ __launch_bounds__(GT) void finite_sum_kernel(const float* a, int64_t 
     }
 }
 
-// One workgroup per (chunk, sequence), numbered chunk-major (geo_of).
+// The backward's grid: one workgroup per (chunk, sequence), numbered as bwd_geo reads them.
 inline unsigned prep_grid(int B, int L, int H) {
     return (unsigned)((int64_t)sisa::cdiv(L, CH) * B * sisa::cdiv(H, HG));
 }
@@ -781,8 +780,7 @@ int launch_prep_bwd(const sisa_prep_bwd_args* a, hipStream_t st) {
     return sisa::launch_status("sisa_prep_bwd");
 }
 
-// A launch's workspace: the exchange header and words of every (sequence, chunk, column), one word per fp32 total
-// (forward) or two per fp64 total (backward). Checked against the grid limit.
+// Shapes whose backward grid stays below 2^31 workgroups.
 inline bool prep_shape_ok(int B, int L, int H) {
     return (int64_t)sisa::cdiv(L, CH) * B * sisa::cdiv(H, HG) < (int64_t)1 << 31;
 }
