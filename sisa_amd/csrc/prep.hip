@@ -23,6 +23,8 @@
 //   backward  one launch, prep_bwd: Phi recomputed from theta and TOT, dPhi and the inverse rotation, the fp64 chunk
 //             totals of (dg, dF, dPhi) handed to the other workgroups of the launch through the workspace (the total
 //             exchange below), the reverse scans. No dPhi rows leave the chip.
+#include <stdlib.h>
+
 #include "common.h"
 #include "host.h"
 
@@ -265,7 +267,8 @@ SISA_DEV Acc carry_of(TotLds<Acc>& tl, Acc (&v)[TPT], const Acc* tot, int bh0, i
 // Progress: the workgroups are numbered chunk-major from the last chunk down (the last chunk of every sequence before
 // the one below it), each publishes its totals before it waits, and it waits only for workgroups of lower number,
 // which the hardware dispatches first, so the lowest unfinished workgroup never waits. The wait is bounded all the
-// same: after SPIN_LIMIT polls the `error` word is set, the missing totals count as zero and the launch ends.
+// same: after SPIN_LIMIT polls the `error` word is set, the missing totals count as zero and the launch ends (the
+// environment variable SISA_PREP_SPIN_LIMIT lowers the bound, so that a test can take that path on purpose).
 struct XchHeader {
     uint32_t epoch, arrivals, error;
 };
@@ -305,7 +308,8 @@ static_assert(GPT * NT == TB * HC && GPT <= 32 && (TB & (TB - 1)) == 0, "gathere
 // the range. All loads of a poll are issued before the first is examined; a total goes to LDS as soon as it has
 // arrived. The first poll may be served by the caches (the totals of chunks whose workgroups finished before this
 // one started are then read from L2 rather than from memory, once per XCD).
-SISA_DEV void xch_gather(XLds& xl, const uint64_t* seqw, int hn, int c0, int c1, uint32_t tag, uint32_t* err, int t) {
+SISA_DEV void xch_gather(XLds& xl, const uint64_t* seqw, int hn, int c0, int c1, uint32_t tag, uint32_t* err, int t,
+                         int spin_limit) {
     const int n = (c1 - c0) * HC;
     double* dst = &xl.t[0][0];
     const uint64_t* src = seqw + ((int64_t)c0 * HC + t) * XW;
@@ -333,7 +337,7 @@ SISA_DEV void xch_gather(XLds& xl, const uint64_t* seqw, int hn, int c0, int c1,
                 pending &= ~(1u << q);
             }
         if (pending == 0) break;
-        if (it == SPIN_LIMIT) {
+        if (it >= spin_limit) {
             __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
             for (int q = 0; q < GPT; ++q)
@@ -348,13 +352,13 @@ SISA_DEV void xch_gather(XLds& xl, const uint64_t* seqw, int hn, int c0, int c1,
 // of the workgroup calls this: it gathers through LDS, TB chunks per batch; the reads of FB chunks are issued before
 // their adds.
 SISA_DEV double carry_xch(XLds& xl, const uint64_t* seqw, int hn, int c0, int c1, uint32_t tag, uint32_t* err,
-                          bool lane, int li, int tid) {
+                          int spin_limit, bool lane, int li, int tid) {
     constexpr int FB = 16;
     double acc = 0.0;
     for (int cb = c0; cb < c1; cb += TB) {
         const int ce = (c1 - cb < TB) ? c1 : cb + TB;
         if (cb > c0) __syncthreads();   // every lane is done with the previous batch
-        xch_gather(xl, seqw, hn, cb, ce, tag, err, tid);
+        xch_gather(xl, seqw, hn, cb, ce, tag, err, tid, spin_limit);
         __syncthreads();
         if (lane) {
             for (int k0 = 0; k0 < ce - cb; k0 += FB) {
@@ -531,7 +535,8 @@ __global__ __launch_bounds__(NT) void prep_fwd_kernel(sisa_prep_fwd_args a) {
 // set to zero. d alpha = -suffix * softplus'(alpha) and dz = suffix * logsigmoid'(z) are formed by the threads that
 // loaded alpha and z.
 template <class T>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 8))) void prep_bwd_kernel(sisa_prep_bwd_args a) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 8))) void prep_bwd_kernel(sisa_prep_bwd_args a,
+                                                                                               int spin_limit) {
     __shared__ ScanLds sm;   // theta, then Phi
     __shared__ ScanLds sq;   // dg, dF and dPhi, then their reverse scans
     __shared__ union {
@@ -664,7 +669,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     // Reverse scans in two levels (fp64, fixed order): the carry of the following chunks, then each value = (carry +
     // following sub-chunk totals) + its suffix within the sub-chunk.
     const bool lane = li >= 0 && li < HC && li / NCOMP < hn;
-    const double sa = carry_xch(tu.d, seqw, hn, c + 1, NCH, tag, &xh->error, lane, li, tid);
+    const double sa = carry_xch(tu.d, seqw, hn, c + 1, NCH, tag, &xh->error, spin_limit, lane, li, tid);
     if (li >= 0 && li < HC) sd.carry[li] = sa;
     __syncthreads();
     if (tid < NTASK) {
@@ -776,7 +781,9 @@ int launch_prep_fwd(const sisa_prep_fwd_args* a, hipStream_t st) {
 
 template <class T>
 int launch_prep_bwd(const sisa_prep_bwd_args* a, hipStream_t st) {
-    prep_bwd_kernel<T><<<prep_grid(a->B, a->L, a->H), NT, 0, st>>>(*a);
+    const char* env = getenv("SISA_PREP_SPIN_LIMIT");
+    const int spin_limit = env ? atoi(env) : SPIN_LIMIT;
+    prep_bwd_kernel<T><<<prep_grid(a->B, a->L, a->H), NT, 0, st>>>(*a, spin_limit < 0 ? 0 : spin_limit);
     return sisa::launch_status("sisa_prep_bwd");
 }
 

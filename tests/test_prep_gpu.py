@@ -295,3 +295,27 @@ def test_finite_sum_flag():
                 t[i] = bad
                 assert not bool(fp.finite_sum_flag(a, b).item()), (na, nb, bad)
                 t[i] = keep
+
+
+def test_exchange_wait_is_bounded(monkeypatch):
+    """The prep backward's wait for other workgroups' chunk totals is bounded. With the bound lowered to one poll
+    (SISA_PREP_SPIN_LIMIT=0, read by the library at each launch) a workgroup whose first poll misses gives up: the
+    launch still ends, and either the error word reports it or every output is exact (no wait ran out). The next
+    launch, on a fresh workspace with the normal bound, is exact and clean."""
+    B, L, H = 4, 4096, 8
+    proj, z, _ = R.make_proj(B, L, H, 55, device=DEV)
+    FP()._EXCHANGE.clear()
+    good = _prep_both(proj, z, H, 5)
+    assert FP().exchange_errors() == 0
+    FP()._EXCHANGE.clear()
+    monkeypatch.setenv("SISA_PREP_SPIN_LIMIT", "0")
+    rushed = _prep_both(proj, z, H, 5)
+    ran_out = FP().exchange_errors() != 0
+    print(f"single-poll bound ran out: {ran_out}", flush=True)
+    assert ran_out or all(torch.equal(x, y) for x, y in zip(good, rushed))
+    monkeypatch.delenv("SISA_PREP_SPIN_LIMIT")
+    FP()._EXCHANGE.clear()
+    again = _prep_both(proj, z, H, 5)
+    assert FP().exchange_errors() == 0
+    assert all(torch.equal(x, y) for x, y in zip(good, again))
+    FP()._EXCHANGE.clear()
