@@ -309,8 +309,10 @@ def test_fused_and_gradient_paths_agree():
 
 
 # ------------------------------------------------------------------------------------------------ gradient path
+# the last case: a ragged row count, a hidden size that is not a multiple of 64 (zero columns added) and a vocabulary
+# that is not a multiple of 128 (zero rows added)
 @pytest.mark.parametrize("N,D,V,seed", [(2048, 512, 50277, 1 / 16), (1024, 768, 1003, 1 / 32),
-                                        (4096, 1024, 50277, 1 / 64)])
+                                        (4096, 1024, 50277, 1 / 64), (74, 200, 1000, 1 / 8)])
 def test_gradients_vs_fp64(N, D, V, seed):
     print(f"[train] N={N} D={D} V={V}", flush=True)
     lce = lce_fn()
