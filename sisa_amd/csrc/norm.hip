@@ -14,9 +14,13 @@
 //
 // Work decomposition: a wave holds RB = 64 / HP rows (HP = the projection width padded to 16, 32 or 64) with NVL =
 // HP / 8 eight-element vectors per lane (lane l holds elements 8 c .. 8 c + 7, c = l + 64 i), so RB * NVL = 8 and
-// the row length is at most 512 NVL. The RB * HP projection partial sums of a lane are reduced over the 64 lanes
-// with a halving exchange (63 shuffles): lane l ends with the total of row l / HP, output l % HP. Weight gradients
-// are reduced in fixed order through caller-provided partials: bitwise reproducible, no atomics.
+// the row length is at most 512 NVL. For up to 16 outputs and rows of at most 768 (a multiple of 64) the projection
+// and its adjoint run on the matrix cores: the workgroup's sixteen rows of n (of dz W_f) pass through LDS and each
+// wave forms a quarter of the columns with v_mfma_f32_16x16x4_f32 (norm_fwd_mfma_kernel, norm_bwd_mfma_kernel).
+// Otherwise a lane's RB * HP projection partial sums are reduced over the 64 lanes with a halving exchange (63
+// shuffles): lane l ends with the total of row l / HP, output l % HP. Weight gradients are reduced in fixed order
+// through caller-provided partials, the independent reductions of the backward sharing launches: bitwise
+// reproducible, no atomics.
 #include "common.h"
 #include "host.h"
 
@@ -181,6 +185,127 @@ __global__ __launch_bounds__(64 * NORM_WAVES) void norm_fwd_kernel(sisa_norm_arg
     if (row < a.N && h < a.H) a.z[row * a.H + h] = t + a.bf[h];
 }
 
+// Forward with the projection on the matrix cores, for 0 < H <= 16 and D a multiple of 64 up to MFMA_DMAX: the
+// normalisation as above (four rows per wave, sixteen per workgroup), then the workgroup's sixteen rows of n go to LDS
+// and wave w forms the 16 x 16 partial z tile of columns [w D/4, (w+1) D/4) with v_mfma_f32_16x16x4_f32 (A = n: lane l
+// holds row l % 16 and reads four consecutive columns with one 16-byte LDS read, one per MFMA of the step; B = W_f:
+// the same four columns of row l % 16 of W_f), and the four partial tiles are summed in wave order (in the LDS
+// space of n once every wave is done with it).
+constexpr int MFMA_DMAX = 768;                  // W_f operand of at most 12 steps in registers
+constexpr int NL_PAD = 4;                       // row padding of the staged n: conflict-free 16-byte reads
+inline int64_t norm_mfma_lds_bytes(int D) { return (int64_t)16 * (D + NL_PAD) * (int64_t)sizeof(float); }
+template <class TX, class TY>
+__global__ __launch_bounds__(64 * NORM_WAVES) void norm_fwd_mfma_kernel(sisa_norm_args a) {
+    constexpr int RB = 4, NVL = 2;
+    extern __shared__ __attribute__((aligned(16))) float dyn_lds[];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int D = a.D, ld = D + NL_PAD, nv = D / 8;
+    float* nl = dyn_lds;                                   // [16][ld]: n of the workgroup's rows
+    f32x4* red = reinterpret_cast<f32x4*>(dyn_lds);        // then [NORM_WAVES][64]: the partial tiles
+    const int64_t g0 = (int64_t)blockIdx.x * 16;
+    const int64_t r0 = g0 + w * RB;
+    f32x8 n[RB][NVL];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        const int64_t row = r0 + r;
+#pragma unroll
+        for (int i = 0; i < NVL; ++i) {
+            const int c = lane + 64 * i;
+            if (row < a.N && c < nv) {
+                n[r][i] = load_f32x8<TX>((const TX*)a.x + row * a.sx + 8 * c);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) n[r][i][e] = 0.f;
+            }
+        }
+    }
+    // W_f operand of the wave's columns: step q, lane l -> W_f[l % 16][w D/4 + 16 q + 4 (l / 16) .. + 3]
+    const int hq = lane & 15, kg = lane >> 4;
+    const int nq = D / 64;                                 // 16-column steps per wave
+    const int cw = w * (D / 4) + 4 * kg;
+    f32x4 wb[MFMA_DMAX / 64];
+#pragma unroll
+    for (int q = 0; q < MFMA_DMAX / 64; ++q)
+        wb[q] = (q < nq && hq < a.H) ? *reinterpret_cast<const f32x4*>(a.wf + (int64_t)hq * D + cw + 16 * q)
+                                     : f32x4{0.f, 0.f, 0.f, 0.f};
+    if (a.res) {   // h = x + res, rounded to x's dtype as the residual add, normalised in place of x
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int64_t row = r0 + r;
+#pragma unroll
+            for (int i = 0; i < NVL; ++i) {
+                const int c = lane + 64 * i;
+                if (row < a.N && c < nv) {
+                    const f32x8 rv = load_f32x8<TY>((const TY*)a.res + row * a.sres + 8 * c);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) n[r][i][e] = rnd<TX>(n[r][i][e] + rv[e]);
+                    store_f32x8<TX>((TX*)a.h + row * a.sh + 8 * c, n[r][i]);
+                }
+            }
+        }
+    }
+    float rstd[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < NVL; ++i)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = fmaf(n[r][i][e], n[r][i][e], ss);
+        rstd[r] = 1.f / sqrtf(wave_sum(ss) / (float)D + a.eps);
+    }
+#pragma unroll
+    for (int i = 0; i < NVL; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nv) {
+            const f32x8 wv = load_f32x8<float>(a.w + 8 * c);
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) n[r][i][e] = rnd<TX>((n[r][i][e] * rstd[r]) * wv[e]);
+                if (r0 + r < a.N) store_f32x8<TY>((TY*)a.y + (r0 + r) * a.sy + 8 * c, n[r][i]);
+                float* dst = nl + (w * RB + r) * ld + 8 * c;
+                *reinterpret_cast<f32x4*>(dst) = f32x4{n[r][i][0], n[r][i][1], n[r][i][2], n[r][i][3]};
+                *reinterpret_cast<f32x4*>(dst + 4) = f32x4{n[r][i][4], n[r][i][5], n[r][i][6], n[r][i][7]};
+            }
+        }
+    }
+    if (a.rstd && lane < RB && r0 + lane < a.N) {
+        float rs = rstd[0];
+#pragma unroll
+        for (int r = 1; r < RB; ++r)
+            if (lane == r) rs = rstd[r];
+        a.rstd[r0 + lane] = rs;
+    }
+    __syncthreads();
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    const float* arow = nl + hq * ld + cw;
+#pragma unroll
+    for (int q = 0; q < MFMA_DMAX / 64; ++q) {
+        if (q < nq) {
+            const f32x4 av = *reinterpret_cast<const f32x4*>(arow + 16 * q);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[t], wb[q][t], acc, 0, 0, 0);
+        }
+    }
+    __syncthreads();   // every wave is done reading n
+    red[w * 64 + lane] = acc;
+    __syncthreads();
+    if (w != 0) return;
+    // lane l holds rows 4 (l / 16) + v of the tile for output h = l % 16
+    f32x4 z = red[lane];
+#pragma unroll
+    for (int k = 1; k < NORM_WAVES; ++k) z += red[k * 64 + lane];
+    if (hq < a.H) {
+        const float bh = a.bf[hq];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int64_t row = g0 + 4 * kg + v;
+            if (row < a.N) a.z[row * a.H + hq] = z[v] + bh;
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ RMSNorm backward
 // dn = dy + dz W_f (the projection term summed first, then added to dy, as autograd sums the two adjoints; for a
 // 16-bit x both roundings to x's dtype are kept: dn = round_x(dy + round_x(dz W_f))), du = dn * w, u = x * rstd,
@@ -310,19 +435,151 @@ __global__ __launch_bounds__(64 * NORM_WAVES) void norm_bwd_kernel(sisa_norm_arg
     }
 }
 
-// dW_f partials: workgroup (column block blockIdx.x, row block blockIdx.y, output block blockIdx.z of 16) computes
+// Backward with the projection's adjoint on the matrix cores (the shapes of norm_fwd_mfma_kernel): per step of four
+// rows per wave the workgroup's sixteen rows of dz W_f are formed as (W_f^T dz^T) tiles, wave w the columns [w D/4,
+// (w+1) D/4), with v_mfma_f32_16x16x4_f32 (A = W_f^T: lane l holds column l % 16 of the tile for the four outputs
+// 4 s + l / 16 of K-step s; B = dz^T of tile row l % 16), so that a lane ends with four consecutive columns of one row,
+// stored to LDS as one 16-byte write; the row pass then reads its rows' products from there. Every wave takes part
+// in both steps (its rows past the end contribute zeros), so the barriers see the whole workgroup.
+template <class TX, class TY>
+__global__ __launch_bounds__(64 * NORM_WAVES) void norm_bwd_mfma_kernel(sisa_norm_args a, float* __restrict__ dw_part) {
+    constexpr int RB = 4, NVL = 2;
+    extern __shared__ __attribute__((aligned(16))) float dyn_lds[];   // [16][D + NL_PAD]: dz W_f of the step's rows
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int D = a.D, ld = D + NL_PAD, nv = D / 8;
+    const int64_t pw0 = (int64_t)blockIdx.x * NORM_WAVES;
+    const int64_t p = pw0 + w;                         // partial row = wave
+    f32x8 u[RB][NVL];
+    auto load_rows = [&](int64_t r0) {
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int64_t row = r0 + r;
+#pragma unroll
+            for (int i = 0; i < NVL; ++i) {
+                const int c = lane + 64 * i;
+                if (row < a.N && c < nv) {
+                    u[r][i] = load_f32x8<TX>((const TX*)a.x + row * a.sx + 8 * c);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) u[r][i][e] = 0.f;
+                }
+            }
+        }
+    };
+    load_rows(p * NORM_RPW);
+    // W_f^T operand: step q, K-step s, lane l -> W_f[4 s + l / 16][w D/4 + 16 q + l % 16]
+    const int jq = lane & 15, kg = lane >> 4;
+    const int nq = D / 64;
+    const int cw = w * (D / 4) + jq;
+    f32x4 wa[MFMA_DMAX / 64];
+#pragma unroll
+    for (int q = 0; q < MFMA_DMAX / 64; ++q)
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+            const int h = 4 * s2 + kg;
+            wa[q][s2] = (q < nq && h < a.H) ? a.wf[(int64_t)h * D + cw + 16 * q] : 0.f;
+        }
+    f32x8 wreg[NVL], dwacc[NVL];
+#pragma unroll
+    for (int i = 0; i < NVL; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nv) wreg[i] = load_f32x8<float>(a.w + 8 * c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dwacc[i][e] = 0.f;
+    }
+#pragma unroll 1
+    for (int it = 0; it < NORM_RPW / RB; ++it) {
+        const int64_t r0 = p * NORM_RPW + it * RB;
+        if (it > 0) load_rows(r0);
+        float rstd[RB];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) rstd[r] = r0 + r < a.N ? a.rstd[r0 + r] : 0.f;
+        // dz^T operand of tile row jq: row (pw0 + jq / 4) * NORM_RPW + it * RB + jq % 4, outputs 4 s + kg
+        const int64_t zrow = (pw0 + (jq >> 2)) * NORM_RPW + it * RB + (jq & 3);
+        float dzb[4];
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) {
+            const int h = 4 * s2 + kg;
+            dzb[s2] = (zrow < a.N && h < a.H) ? a.dz[zrow * a.H + h] : 0.f;
+        }
+        if (it > 0) __syncthreads();                   // every wave is done reading the previous products
+#pragma unroll
+        for (int q = 0; q < MFMA_DMAX / 64; ++q) {
+            if (q < nq) {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[q][s2], dzb[s2], acc, 0, 0, 0);
+                // lane l: columns w D/4 + 16 q + 4 (l / 16) .. + 3 of tile row l % 16
+                *reinterpret_cast<f32x4*>(dyn_lds + jq * ld + w * (D / 4) + 16 * q + 4 * kg) = acc;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int64_t row = r0 + r;
+            const float* pr = dyn_lds + (w * RB + r) * ld;
+            float dot = 0.f;
+            f32x8 dn[NVL];
+#pragma unroll
+            for (int i = 0; i < NVL; ++i) {
+                const int c = lane + 64 * i;
+                if (row < a.N && c < nv) {
+                    const f32x8 g = load_f32x8<TY>((const TY*)a.dy + row * a.sdy + 8 * c);
+                    const f32x4 plo = *reinterpret_cast<const f32x4*>(pr + 8 * c);
+                    const f32x4 phi = *reinterpret_cast<const f32x4*>(pr + 8 * c + 4);
+                    const f32x8 pj = {plo[0], plo[1], plo[2], plo[3], phi[0], phi[1], phi[2], phi[3]};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float d = sizeof(TX) == 4 ? g[e] + pj[e] : rnd<TX>(g[e] + rnd<TX>(pj[e]));
+                        u[r][i][e] *= rstd[r];
+                        dwacc[i][e] = fmaf(d, u[r][i][e], dwacc[i][e]);
+                        dn[i][e] = d * wreg[i][e];                     // du
+                        dot = fmaf(dn[i][e], u[r][i][e], dot);
+                    }
+                }
+            }
+            const float mdot = wave_sum(dot) / (float)D;
+            if (row < a.N) {
+#pragma unroll
+                for (int i = 0; i < NVL; ++i) {
+                    const int c = lane + 64 * i;
+                    if (c < nv) {
+                        f32x8 o;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) o[e] = rstd[r] * (dn[i][e] - u[r][i][e] * mdot);
+                        if (a.dh) {   // plus the residual stream's gradient of h, summed in x's dtype
+                            const f32x8 hv = load_f32x8<TX>((const TX*)a.dh + row * a.sdh + 8 * c);
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) o[e] = rnd<TX>(o[e]) + hv[e];
+                        }
+                        store_f32x8<TX>((TX*)a.dx + row * a.sdx + 8 * c, o);
+                    }
+                }
+            }
+        }
+    }
+    if (p * NORM_RPW >= a.N) return;
+    float* dwp = dw_part + p * D;
+#pragma unroll
+    for (int i = 0; i < NVL; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nv) store_f32x8<float>(dwp + 8 * c, dwacc[i]);
+    }
+}
+
+// dW_f partials: workgroup (column block bx, row block by, output block bz of 16) computes
 // P[h][f] = sum over its WF_ROWS rows of dz[row][h] * n[row][f] with v_mfma_f32_16x16x4_f32 (A = dz^T, 16 outputs x
 // 4 rows; B = n, 4 rows x 16 columns; n recomputed as round_x((x * rstd) * w)); wave w owns WF_TPW column tiles.
 // The workgroup of column block 0 also writes the row block's sum of dz.
 template <class TX>
-__global__ __launch_bounds__(64 * NORM_WAVES) void forget_dw_kernel(sisa_norm_args a, float* __restrict__ part,
-                                                                     float* __restrict__ dbpart) {
+SISA_DEV void forget_dw_block(const sisa_norm_args& a, float* __restrict__ part, float* __restrict__ dbpart, int bx,
+                              int by, int bz) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int kr = lane >> 4, col = lane & 15;
     const int hp = 16 * ((a.H + 15) / 16);
-    const int h = 16 * blockIdx.z + col;               // A operand: output index of this lane
-    const int64_t rb0 = (int64_t)blockIdx.y * WF_ROWS;
-    const int f0 = (blockIdx.x * NORM_WAVES + w) * 16 * WF_TPW;
+    const int h = 16 * bz + col;                       // A operand: output index of this lane
+    const int64_t rb0 = (int64_t)by * WF_ROWS;
+    const int f0 = (bx * NORM_WAVES + w) * 16 * WF_TPW;
     float wv[WF_TPW];
 #pragma unroll
     for (int t = 0; t < WF_TPW; ++t) {
@@ -359,18 +616,18 @@ __global__ __launch_bounds__(64 * NORM_WAVES) void forget_dw_kernel(sisa_norm_ar
         }
     }
     // D layout: lane l, register i -> output 4 (l / 16) + i of this block, column f0 + 16 t + l % 16
-    float* P = part + (int64_t)blockIdx.y * hp * a.D;
+    float* P = part + (int64_t)by * hp * a.D;
 #pragma unroll
     for (int t = 0; t < WF_TPW; ++t) {
         const int f = f0 + 16 * t + col;
         if (f < a.D)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) P[(int64_t)(16 * blockIdx.z + 4 * kr + i) * a.D + f] = acc[t][i];
+            for (int i = 0; i < 4; ++i) P[(int64_t)(16 * bz + 4 * kr + i) * a.D + f] = acc[t][i];
     }
-    if (blockIdx.x == 0 && w == 0) {
+    if (bx == 0 && w == 0) {
         dbs += __shfl_xor(dbs, 16);
         dbs += __shfl_xor(dbs, 32);
-        if (kr == 0) dbpart[(int64_t)blockIdx.y * hp + h] = dbs;
+        if (kr == 0) dbpart[(int64_t)by * hp + h] = dbs;
     }
 }
 
@@ -392,32 +649,63 @@ SISA_DEV float ordered_sum(const float* __restrict__ p, int64_t stride, int64_t 
 
 // Column sums of a (rows, cols) fp32 matrix in row order, split over DW_SPLIT row ranges: level 2 writes
 // part2[split][col], level 3 sums the splits.
-__global__ __launch_bounds__(256) void colsum2_kernel(const float* __restrict__ part, float* __restrict__ part2,
-                                                      int64_t rows, int cols) {
-    const int c = blockIdx.x * 256 + threadIdx.x;
+SISA_DEV void colsum2_block(const float* __restrict__ part, float* __restrict__ part2, int64_t rows, int cols, int bx,
+                            int by) {
+    const int c = bx * 256 + threadIdx.x;
     if (c >= cols) return;
     const int64_t per = (rows + DW_SPLIT - 1) / DW_SPLIT;
-    const int64_t k0 = blockIdx.y * per, k1 = k0 + per < rows ? k0 + per : rows;
-    part2[(int64_t)blockIdx.y * cols + c] = k1 > k0 ? ordered_sum(part + k0 * cols + c, cols, k1 - k0, 0.f) : 0.f;
+    const int64_t k0 = by * per, k1 = k0 + per < rows ? k0 + per : rows;
+    part2[(int64_t)by * cols + c] = k1 > k0 ? ordered_sum<32>(part + k0 * cols + c, cols, k1 - k0, 0.f) : 0.f;
 }
 
-__global__ __launch_bounds__(256) void colsum3_kernel(const float* __restrict__ part2, float* __restrict__ out,
-                                                      int cols) {
-    const int c = blockIdx.x * 256 + threadIdx.x;
+SISA_DEV void colsum3_block(const float* __restrict__ part2, float* __restrict__ out, int cols, int bx) {
+    const int c = bx * 256 + threadIdx.x;
     if (c >= cols) return;
-    out[c] = ordered_sum<32>(part2 + c, cols, DW_SPLIT, 0.f);
+    out[c] = ordered_sum<64>(part2 + c, cols, DW_SPLIT, 0.f);
 }
 
 // dW_f[h][f] (and db_f[h]) = sum over the row-block partials in order.
-__global__ __launch_bounds__(256) void forget_dw_final_kernel(sisa_norm_args a, const float* __restrict__ part,
-                                                              const float* __restrict__ dbpart, int nrb) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+SISA_DEV void forget_dw_final_block(const sisa_norm_args& a, const float* __restrict__ part,
+                                    const float* __restrict__ dbpart, int nrb, int bx) {
+    const int64_t idx = (int64_t)bx * 256 + threadIdx.x;
     const int hp = 16 * ((a.H + 15) / 16);
     if (idx < (int64_t)a.H * a.D) {
         const int h = (int)(idx / a.D), f = (int)(idx % a.D);
-        a.dwf[idx] = ordered_sum<32>(part + (int64_t)h * a.D + f, (int64_t)hp * a.D, nrb, 0.f);
+        a.dwf[idx] = ordered_sum<64>(part + (int64_t)h * a.D + f, (int64_t)hp * a.D, nrb, 0.f);
     }
-    if (blockIdx.x == 0 && threadIdx.x < a.H) a.dbf[threadIdx.x] = ordered_sum<32>(dbpart + threadIdx.x, hp, nrb, 0.f);
+    if (bx == 0 && threadIdx.x < a.H) a.dbf[threadIdx.x] = ordered_sum<64>(dbpart + threadIdx.x, hp, nrb, 0.f);
+}
+
+// Workspace of the backward: per-wave dw partial rows, their DW_SPLIT second-level sums, the dW_f and db_f partials
+// of the row blocks.
+struct NormWs {
+    float *dw_part, *dw_part2, *wf_part, *db_part;
+};
+
+// The reductions after the row pass run as two launches whose workgroups take different jobs (all are independent
+// within a launch): the second has the dW_f partial workgroups (nf of them; grid nfx x nfy x nfz, numbered x
+// fastest) and the level-2 dw column sums (DW_SPLIT x ceil(D / 256) workgroups); the third the level-3 dw sums and
+// the dW_f / db_f totals.
+template <class TX>
+__global__ __launch_bounds__(256) void norm_dw_stage2_kernel(sisa_norm_args a, NormWs ws, int64_t np, int nfx, int nfy,
+                                                            int nfz) {
+    const int64_t nf = (int64_t)nfx * nfy * nfz;
+    const int64_t b = blockIdx.x;
+    if (b < nf) {
+        forget_dw_block<TX>(a, ws.wf_part, ws.db_part, (int)(b % nfx), (int)((b / nfx) % nfy), (int)(b / ((int64_t)nfx * nfy)));
+        return;
+    }
+    const int cb = (int)(b - nf), nc = (a.D + 255) / 256;
+    colsum2_block(ws.dw_part, ws.dw_part2, np, a.D, cb % nc, cb / nc);
+}
+
+__global__ __launch_bounds__(256) void norm_dw_final_kernel(sisa_norm_args a, NormWs ws, int nrb) {
+    const int nc = (a.D + 255) / 256;
+    if ((int)blockIdx.x < nc) {
+        colsum3_block(ws.dw_part2, a.dw, a.D, blockIdx.x);
+        return;
+    }
+    forget_dw_final_block(a, ws.wf_part, ws.db_part, nrb, (int)blockIdx.x - nc);
 }
 
 // ------------------------------------------------------------------------------------------------ host side
@@ -429,10 +717,6 @@ int norm_hp(const sisa_norm_args* a) {
 }
 
 int64_t norm_nrb(int64_t N) { return sisa::cdiv(N, WF_ROWS); }
-
-struct NormWs {
-    float *dw_part, *dw_part2, *wf_part, *db_part;
-};
 
 NormWs norm_ws(const sisa_norm_args* a) {
     NormWs w;
@@ -455,28 +739,33 @@ template <class TX, class TY, int HP>
 int launch_norm_hp(const sisa_norm_args* a, int bwd, hipStream_t st) {
     constexpr int RB = 64 / HP;
     if (!bwd) {
+        if (HP == 16 && a->H > 0 && a->D % 64 == 0 && a->D <= MFMA_DMAX) {
+            norm_fwd_mfma_kernel<TX, TY><<<(unsigned)sisa::cdiv(a->N, 16), 64 * NORM_WAVES,
+                                           (size_t)norm_mfma_lds_bytes(a->D), st>>>(*a);
+            return sisa::launch_status("sisa_norm_fwd");
+        }
         const int64_t waves = sisa::cdiv(a->N, RB);
         norm_fwd_kernel<TX, TY, HP><<<(unsigned)sisa::cdiv(waves, NORM_WAVES), 64 * NORM_WAVES, 0, st>>>(*a);
         return sisa::launch_status("sisa_norm_fwd");
     }
     const NormWs ws = norm_ws(a);
     const int64_t np = sisa::cdiv(a->N, NORM_RPW);
-    norm_bwd_kernel<TX, TY, HP><<<(unsigned)sisa::cdiv(np, NORM_WAVES), 64 * NORM_WAVES, 0, st>>>(*a, ws.dw_part);
+    if (HP == 16 && a->H > 0 && a->D % 64 == 0 && a->D <= MFMA_DMAX)
+        norm_bwd_mfma_kernel<TX, TY><<<(unsigned)sisa::cdiv(np, NORM_WAVES), 64 * NORM_WAVES,
+                                       (size_t)norm_mfma_lds_bytes(a->D), st>>>(*a, ws.dw_part);
+    else
+        norm_bwd_kernel<TX, TY, HP><<<(unsigned)sisa::cdiv(np, NORM_WAVES), 64 * NORM_WAVES, 0, st>>>(*a, ws.dw_part);
     int rc = sisa::launch_status("sisa_norm_bwd");
     if (rc) return rc;
-    colsum2_kernel<<<dim3((unsigned)sisa::cdiv(a->D, 256), DW_SPLIT), 256, 0, st>>>(ws.dw_part, ws.dw_part2, np,
-                                                                                     a->D);
-    colsum3_kernel<<<(unsigned)sisa::cdiv(a->D, 256), 256, 0, st>>>(ws.dw_part2, a->dw, a->D);
-    rc = sisa::launch_status("sisa_norm_bwd (dw)");
-    if (rc || a->H == 0) return rc;
     const int nrb = (int)norm_nrb(a->N);
-    const dim3 grid((unsigned)sisa::cdiv(a->D, 16 * WF_TPW * NORM_WAVES), (unsigned)nrb, (unsigned)sisa::cdiv(a->H, 16));
-    forget_dw_kernel<TX><<<grid, 64 * NORM_WAVES, 0, st>>>(*a, ws.wf_part, ws.db_part);
-    rc = sisa::launch_status("sisa_norm_bwd (dW_f)");
+    const int nfx = a->H > 0 ? (int)sisa::cdiv(a->D, 16 * WF_TPW * NORM_WAVES) : 0, nfz = (int)sisa::cdiv(a->H, 16);
+    const int64_t nf = (int64_t)nfx * nrb * nfz, nc = sisa::cdiv(a->D, 256);
+    norm_dw_stage2_kernel<TX><<<(unsigned)(nf + nc * DW_SPLIT), 256, 0, st>>>(*a, ws, np, nfx, nrb, nfz);
+    rc = sisa::launch_status("sisa_norm_bwd (dw, dW_f partials)");
     if (rc) return rc;
-    forget_dw_final_kernel<<<(unsigned)sisa::cdiv((int64_t)a->H * a->D, 256), 256, 0, st>>>(*a, ws.wf_part,
-                                                                                             ws.db_part, nrb);
-    return sisa::launch_status("sisa_norm_bwd (dW_f final)");
+    const int64_t nfin = a->H > 0 ? sisa::cdiv((int64_t)a->H * a->D, 256) : 0;
+    norm_dw_final_kernel<<<(unsigned)(nc + nfin), 256, 0, st>>>(*a, ws, nrb);
+    return sisa::launch_status("sisa_norm_bwd (dw, dW_f totals)");
 }
 
 template <class TX, class TY>
