@@ -22,13 +22,16 @@ ARCH = "gfx950"
 # -packed-fp32-ops: hipcc never emits v_pk_{add,mul,fma}_f32 for this library.
 HIPFLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", f"-I{os.path.join(ROOT, 'include')}",
             f"-I{CSRC}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
-# Per-source additions: the backward attention kernels (dependency chains of MFMA, exponentials and fp32 row sums),
-# the fused CE forward, the weight-gradient GEMM (all operand fragments of a step read ahead of its MFMAs) and the
-# decoder-block kernels (the forward norms 2-5 % faster) run faster under LLVM's max-ILP machine scheduler; the
-# forward attention kernel, the CE training kernels and the prep kernels are fastest under the default one (measured
-# on MI355X against max-ILP, max-memory-clause, iterative-ILP and iterative-minreg).
+# Per-source additions, each the fastest of the default, max-ILP, max-memory-clause, iterative-ILP and
+# iterative-minreg machine schedulers measured on MI355X: max-ILP for the dkv attention kernel (dependency chains of
+# MFMA, exponentials and fp32 row sums), the fused CE forward, the weight-gradient GEMM (all operand fragments of a
+# step read ahead of its MFMAs) and the decoder-block kernels (the forward norms 2-5 % faster); iterative-ILP for the
+# dq attention kernel (4-6 % faster than under max-ILP, which makes the dkv kernel 1-4 % slower); the default one
+# for the forward attention kernel, the CE training kernels and the prep kernels.
 _MAX_ILP = ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
-EXTRA_FLAGS = {"attention_bwd.hip": _MAX_ILP, "lmce_fwd.hip": _MAX_ILP, "wgrad.hip": _MAX_ILP, "norm.hip": _MAX_ILP}
+_ITER_ILP = ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]
+EXTRA_FLAGS = {"attention_bwd.hip": _MAX_ILP, "attention_dq.hip": _ITER_ILP, "lmce_fwd.hip": _MAX_ILP,
+               "wgrad.hip": _MAX_ILP, "norm.hip": _MAX_ILP}
 
 
 def _hipcc() -> str:

@@ -1,5 +1,6 @@
-// SISA attention for gfx950: decay factors, forward and exact-delta backward (query-owned and key-owned kernels, in
-// attention_bwd.hip, which also hold the deterministic fp64 dlambda reduction), with the C entry points.
+// SISA attention for gfx950: decay factors, forward and exact-delta backward (the query-owned kernel in
+// attention_dq.hip, the key-owned one in attention_bwd.hip; they also hold the deterministic fp64 dlambda reduction),
+// with the C entry points.
 //
 //   s_ij = q_i.k_j / 8 + lam * exp(g_i - g_j) * (c_i.b_j) + (F_i - F_j)        (j <= i)
 //   o_i  = sum_j softmax_j(s_ij) v_j
@@ -519,7 +520,7 @@ static int check_bwd(const sisa_attn_bwd_args* a) {
     return SISA_OK;
 }
 
-// the dq and dkv kernels (attention_bwd.hip); dlambda is summed inside them
+// the dq and dkv kernels (attention_dq.hip, attention_bwd.hip); dlambda is summed inside them
 static int launch_bwd_any(const sisa_attn_bwd_args* a, hipStream_t st) { return sisa::detail::attn_bwd_dq_dkv(a, st); }
 
 extern "C" int sisa_attn_bwd(const sisa_attn_bwd_args* a, void* stream) {

@@ -1,6 +1,6 @@
-// Definitions shared by the two SISA attention translation units: attention.hip (decay factors, forward,
-// dlambda and the C entry points) and attention_bwd.hip (the dq and dkv kernels of the exact-delta backward,
-// compiled with a scheduler of their own). Reference: src/sisa/kernels/attention.py.
+// Definitions shared by the SISA attention translation units: attention.hip (decay factors, forward, dlambda and the
+// C entry points), attention_dq.hip and attention_bwd.hip (the dq and the dkv kernel of the exact-delta backward,
+// each compiled with a scheduler of its own). Reference: src/sisa/kernels/attention.py.
 #pragma once
 #include "common.h"
 #include "host.h"
@@ -81,5 +81,7 @@ namespace sisa {
 namespace detail {
 // The dq and dkv launches of sisa_attn_bwd (attention_bwd.hip), after the entry point's checks; 0 or an error code.
 __attribute__((visibility("hidden"))) int attn_bwd_dq_dkv(const sisa_attn_bwd_args* a, hipStream_t st);
+// The dq launch alone (attention_dq.hip).
+__attribute__((visibility("hidden"))) int attn_bwd_dq(const sisa_attn_bwd_args* a, hipStream_t st);
 }  // namespace detail
 }  // namespace sisa

@@ -12,7 +12,7 @@ largest rise of ``g`` in each block) unless the caller brings factors, then ``si
 (B, L, H, D) memory order, the row log-sum-exp (log2 units) and, for the exact backward, the self-normalised fp32
 output o''. Backward: ``sisa_attn_bwd`` (two launches: dq with the fp64 dlambda sums of 16-row groups, then
 dk/dv/db, in which one workgroup adds each head's group sums in a fixed order; deterministic). All numerics live in
-csrc/attention.hip and csrc/attention_bwd.hip.
+csrc/attention.hip, csrc/attention_dq.hip and csrc/attention_bwd.hip.
 """
 from __future__ import annotations
 
