@@ -79,7 +79,11 @@ def test_add_norm_kernel(xd, yd, N, D):
                                          (torch.float32, torch.bfloat16, 100, 1536, 24),
                                          (torch.float32, torch.float32, 9, 4096, 64),
                                          (torch.float16, torch.float16, 5, 200, 5),
-                                         (torch.float32, torch.bfloat16, 300, 768, 0)])
+                                         (torch.float32, torch.bfloat16, 300, 768, 0),
+                                         # the matrix-core projection at its edges: one 16-column step per wave with
+                                         # all 16 outputs, and a single output with 16-bit rows
+                                         (torch.float32, torch.bfloat16, 17, 64, 16),
+                                         (torch.bfloat16, torch.bfloat16, 49, 768, 1)])
 def test_norm_forget_kernel(xd, yd, N, D, H):
     """Fused RMSNorm + fp32 forget projection (forward y, z; backward dx, dw, dW_f, db_f) against float64 autograd
     of the same formula: n = (x * rstd) * w, z = round_x(n) W_f^T + b_f, y = round_y(round_x(n))."""
