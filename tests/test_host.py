@@ -308,6 +308,15 @@ def test_bench_refuses_more_than_one_gpu():
     assert pr.returncode == 2 and "one GPU" in pr.stderr
 
 
+def test_build_flags_name_existing_sources():
+    """Every per-source compiler addition of the build names a HIP source that exists (a renamed or split source would
+    otherwise silently lose its scheduler choice), and the HIP sources all carry the packed-fp32 exclusion."""
+    from sisa_amd import build
+    sources = {os.path.basename(p) for p in build.glob.glob(os.path.join(build.CSRC, "*.hip"))}
+    assert set(build.EXTRA_FLAGS) <= sources, set(build.EXTRA_FLAGS) - sources
+    assert "-packed-fp32-ops" in build.HIPFLAGS
+
+
 def test_graft_entry_points_exist():
     sys.path.insert(0, ROOT)
     import __graft_entry__ as ge
