@@ -1,5 +1,7 @@
-"""Library GEMM selection for the projection GEMMs around the hot path (the W_cat, W_O, gate/up and down projections
-and the LM-head GEMMs of the chunked cross-entropy).
+"""Library GEMM selection for the projection GEMMs around the hot path: the forward and input-gradient products of
+the W_cat, W_O, gate/up and down projections, the gate/up weight gradient and the LM head's logits GEMM of the
+library arrangement the cross-entropy benchmark times beside its own kernels (the other weight gradients and the
+cross-entropy itself run on this library's HIP kernels).
 
 These GEMMs stay on hipBLASLt / rocBLAS through ``torch.mm``/``F.linear``. PyTorch-ROCm's TunableOp can pick, per
 GEMM shape and layout, the fastest solution among the libraries' kernels instead of the default heuristic; at the
